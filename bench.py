@@ -1,0 +1,340 @@
+"""Benchmark of the GGUF quantized-linear hot path on one MI355X.
+
+Headline ("C2"): Q4_K decode GEMV at Qwen3-8B MLP
+shapes, M = 1.  One *step* is one decode MLP's three linears, each its own
+launch through the C ABI: gate [12288 x 4096], up [12288 x 4096] and down
+[4096 x 12288].  ``value`` is the algorithmic bytes of all K steps (packed
+weights + fp16 x + fp16 out) divided by the timed region.
+
+Protocol (after benchmarks/kernels/showcase/benchmark.py:66-94): every launch
+is bound once (allocation-free BoundCall), the K steps are captured into one
+HIP graph, and the graph replay is timed with HIP events recorded on the
+launch stream.  Weights rotate through distinct copies (>= 3 x 256 MiB per
+rotation) so no launch finds its weights in the 256 MiB MALL.
+
+Also reported: ``roofline`` for the dominant kernel (Q4_K GEMV 12288 x 4096),
+``cpu_baseline`` (the C restatement in oracle/, invoked through its
+TensorKernelV1 entry exactly as the reference CPU provider invokes images), and
+``details`` for the other BASELINE configurations (C2 M = 4/8, C3 LM head, C4
+prefill GEMM, C5 decoder-layer chain).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+FP16_PEAK_TFLOPS = 2516.6   # MI355X dense fp16 MFMA
+MALL_BYTES = 256 << 20
+ROTATION_BYTES = 3 * MALL_BYTES
+METRIC = "Q4_K/Q6_K decode GEMV GB/s (% HBM peak); prefill dequant-GEMM TFLOP/s"
+GEOMETRY = {"q4_0": (32, 18), "q8_0": (32, 34), "q4_k": (256, 144), "q6_k": (256, 210)}
+
+
+def log(*parts):
+    print("[bench]", *parts, file=sys.stderr, flush=True)
+
+
+def weight_bytes(encoding, n, k):
+    qk, block = GEOMETRY[encoding]
+    return n * (k // qk) * block
+
+
+def gemv_bytes(encoding, m, n, k, out_itemsize):
+    return weight_bytes(encoding, n, k) + 2 * m * k + out_itemsize * m * n
+
+
+class Linear:
+    """One linear layer: R rotated weight copies, its input and output, bound calls."""
+
+    def __init__(self, device, kernel, encoding, m, n, k, out_dtype, copies, seed, x=None):
+        from tests import gguf_cases as cases
+
+        self.device, self.encoding, self.m, self.n, self.k = device, encoding, m, n, k
+        self.out_dtype = out_dtype
+        raw = cases.weight(n, k, encoding, seed)
+        first = device.from_numpy(raw)
+        self.weights = [first] + [device.empty(raw.shape, "uint8").copy_from(first) for _ in range(copies - 1)]
+        self.x = x if x is not None else device.from_numpy(cases.activation(m, k, seed + 1))
+        self.out = device.empty((m, n), out_dtype)
+        self.exe = device.load(kernel, encoding=encoding, out_dtype=out_dtype)
+        self.calls = [self.exe.bind(self.x, w, self.out) for w in self.weights]
+        self.bytes = gemv_bytes(encoding, m, n, k, np.dtype(out_dtype).itemsize)
+        self.flops = 2 * m * n * k
+
+    def release(self):
+        for b in self.weights + [self.out]:
+            b.release()
+
+
+def copies_for(bytes_per_rotation_unit):
+    return max(2, math.ceil(ROTATION_BYTES / bytes_per_rotation_unit))
+
+
+def time_graph(device, launches, replays=3):
+    """Capture ``launches`` (callables) into one graph; return the median seconds of one replay."""
+    graph = device.graph(lambda: [launch() for launch in launches])
+    try:
+        graph.replay()
+        device.synchronize()
+        samples = []
+        for _ in range(replays):
+            start = device.record_event(timing=True)
+            graph.replay()
+            stop = device.record_event(timing=True)
+            stop.synchronize()
+            samples.append(device.elapsed_ms(start, stop) * 1e-3)
+            start.release()
+            stop.release()
+        return statistics.median(samples)
+    finally:
+        graph.close()
+
+
+def rotated_launches(linears, steps):
+    """``steps`` passes over the linears, each pass using the next weight copy."""
+    out = []
+    for step in range(steps):
+        for layer in linears:
+            out.append(layer.calls[step % len(layer.calls)].launch)
+    return out
+
+
+# ------------------------------------------------------------ CPU baseline --
+
+def cpu_baseline(budget_s=10.0):
+    """Time the oracle's TensorKernelV1 CPU entry on the headline step."""
+    import ctypes as c
+
+    from oracle import gguf_ref
+    from tensor_amd.runtime import abi
+    from tests import gguf_cases as cases
+
+    if not gguf_ref.LIBRARY.exists():
+        gguf_ref.build()
+    oracle = gguf_ref.c_oracle()
+    cores = min(16, len(os.sched_getaffinity(0)))
+    layers = [("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
+    copies = 4  # 340 MB of distinct weights per rotation (beyond the host LLC)
+    data = []
+    for i, (_, n, k) in enumerate(layers):
+        first = cases.weight(n, k, "q4_k", 1000 + i)
+        raws = [first] + [first.copy() for _ in range(copies - 1)]
+        x = cases.activation(1, k, 2000 + i)
+        out = np.empty((1, n), np.float16)
+        data.append((raws, x, out, n, k))
+
+    def call_for(x, raw, out):
+        keep = []
+        args = (abi.Argument * 4)()
+        for j, (arr, dtype) in enumerate(((x, 10), (raw, 3), (out, 10))):
+            shape = (c.c_int64 * 2)(*arr.shape)
+            strides = (c.c_int64 * 2)(arr.strides[0], arr.strides[1])
+            keep += [shape, strides]
+            args[j].kind, args[j].dtype = 1, dtype
+            args[j].buffer = abi.BufferDescriptor(arr.ctypes.data, arr.nbytes, shape, strides, 2, dtype, 1, 0)
+        args[3].kind, args[3].dtype, args[3].scalar = 2, 7, 12
+        call = abi.CallDescriptor(1, 72, args, 4, 0, (c.c_uint32 * 3)(1, 1, 1), (c.c_uint32 * 3)(1, 1, 1), 0,
+                                  abi.StreamDescriptor(1, 0, 0))
+        return call, keep, args
+
+    calls = [[call_for(x, raw, out) for raw in raws] for raws, x, out, _, _ in data]
+    entry = oracle.entry
+    entry.argtypes = [c.POINTER(abi.CallDescriptor), c.POINTER(abi.ErrorDescriptor)]
+    entry.restype = c.c_int32
+    step_bytes = sum(gemv_bytes("q4_k", 1, n, k, 2) for _, _, _, n, k in data)
+
+    def measure(threads, seconds):
+        oracle.set_threads(threads)
+        error = abi.ErrorDescriptor()
+        samples, step, begin = [], 0, time.perf_counter()
+        while time.perf_counter() - begin < seconds or len(samples) < 3:
+            t0 = time.perf_counter()
+            for layer in calls:
+                status = entry(c.byref(layer[step % copies][0]), c.byref(error))
+                if status:
+                    raise RuntimeError(error.message.decode())
+            samples.append(time.perf_counter() - t0)
+            step += 1
+        return statistics.median(samples), len(samples)
+
+    multi, n_multi = measure(cores, budget_s * 0.75)
+    single, n_single = measure(1, budget_s * 0.25)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((line.split(":", 1)[1].strip() for line in f if line.startswith("model name")), "")
+    except OSError:
+        pass
+    return {
+        "value": round(step_bytes / multi / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{n_multi} steps of the headline step (Q4_K GEMV M=1 gate+up+down, {step_bytes} B/step), "
+                  f"median {multi * 1e3:.2f} ms/step on {cores} threads; weights rotated over {copies} copies",
+        "single_thread_gbs": round(step_bytes / single / 1e9, 3),
+        "single_thread_ms_per_step": round(single * 1e3, 3),
+        "cpu_model": model,
+    }
+
+
+# ------------------------------------------------------------------- main --
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=300)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--no-details", action="store_true", help="headline only")
+    parser.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        parser.error("steps must be >= 1 and warmup >= 0")
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import tensor_amd as tx
+
+    device = tx.Device(0, provider="hip")
+    with device:
+        log("device", device.info["name"], device.info["arch_features"], "CUs", device.info["compute_units"])
+        # ---- headline: C2 Q4_K GEMV M=1, gate + up + down per step
+        per_step_weights = 2 * weight_bytes("q4_k", 12288, 4096) + weight_bytes("q4_k", 4096, 12288)
+        copies = copies_for(per_step_weights)
+        log("headline weights", per_step_weights, "B per step,", copies, "rotated copies")
+        gate = Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 1)
+        up = Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 3, x=gate.x)
+        down = Linear(device, "gguf_gemv", "q4_k", 1, 4096, 12288, "float16", copies, 5)
+        mlp = [gate, up, down]
+        step_bytes = sum(layer.bytes for layer in mlp)
+        for launch in rotated_launches(mlp, args.warmup):
+            launch()
+        device.synchronize()
+        log("warmup done", args.warmup, "steps")
+        seconds = time_graph(device, rotated_launches(mlp, args.steps), replays=3)
+        value = step_bytes * args.steps / seconds / 1e9
+        log(f"headline {value:.1f} GB/s, {seconds / args.steps * 1e6:.2f} us/step")
+
+        # ---- roofline of the dominant kernel: Q4_K GEMV 12288 x 4096, M=1
+        launches = 200
+        kernel_s = time_graph(device, [gate.calls[i % copies].launch for i in range(launches)]) / launches
+        achieved = gate.bytes / kernel_s / 1e9
+        roofline = {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "gemv_q4k<M=1> 12288x4096 fp16 out",
+            "avg_us": round(kernel_s * 1e6, 3),
+            "algorithmic_bytes": gate.bytes,
+        }
+        log(f"roofline kernel {kernel_s * 1e6:.2f} us -> {achieved:.1f} GB/s")
+
+        details = {}
+        if not args.no_details:
+            details = run_details(device, gate.x, log)
+        for layer in mlp:
+            layer.release()
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(seconds / args.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 x q4_k -> fp32 accumulate",
+        "data": "synthetic: seeded N(0,0.02) weights quantized to Q4_K, N(0,1) fp16 activations",
+        "config": {
+            "workload": "C2 Q4_K decode GEMV, M=1, Qwen3-8B MLP step = gate 12288x4096 + up 12288x4096 "
+                        "+ down 4096x12288, fp16 out, weights rotated through "
+                        f"{copies} copies ({copies * per_step_weights >> 20} MiB)",
+            "M": 1,
+            "hidden": 4096,
+            "intermediate": 12288,
+            "bytes_per_step": step_bytes,
+            "timing": "HIP graph of all K steps, HIP events on the launch stream",
+        },
+        "roofline": roofline,
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(args.cpu_seconds),
+        "details": details,
+    }
+    print(json.dumps(result))
+    return 0
+
+
+def run_details(device, x4096, log):
+    """Per-config figures for the other BASELINE configurations."""
+    details = {}
+
+    def gemv_case(name, encoding, m, n, k, out_dtype, launches=60):
+        copies = copies_for(weight_bytes(encoding, n, k))
+        layer = Linear(device, "gguf_gemv", encoding, m, n, k, out_dtype, copies, 7 + m)
+        seconds = time_graph(device, [layer.calls[i % copies].launch for i in range(launches)]) / launches
+        gbs = layer.bytes / seconds / 1e9
+        details[name] = {"us": round(seconds * 1e6, 3), "GB/s": round(gbs, 1),
+                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
+        log(name, details[name])
+        layer.release()
+
+    for m in (1, 4, 8):
+        gemv_case(f"C2_q4k_gemv_m{m}_12288x4096", "q4_k", m, 12288, 4096, "float16")
+        gemv_case(f"C2_q4k_gemv_m{m}_4096x12288", "q4_k", m, 4096, 12288, "float16")
+    gemv_case("C3_q6k_lm_head_m1_151936x4096_fp32", "q6_k", 1, 151936, 4096, "float32", launches=20)
+
+    def gemm_case(name, encoding, m, n, k, launches=10):
+        layer = Linear(device, "gguf_gemm", encoding, m, n, k, "float16", 2, 9)
+        seconds = time_graph(device, [layer.calls[i % 2].launch for i in range(launches)]) / launches
+        tflops = layer.flops / seconds / 1e12
+        details[name] = {"us": round(seconds * 1e6, 2), "TFLOP/s": round(tflops, 2),
+                         "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
+        log(name, details[name])
+        layer.release()
+
+    gemm_case("C4_q4k_gemm_m512_12288x4096", "q4_k", 512, 12288, 4096)
+    gemm_case("C4_q4k_gemm_m2048_12288x4096", "q4_k", 2048, 12288, 4096, launches=4)
+
+    # C5: q, k, v, o, gate, up (Q4_K) and down (Q6_K) chained on one stream
+    shapes = [("q", "q4_k", 4096, 4096), ("k", "q4_k", 1024, 4096), ("v", "q4_k", 1024, 4096),
+              ("o", "q4_k", 4096, 4096), ("gate", "q4_k", 12288, 4096), ("up", "q4_k", 12288, 4096),
+              ("down", "q6_k", 4096, 12288)]
+    layer_weights = sum(weight_bytes(e, n, k) for _, e, n, k in shapes)
+    for m, kernel in ((1, "gguf_gemv"), (256, "gguf_gemm")):
+        copies = copies_for(layer_weights) if m == 1 else 2
+        layers = [Linear(device, kernel, e, m, n, k, "float16", copies, 20 + i) for i, (_, e, n, k) in enumerate(shapes)]
+        steps = 20 if m == 1 else 4
+        seconds = time_graph(device, rotated_launches(layers, steps)) / steps
+        total_bytes = sum(layer.bytes for layer in layers)
+        total_flops = sum(layer.flops for layer in layers)
+        details[f"C5_layer_m{m}"] = {
+            "us": round(seconds * 1e6, 2),
+            "GB/s": round(total_bytes / seconds / 1e9, 1),
+            "TFLOP/s": round(total_flops / seconds / 1e12, 2),
+        }
+        log(f"C5_layer_m{m}", details[f"C5_layer_m{m}"])
+        for layer in layers:
+            layer.release()
+    return details
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,158 @@
+/*
+ * libtensor_hip.so — the ROCm (gfx950) provider's C ABI.
+ *
+ * Two groups of entry points:
+ *
+ *  1. GGUF quantized-linear kernels, in the reference's native entry shape
+ *     TensorKernelV1 (src/tensor/include/tensor/abi.h:135-141).  Each validates
+ *     the call the way the reference's CPU image wrapper does
+ *     (src/tensor/compiler/cpu.py:49-155: ABI version, struct size, flags,
+ *     argument count, kinds, dtypes, device, rank/shape/stride/byte_size,
+ *     alignment) before it touches device memory, then enqueues asynchronously
+ *     on (hipStream_t)call->stream.handle and returns.  They replace the
+ *     AKAS GGUF kernels that the reference builds into .tbin images and
+ *     launches through Executable.launch -> Device._launch -> cuLaunchKernel
+ *     (benchmarks/kernels/showcase/kernels.py:114-119,
+ *      benchmarks/kernels/showcase/benchmark.py:276-290,
+ *      src/tensor/providers/cuda/device.py:211-229).
+ *
+ *  2. Runtime services the Python provider binds through ctypes, replacing the
+ *     CUDA driver calls of src/tensor/providers/cuda/driver.py:40-145
+ *     (memory, copies, streams, events, graphs, device properties).
+ *
+ * Every function returns TENSOR_OK or a TENSOR_ERROR_* code and, when error
+ * is non-null, fills it with a NUL-terminated message.  No C++ exception
+ * crosses this boundary.  Kernel calls borrow every descriptor until return;
+ * device buffers must stay alive until the stream has finished the work.
+ */
+#ifndef TENSOR_HIP_H
+#define TENSOR_HIP_H
+
+#include "tensor/abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML block type ids accepted by the GGUF entry points. */
+#define TENSOR_GGML_Q4_0 2u
+#define TENSOR_GGML_Q8_0 8u
+#define TENSOR_GGML_Q4_K 12u
+#define TENSOR_GGML_Q6_K 14u
+
+/* Largest activation row count of the decode GEMV entry. */
+#define TENSOR_GGUF_GEMV_MAX_M 8
+
+/* ----------------------------------------------------------- kernels --- */
+
+/*
+ * Decode GEMV, out[m, n] = sum_k x[m, k] * dequant(W)[n, k], fp32 accumulate.
+ * Replaces AKAS gemv_packed (benchmarks/kernels/showcase/kernels.py:119, the
+ * m == 1 branch; arguments [x, w, out] at benchmark.py:293-295, :460-464;
+ * numerics benchmark.py:466-472).  Arguments, in order:
+ *   0 x    buffer fp16  [M, K], 1 <= M <= TENSOR_GGUF_GEMV_MAX_M
+ *   1 w    buffer uint8 [N, K/QK*BLOCK]   raw GGUF rows
+ *   2 out  buffer fp16 or fp32 [M, N]
+ *   3 type scalar uint32 GGML type id
+ * Buffers: device type TENSOR_DEVICE_ROCM, the stream's ordinal, 16-byte
+ * aligned addresses, contiguous byte strides.
+ */
+int32_t tensor_gguf_gemv_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/*
+ * Prefill fused dequant-GEMM, out[m, n] = sum_k fp16(x[m, k]) *
+ * fp16(dequant(W)[n, k]), fp32 accumulate.  Replaces AKAS _packed
+ * (benchmarks/kernels/showcase/kernels.py:119, the m > 1 branch; numerics
+ * benchmark.py:473-477, triton_kernels.py:199-211).  Same arguments as
+ * tensor_gguf_gemv_v1 with any M >= 1.
+ */
+int32_t tensor_gguf_gemm_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/*
+ * Quantized linear with the reference showcase's dispatch: the decode GEMV
+ * for M <= TENSOR_GGUF_GEMV_MAX_M, the fused GEMM otherwise
+ * (benchmarks/kernels/showcase/kernels.py:114-119 picks gemv_packed for
+ * m == 1 and _packed otherwise).  Same arguments as tensor_gguf_gemv_v1.
+ */
+int32_t tensor_gguf_linear_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/*
+ * Dequantize raw GGUF rows: out[n, k] = dequant(W)[n, k], exact in fp32 and
+ * round-to-nearest-even in fp16 (block decoding of
+ * benchmarks/kernels/showcase/triton_kernels.py:134-181, the decode_ggml
+ * device function).  Arguments, in order:
+ *   0 w    buffer uint8 [N, K/QK*BLOCK]
+ *   1 out  buffer fp16 or fp32 [N, K]
+ *   2 type scalar uint32 GGML type id
+ */
+int32_t tensor_gguf_dequant_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/* ---------------------------------------------------- runtime services --- */
+
+typedef struct TensorHipDeviceInfoV1 {
+  char name[256];
+  char arch[64];             /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  uint64_t total_memory;     /* bytes */
+  uint64_t l2_cache_bytes;
+  int32_t compute_units;
+  int32_t clock_khz;
+  int32_t memory_clock_khz;
+  int32_t memory_bus_width;
+  int32_t max_threads_per_block;
+  int32_t max_shared_memory_per_block;
+  int32_t warp_size;
+  int32_t max_grid[3];
+  int32_t max_block[3];
+} TensorHipDeviceInfoV1;
+
+int32_t tensor_hip_device_count(int32_t *count, TensorErrorV1 *error);
+int32_t tensor_hip_device_info(int32_t ordinal, TensorHipDeviceInfoV1 *info,
+                               TensorErrorV1 *error);
+int32_t tensor_hip_set_device(int32_t ordinal, TensorErrorV1 *error);
+int32_t tensor_hip_device_synchronize(TensorErrorV1 *error);
+
+int32_t tensor_hip_malloc(uint64_t bytes, uint64_t *address, TensorErrorV1 *error);
+int32_t tensor_hip_free(uint64_t address, TensorErrorV1 *error);
+/* Host <-> device copies are synchronous with respect to the host. */
+int32_t tensor_hip_copy_htod(uint64_t dst, const void *src, uint64_t bytes,
+                             uint64_t stream, TensorErrorV1 *error);
+int32_t tensor_hip_copy_dtoh(void *dst, uint64_t src, uint64_t bytes,
+                             uint64_t stream, TensorErrorV1 *error);
+/* Device copies, fills and 2-D copies are ordered on the stream. */
+int32_t tensor_hip_copy_dtod(uint64_t dst, uint64_t src, uint64_t bytes,
+                             uint64_t stream, TensorErrorV1 *error);
+int32_t tensor_hip_copy_2d(uint64_t dst, uint64_t dst_pitch, uint64_t src,
+                           uint64_t src_pitch, uint64_t width, uint64_t height,
+                           uint64_t stream, TensorErrorV1 *error);
+int32_t tensor_hip_fill_u8(uint64_t dst, uint8_t value, uint64_t bytes,
+                           uint64_t stream, TensorErrorV1 *error);
+
+int32_t tensor_hip_stream_create(uint64_t *stream, TensorErrorV1 *error);
+int32_t tensor_hip_stream_destroy(uint64_t stream, TensorErrorV1 *error);
+int32_t tensor_hip_stream_synchronize(uint64_t stream, TensorErrorV1 *error);
+int32_t tensor_hip_stream_wait_event(uint64_t stream, uint64_t event,
+                                     TensorErrorV1 *error);
+
+int32_t tensor_hip_event_create(uint64_t *event, int32_t timing, TensorErrorV1 *error);
+int32_t tensor_hip_event_destroy(uint64_t event, TensorErrorV1 *error);
+int32_t tensor_hip_event_record(uint64_t event, uint64_t stream, TensorErrorV1 *error);
+int32_t tensor_hip_event_synchronize(uint64_t event, TensorErrorV1 *error);
+/* Sets *complete to 1 when the event has completed, else 0. */
+int32_t tensor_hip_event_query(uint64_t event, int32_t *complete, TensorErrorV1 *error);
+int32_t tensor_hip_event_elapsed(float *milliseconds, uint64_t start, uint64_t stop,
+                                 TensorErrorV1 *error);
+
+/* Stream capture into a graph (the reference's CudaGraph,
+ * src/tensor/providers/cuda/graph.py:8-98). */
+int32_t tensor_hip_capture_begin(uint64_t stream, TensorErrorV1 *error);
+int32_t tensor_hip_capture_end(uint64_t stream, uint64_t *graph_exec, TensorErrorV1 *error);
+int32_t tensor_hip_graph_launch(uint64_t graph_exec, uint64_t stream, TensorErrorV1 *error);
+int32_t tensor_hip_graph_destroy(uint64_t graph_exec, TensorErrorV1 *error);
+
+/* Library build identity: "tensor_hip <abi> <arch>". */
+const char *tensor_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TENSOR_HIP_H */

@@ -1,0 +1,372 @@
+// Decode GEMV over raw GGUF rows: out[m, n] = sum_k x[m, k] * W[n, k].
+//
+// HBM-bound weight streaming (reference kernel: AKAS gemv_packed, called at
+// benchmarks/kernels/showcase/kernels.py:114-119; restated by the Triton
+// gguf_gemv at triton_kernels.py:214-222).  Design for gfx950:
+//
+//  * One wave64 owns R consecutive rows.  Its lanes tile one "step" of the
+//    row: every lane issues 16-byte loads of packed block bytes, so one wave
+//    load instruction streams a contiguous ~1 KiB stretch of the row.
+//  * Packed codes are never converted to float element by element: bytes are
+//    spread into fp16 pairs "1024 + code" with one v_perm_b32 per two codes,
+//    then v_dot2_f32_f16 multiplies them with the fp16 activations and
+//    accumulates in fp32.  The 1024 offset (and the code bias of signed
+//    formats) is removed once per block run as  scale * (acc - bias * sum(x)),
+//    with sum(x) shared by all R rows of the wave.
+//  * Block scales and mins are unpacked in registers; the activation slice of
+//    a lane is loaded once per step and reused for all R rows.
+//  * Each row's partials are reduced across the wave with shuffles.
+#include "gguf_common.h"
+#include "gguf_launch.h"
+
+namespace tensor_gguf {
+
+// x is fp16 [M, K] (row stride K), W raw rows of row_bytes, out [M, N].
+
+// ------------------------------------------------------------------ Q4_K ---
+// Lane plan: 8 lanes per 144-byte super-block, 8 super-blocks per step.
+// Lane (slot, c): super-block slot = lane/8, 16-byte quant chunk c = lane%8,
+// i.e. pair j = c/2 (sub-blocks 2j, 2j+1) and half h = c%2 of its 32 bytes.
+// Low nibbles are elements 64j+16h+t of the block, high nibbles 64j+32+16h+t.
+template <int M, int R, typename OutT>
+__global__ __launch_bounds__(256) void gemv_q4k(const _Float16* __restrict__ x,
+                                                const uint8_t* __restrict__ w,
+                                                OutT* __restrict__ out, int n_rows, int k) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  if (row0 >= n_rows) return;
+  const int blocks = k >> 8;
+  const size_t row_bytes = (size_t)blocks * 144;
+  const int slot = lane >> 3, c = lane & 7, j = c >> 1, h = c & 1;
+  const int quant_offset = 16 + 32 * j + 16 * h;
+  const int x_offset = 64 * j + 16 * h;
+  const int rows = min(R, n_rows - row0);
+  float acc[M][R];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+  for (int b = slot; b < blocks; b += 8) {
+    uint4 xl[M][2], xh[M][2];
+    float sl[M], sh[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint8_t* xp = reinterpret_cast<const uint8_t*>(x + (size_t)m * k + b * 256 + x_offset);
+      xl[m][0] = load16(xp);
+      xl[m][1] = load16(xp + 16);
+      xh[m][0] = load16(xp + 64);
+      xh[m][1] = load16(xp + 80);
+    }
+    uint4 head[R], quant[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r < rows) {
+        const uint8_t* block = w + (size_t)(row0 + r) * row_bytes + (size_t)b * 144;
+        head[r] = load16(block);
+        quant[r] = load16(block + quant_offset);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      sl[m] = sum16(xl[m][0], xl[m][1]);
+      sh[m] = sum16(xh[m][0], xh[m][1]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r >= rows) break;
+      float al[M], ah[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) al[m] = ah[m] = 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t q = word(quant[r], u);
+        const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+        const uint32_t lo01 = magic01(lo), lo23 = magic23(lo);
+        const uint32_t hi01 = magic01(hi), hi23 = magic23(hi);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          al[m] = dot2(lo01, word(xl[m][u >> 1], 2 * (u & 1)), al[m]);
+          al[m] = dot2(lo23, word(xl[m][u >> 1], 2 * (u & 1) + 1), al[m]);
+          ah[m] = dot2(hi01, word(xh[m][u >> 1], 2 * (u & 1)), ah[m]);
+          ah[m] = dot2(hi23, word(xh[m][u >> 1], 2 * (u & 1) + 1), ah[m]);
+        }
+      }
+      int sc_lo, mn_lo, sc_hi, mn_hi;
+      q4k_scale_pair(head[r].y, head[r].z, head[r].w, j, sc_lo, mn_lo, sc_hi, mn_hi);
+      const float d = half_bits_to_float(head[r].x), dmin = half_bits_to_float(head[r].x >> 16);
+      const float ds_lo = d * (float)sc_lo, ds_hi = d * (float)sc_hi;
+      const float c_lo = 1024.0f * ds_lo + dmin * (float)mn_lo;
+      const float c_hi = 1024.0f * ds_hi + dmin * (float)mn_hi;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float v = acc[m][r];
+        v = fmaf(ds_lo, al[m], v);
+        v = fmaf(-c_lo, sl[m], v);
+        v = fmaf(ds_hi, ah[m], v);
+        v = fmaf(-c_hi, sh[m], v);
+        acc[m][r] = v;
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(acc[m][r]);
+      if (lane == 0 && r < rows) store_out<OutT>(out, (size_t)m * n_rows + row0 + r, v);
+    }
+}
+
+// ------------------------------------------------------------------ Q6_K ---
+// Lane plan: 4 lanes per 210-byte super-block, 16 super-blocks per step.
+// Lane part p = lane%4: half hh = p/2 (elements 128*hh ..), l0 = 16*(p%2).
+// Its 16 bytes of ql at 64hh+l0 (quarters 0 and 2), of ql at 64hh+32+l0
+// (quarters 1 and 3) and of qh at 128+32hh+l0 decode the four 16-element
+// runs 128hh + 32c + l0 + t (c = 0..3), each one scale group.
+template <int M, int R, typename OutT>
+__global__ __launch_bounds__(256) void gemv_q6k(const _Float16* __restrict__ x,
+                                                const uint8_t* __restrict__ w,
+                                                OutT* __restrict__ out, int n_rows, int k) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  if (row0 >= n_rows) return;
+  const int blocks = k >> 8;
+  const size_t row_bytes = (size_t)blocks * 210;
+  const int slot = lane >> 2, part = lane & 3, hh = part >> 1, l0 = 16 * (part & 1);
+  const int rows = min(R, n_rows - row0);
+  float acc[M][R];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+  for (int b = slot; b < blocks; b += 16) {
+    uint4 xs[M][4][2];
+    float sx[M][4];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint8_t* xp =
+            reinterpret_cast<const uint8_t*>(x + (size_t)m * k + b * 256 + 128 * hh + 32 * c + l0);
+        xs[m][c][0] = load16(xp);
+        xs[m][c][1] = load16(xp + 16);
+      }
+    uint4 qa[R], qb[R], qh[R];
+    uint2 sc8[R];
+    uint32_t dword[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r < rows) {
+        const uint8_t* block = w + (size_t)(row0 + r) * row_bytes + (size_t)b * 210;
+        qa[r] = load16(block + 64 * hh + l0);
+        qb[r] = load16(block + 64 * hh + 32 + l0);
+        qh[r] = load16(block + 128 + 32 * hh + l0);
+        sc8[r] = load8(block + 192 + 8 * hh);
+        dword[r] = load4(block + 206);  // high half is d
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sx[m][c] = sum16(xs[m][c][0], xs[m][c][1]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r >= rows) break;
+      float a[M][4];
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) a[m][c] = 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t A = word(qa[r], u), B = word(qb[r], u), H = word(qh[r], u);
+        uint32_t q[4];
+        q[0] = (A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u);
+        q[1] = (B & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u);
+        q[2] = ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
+        q[3] = ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint32_t p01 = magic01(q[c]), p23 = magic23(q[c]);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            a[m][c] = dot2(p01, word(xs[m][c][u >> 1], 2 * (u & 1)), a[m][c]);
+            a[m][c] = dot2(p23, word(xs[m][c][u >> 1], 2 * (u & 1) + 1), a[m][c]);
+          }
+        }
+      }
+      const float d = half_bits_to_float(dword[r] >> 16);
+      // scale of run c sits at byte 2c + (l0/16) of the 8 bytes at 192 + 8hh
+      const int p = part & 1;
+      float ds[4];
+      ds[0] = d * (float)(int8_t)(sc8[r].x >> (8 * p));
+      ds[1] = d * (float)(int8_t)(sc8[r].x >> (8 * (2 + p)));
+      ds[2] = d * (float)(int8_t)(sc8[r].y >> (8 * p));
+      ds[3] = d * (float)(int8_t)(sc8[r].y >> (8 * (2 + p)));
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float v = acc[m][r];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          v = fmaf(ds[c], a[m][c], v);
+          v = fmaf(-1056.0f * ds[c], sx[m][c], v);
+        }
+        acc[m][r] = v;
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(acc[m][r]);
+      if (lane == 0 && r < rows) store_out<OutT>(out, (size_t)m * n_rows + row0 + r, v);
+    }
+}
+
+// ------------------------------------------------------------ Q8_0, Q4_0 ---
+// Lane plan: one 32-element block per lane, 64 blocks per step.
+template <int TYPE, int M, int R, typename OutT>
+__global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
+                                                const uint8_t* __restrict__ w,
+                                                OutT* __restrict__ out, int n_rows, int k) {
+  constexpr int kBytes = TYPE == kQ8_0 ? 34 : 18;
+  // bias removed per block: 1024 from the fp16 widening, plus 128 for the
+  // sign flip of Q8_0 codes or 8 for the Q4_0 code offset
+  constexpr float kBias = TYPE == kQ8_0 ? 1152.0f : 1032.0f;
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  if (row0 >= n_rows) return;
+  const int blocks = k >> 5;
+  const size_t row_bytes = (size_t)blocks * kBytes;
+  const int rows = min(R, n_rows - row0);
+  float acc[M][R];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+  for (int b = lane; b < blocks; b += 64) {
+    uint4 xs[M][4];
+    float sx[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint8_t* xp = reinterpret_cast<const uint8_t*>(x + (size_t)m * k + b * 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xs[m][i] = load16(xp + 16 * i);
+    }
+    uint32_t head[R];
+    uint4 q0[R], q1[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r < rows) {
+        const uint8_t* block = w + (size_t)(row0 + r) * row_bytes + (size_t)b * kBytes;
+        head[r] = (uint32_t)block[0] | ((uint32_t)block[1] << 8);
+        q0[r] = load16(block + 2);
+        if (TYPE == kQ8_0) q1[r] = load16(block + 18);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      sx[m] = sum16(xs[m][0], xs[m][1]) + sum16(xs[m][2], xs[m][3]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r >= rows) break;
+      float a[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) a[m] = 0.0f;
+      if (TYPE == kQ8_0) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          // flip the sign bit: int8 code v becomes the unsigned byte v + 128
+          const uint32_t q = word(u < 4 ? q0[r] : q1[r], u & 3) ^ 0x80808080u;
+          const uint32_t p01 = magic01(q), p23 = magic23(q);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            a[m] = dot2(p01, word(xs[m][u >> 1], 2 * (u & 1)), a[m]);
+            a[m] = dot2(p23, word(xs[m][u >> 1], 2 * (u & 1) + 1), a[m]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t q = word(q0[r], u);
+          const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+          const uint32_t lo01 = magic01(lo), lo23 = magic23(lo);
+          const uint32_t hi01 = magic01(hi), hi23 = magic23(hi);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            // element t = 4u.. low nibbles; 16 + 4u.. high nibbles
+            a[m] = dot2(lo01, word(xs[m][u >> 1], 2 * (u & 1)), a[m]);
+            a[m] = dot2(lo23, word(xs[m][u >> 1], 2 * (u & 1) + 1), a[m]);
+            a[m] = dot2(hi01, word(xs[m][2 + (u >> 1)], 2 * (u & 1)), a[m]);
+            a[m] = dot2(hi23, word(xs[m][2 + (u >> 1)], 2 * (u & 1) + 1), a[m]);
+          }
+        }
+      }
+      const float d = half_bits_to_float(head[r]);
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[m][r] = fmaf(d, a[m] - kBias * sx[m], acc[m][r]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(acc[m][r]);
+      if (lane == 0 && r < rows) store_out<OutT>(out, (size_t)m * n_rows + row0 + r, v);
+    }
+}
+
+// --------------------------------------------------------------- launch ---
+
+template <int M, typename OutT>
+static hipError_t launch_m(const GemvArgs& a, hipStream_t stream) {
+  const _Float16* x = static_cast<const _Float16*>(a.x);
+  const uint8_t* w = static_cast<const uint8_t*>(a.w);
+  OutT* out = static_cast<OutT*>(a.out);
+  constexpr int R = M <= 2 ? 4 : (M <= 4 ? 2 : 1);
+  const int waves = (a.n + R - 1) / R;
+  const dim3 grid((waves + 3) / 4), block(256);
+  switch (a.type) {
+    case kQ4_K:
+      hipLaunchKernelGGL((gemv_q4k<M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
+      break;
+    case kQ6_K:
+      hipLaunchKernelGGL((gemv_q6k<M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
+      break;
+    case kQ8_0:
+      hipLaunchKernelGGL((gemv_q32<kQ8_0, M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
+      break;
+    case kQ4_0:
+      hipLaunchKernelGGL((gemv_q32<kQ4_0, M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <typename OutT>
+static hipError_t launch_out(const GemvArgs& a, hipStream_t stream) {
+  switch (a.m) {
+    case 1: return launch_m<1, OutT>(a, stream);
+    case 2: return launch_m<2, OutT>(a, stream);
+    case 3: return launch_m<3, OutT>(a, stream);
+    case 4: return launch_m<4, OutT>(a, stream);
+    case 5: return launch_m<5, OutT>(a, stream);
+    case 6: return launch_m<6, OutT>(a, stream);
+    case 7: return launch_m<7, OutT>(a, stream);
+    case 8: return launch_m<8, OutT>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t stream) {
+  return a.out_half ? launch_out<_Float16>(a, stream) : launch_out<float>(a, stream);
+}
+
+}  // namespace tensor_gguf

@@ -1,0 +1,34 @@
+// Host-side launch descriptors shared by the GGUF kernel translation units.
+// Shapes have been validated by the C-ABI entry points before these run.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tensor_gguf {
+
+struct GemvArgs {
+  const void* x;   // fp16 [m, k]
+  const void* w;   // raw GGUF rows [n, row_bytes]
+  void* out;       // fp16 or fp32 [m, n]
+  int type;        // GGML type id
+  int m, n, k;
+  bool out_half;
+};
+
+struct DequantArgs {
+  const void* w;   // raw GGUF rows [n, row_bytes]
+  void* out;       // fp16 or fp32 [n, k]
+  int type;
+  int n, k;
+  bool out_half;
+};
+
+// Largest M the decode GEMV entry accepts.
+constexpr int kGemvMaxM = 8;
+
+hipError_t launch_gemv(const GemvArgs& args, hipStream_t stream);
+hipError_t launch_dequant(const DequantArgs& args, hipStream_t stream);
+hipError_t launch_gemm(const GemvArgs& args, hipStream_t stream);
+
+}  // namespace tensor_gguf

@@ -1,0 +1,389 @@
+// C-ABI entry points of libtensor_hip.so: GGUF kernels in the TensorKernelV1
+// shape and the runtime services the Python provider binds with ctypes.
+// Declarations and their reference counterparts: include/tensor_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "gguf_launch.h"
+#include "tensor_hip.h"
+
+namespace {
+
+int32_t fail(TensorErrorV1* error, int32_t code, const char* format, ...) {
+  if (error) {
+    error->code = code;
+    va_list args;
+    va_start(args, format);
+    std::vsnprintf(error->message, sizeof(error->message), format, args);
+    va_end(args);
+  }
+  return code;
+}
+
+int32_t ok(TensorErrorV1* error) {
+  if (error) {
+    error->code = TENSOR_OK;
+    error->message[0] = 0;
+  }
+  return TENSOR_OK;
+}
+
+int32_t hip_fail(TensorErrorV1* error, hipError_t status, const char* what) {
+  return fail(error, TENSOR_ERROR_PROVIDER, "%s: %s (%s, %d)", what, hipGetErrorString(status),
+              hipGetErrorName(status), (int)status);
+}
+
+#define HIP_TRY(expr, what)                                  \
+  do {                                                       \
+    hipError_t status_ = (expr);                             \
+    if (status_ != hipSuccess) return hip_fail(error, status_, what); \
+  } while (0)
+
+struct Format {
+  int qk;
+  int bytes;
+};
+
+bool ggml_format(uint64_t type, Format* format) {
+  switch (type) {
+    case TENSOR_GGML_Q4_0: *format = {32, 18}; return true;
+    case TENSOR_GGML_Q8_0: *format = {32, 34}; return true;
+    case TENSOR_GGML_Q4_K: *format = {256, 144}; return true;
+    case TENSOR_GGML_Q6_K: *format = {256, 210}; return true;
+    default: return false;
+  }
+}
+
+// Common header checks of every kernel call (src/tensor/compiler/cpu.py:59-66).
+// Pure descriptor checks only: nothing here touches the HIP runtime, so every
+// argument error is reported before any device state is consulted.
+int32_t check_call(const TensorCallV1* call, uint32_t arguments, TensorErrorV1* error) {
+  if (!call || call->abi_version != TENSOR_ABI_VERSION || call->struct_size < sizeof(TensorCallV1))
+    return fail(error, TENSOR_ERROR_ABI, "unsupported call ABI");
+  if (call->flags || call->argument_count != arguments || !call->arguments)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "invalid argument count or flags");
+  if (call->stream.device_type != TENSOR_DEVICE_ROCM || call->stream.device_ordinal < 0)
+    return fail(error, TENSOR_ERROR_PROVIDER, "ROCm calls need a ROCm stream");
+  return TENSOR_OK;
+}
+
+// The stream's ordinal must be the calling thread's current HIP device.
+int32_t check_device(const TensorCallV1* call, TensorErrorV1* error) {
+  int device = -1;
+  hipError_t status = hipGetDevice(&device);
+  if (status != hipSuccess) return hip_fail(error, status, "hipGetDevice");
+  if (call->stream.device_ordinal != device)
+    return fail(error, TENSOR_ERROR_PROVIDER, "stream ordinal %d is not the current device %d",
+                (int)call->stream.device_ordinal, device);
+  return TENSOR_OK;
+}
+
+// A rank-2 contiguous device buffer of one of the allowed dtypes.
+int32_t check_matrix(const TensorArgumentV1& arg, const char* name, int ordinal, uint32_t dtype_a,
+                     uint32_t dtype_b, TensorErrorV1* error) {
+  const TensorBufferV1& b = arg.buffer;
+  if (arg.kind != TENSOR_ARG_BUFFER || (arg.dtype != dtype_a && arg.dtype != dtype_b) ||
+      b.dtype != arg.dtype)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "%s: wrong argument kind or dtype", name);
+  if (b.device_type != TENSOR_DEVICE_ROCM || b.device_ordinal != ordinal || !b.address ||
+      b.address % 16 || b.rank != 2 || !b.shape || !b.strides)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "%s: invalid buffer descriptor", name);
+  const uint64_t item = arg.dtype == TENSOR_UINT8 ? 1 : arg.dtype == TENSOR_FLOAT16 ? 2 : 4;
+  uint64_t bytes = item;
+  for (int axis = 1; axis >= 0; --axis) {
+    if (b.shape[axis] <= 0 || b.shape[axis] >= (int64_t)1 << 31 ||
+        b.strides[axis] != (int64_t)bytes)
+      return fail(error, TENSOR_ERROR_ARGUMENT, "%s: shape, stride or size mismatch", name);
+    bytes *= (uint64_t)b.shape[axis];
+  }
+  if (b.byte_size < bytes)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "%s: insufficient buffer storage", name);
+  return TENSOR_OK;
+}
+
+int32_t check_type(const TensorArgumentV1& arg, Format* format, TensorErrorV1* error) {
+  if (arg.kind != TENSOR_ARG_SCALAR || arg.dtype != TENSOR_UINT32)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "type: wrong argument kind or dtype");
+  if (arg.scalar >> 32)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "type: noncanonical scalar payload");
+  if (!ggml_format(arg.scalar, format))
+    return fail(error, TENSOR_ERROR_ARGUMENT, "type: unsupported GGML type %llu",
+                (unsigned long long)arg.scalar);
+  return TENSOR_OK;
+}
+
+enum class Op { kGemv, kGemm, kLinear };
+
+int32_t linear_call(const TensorCallV1* call, TensorErrorV1* error, Op op) {
+  ok(error);
+  if (int32_t s = check_call(call, 4, error)) return s;
+  const int ordinal = call->stream.device_ordinal;
+  const TensorArgumentV1* a = call->arguments;
+  Format format;
+  if (int32_t s = check_type(a[3], &format, error)) return s;
+  if (int32_t s = check_matrix(a[0], "x", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT16, error)) return s;
+  if (int32_t s = check_matrix(a[1], "w", ordinal, TENSOR_UINT8, TENSOR_UINT8, error)) return s;
+  if (int32_t s = check_matrix(a[2], "out", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT32, error)) return s;
+  const int64_t m = a[0].buffer.shape[0], k = a[0].buffer.shape[1], n = a[1].buffer.shape[0];
+  if (k % format.qk || a[1].buffer.shape[1] != k / format.qk * format.bytes)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "w: shape, stride or size mismatch");
+  if (a[2].buffer.shape[0] != m || a[2].buffer.shape[1] != n)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "out: shape, stride or size mismatch");
+  if (op == Op::kGemv && m > tensor_gguf::kGemvMaxM)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "x: decode GEMV takes at most %d rows",
+                tensor_gguf::kGemvMaxM);
+  if (int32_t s = check_device(call, error)) return s;
+  tensor_gguf::GemvArgs args;
+  args.x = reinterpret_cast<const void*>(a[0].buffer.address);
+  args.w = reinterpret_cast<const void*>(a[1].buffer.address);
+  args.out = reinterpret_cast<void*>(a[2].buffer.address);
+  args.type = (int)a[3].scalar;
+  args.m = (int)m;
+  args.n = (int)n;
+  args.k = (int)k;
+  args.out_half = a[2].dtype == TENSOR_FLOAT16;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
+  const bool gemv = op == Op::kGemv || (op == Op::kLinear && m <= tensor_gguf::kGemvMaxM);
+  hipError_t status = gemv ? tensor_gguf::launch_gemv(args, stream) : tensor_gguf::launch_gemm(args, stream);
+  if (status != hipSuccess) return hip_fail(error, status, gemv ? "GGUF GEMV launch" : "GGUF GEMM launch");
+  return TENSOR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t tensor_gguf_gemv_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  return linear_call(call, error, Op::kGemv);
+}
+
+int32_t tensor_gguf_gemm_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  return linear_call(call, error, Op::kGemm);
+}
+
+int32_t tensor_gguf_linear_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  return linear_call(call, error, Op::kLinear);
+}
+
+int32_t tensor_gguf_dequant_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  ok(error);
+  if (int32_t s = check_call(call, 3, error)) return s;
+  const int ordinal = call->stream.device_ordinal;
+  const TensorArgumentV1* a = call->arguments;
+  Format format;
+  if (int32_t s = check_type(a[2], &format, error)) return s;
+  if (int32_t s = check_matrix(a[0], "w", ordinal, TENSOR_UINT8, TENSOR_UINT8, error)) return s;
+  if (int32_t s = check_matrix(a[1], "out", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT32, error)) return s;
+  const int64_t n = a[0].buffer.shape[0], k = a[1].buffer.shape[1];
+  if (a[1].buffer.shape[0] != n || k % format.qk ||
+      a[0].buffer.shape[1] != k / format.qk * format.bytes)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "out: shape, stride or size mismatch");
+  if (int32_t s = check_device(call, error)) return s;
+  tensor_gguf::DequantArgs args;
+  args.w = reinterpret_cast<const void*>(a[0].buffer.address);
+  args.out = reinterpret_cast<void*>(a[1].buffer.address);
+  args.type = (int)a[2].scalar;
+  args.n = (int)n;
+  args.k = (int)k;
+  args.out_half = a[1].dtype == TENSOR_FLOAT16;
+  hipError_t status = tensor_gguf::launch_dequant(args, reinterpret_cast<hipStream_t>(call->stream.handle));
+  if (status != hipSuccess) return hip_fail(error, status, "GGUF dequant launch");
+  return TENSOR_OK;
+}
+
+// ------------------------------------------------------ runtime services ---
+
+int32_t tensor_hip_device_count(int32_t* count, TensorErrorV1* error) {
+  int value = 0;
+  hipError_t status = hipGetDeviceCount(&value);
+  if (status == hipErrorNoDevice) value = 0;
+  else if (status != hipSuccess) return hip_fail(error, status, "hipGetDeviceCount");
+  *count = value;
+  return ok(error);
+}
+
+int32_t tensor_hip_device_info(int32_t ordinal, TensorHipDeviceInfoV1* info, TensorErrorV1* error) {
+  hipDeviceProp_t p;
+  HIP_TRY(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
+  std::memset(info, 0, sizeof(*info));
+  std::snprintf(info->name, sizeof(info->name), "%s", p.name);
+  std::snprintf(info->arch, sizeof(info->arch), "%s", p.gcnArchName);
+  info->total_memory = p.totalGlobalMem;
+  info->l2_cache_bytes = (uint64_t)p.l2CacheSize;
+  info->compute_units = p.multiProcessorCount;
+  info->clock_khz = p.clockRate;
+  info->memory_clock_khz = p.memoryClockRate;
+  info->memory_bus_width = p.memoryBusWidth;
+  info->max_threads_per_block = p.maxThreadsPerBlock;
+  info->max_shared_memory_per_block = (int32_t)p.sharedMemPerBlock;
+  info->warp_size = p.warpSize;
+  for (int i = 0; i < 3; ++i) {
+    info->max_grid[i] = p.maxGridSize[i];
+    info->max_block[i] = p.maxThreadsDim[i];
+  }
+  return ok(error);
+}
+
+int32_t tensor_hip_set_device(int32_t ordinal, TensorErrorV1* error) {
+  HIP_TRY(hipSetDevice(ordinal), "hipSetDevice");
+  return ok(error);
+}
+
+int32_t tensor_hip_device_synchronize(TensorErrorV1* error) {
+  HIP_TRY(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  return ok(error);
+}
+
+int32_t tensor_hip_malloc(uint64_t bytes, uint64_t* address, TensorErrorV1* error) {
+  void* p = nullptr;
+  HIP_TRY(hipMalloc(&p, bytes ? bytes : 1), "hipMalloc");
+  *address = reinterpret_cast<uint64_t>(p);
+  return ok(error);
+}
+
+int32_t tensor_hip_free(uint64_t address, TensorErrorV1* error) {
+  HIP_TRY(hipFree(reinterpret_cast<void*>(address)), "hipFree");
+  return ok(error);
+}
+
+int32_t tensor_hip_copy_htod(uint64_t dst, const void* src, uint64_t bytes, uint64_t stream,
+                             TensorErrorV1* error) {
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), src, bytes, hipMemcpyHostToDevice, s),
+          "hipMemcpyAsync(HtoD)");
+  HIP_TRY(hipStreamSynchronize(s), "hipStreamSynchronize");
+  return ok(error);
+}
+
+int32_t tensor_hip_copy_dtoh(void* dst, uint64_t src, uint64_t bytes, uint64_t stream,
+                             TensorErrorV1* error) {
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  HIP_TRY(hipMemcpyAsync(dst, reinterpret_cast<const void*>(src), bytes, hipMemcpyDeviceToHost, s),
+          "hipMemcpyAsync(DtoH)");
+  HIP_TRY(hipStreamSynchronize(s), "hipStreamSynchronize");
+  return ok(error);
+}
+
+int32_t tensor_hip_copy_dtod(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream,
+                             TensorErrorV1* error) {
+  HIP_TRY(hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src), bytes,
+                         hipMemcpyDeviceToDevice, reinterpret_cast<hipStream_t>(stream)),
+          "hipMemcpyAsync(DtoD)");
+  return ok(error);
+}
+
+int32_t tensor_hip_copy_2d(uint64_t dst, uint64_t dst_pitch, uint64_t src, uint64_t src_pitch,
+                           uint64_t width, uint64_t height, uint64_t stream, TensorErrorV1* error) {
+  HIP_TRY(hipMemcpy2DAsync(reinterpret_cast<void*>(dst), dst_pitch, reinterpret_cast<const void*>(src),
+                           src_pitch, width, height, hipMemcpyDeviceToDevice,
+                           reinterpret_cast<hipStream_t>(stream)),
+          "hipMemcpy2DAsync");
+  return ok(error);
+}
+
+int32_t tensor_hip_fill_u8(uint64_t dst, uint8_t value, uint64_t bytes, uint64_t stream,
+                           TensorErrorV1* error) {
+  HIP_TRY(hipMemsetAsync(reinterpret_cast<void*>(dst), value, bytes, reinterpret_cast<hipStream_t>(stream)),
+          "hipMemsetAsync");
+  return ok(error);
+}
+
+int32_t tensor_hip_stream_create(uint64_t* stream, TensorErrorV1* error) {
+  hipStream_t s = nullptr;
+  HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+  *stream = reinterpret_cast<uint64_t>(s);
+  return ok(error);
+}
+
+int32_t tensor_hip_stream_destroy(uint64_t stream, TensorErrorV1* error) {
+  HIP_TRY(hipStreamDestroy(reinterpret_cast<hipStream_t>(stream)), "hipStreamDestroy");
+  return ok(error);
+}
+
+int32_t tensor_hip_stream_synchronize(uint64_t stream, TensorErrorV1* error) {
+  HIP_TRY(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)), "hipStreamSynchronize");
+  return ok(error);
+}
+
+int32_t tensor_hip_stream_wait_event(uint64_t stream, uint64_t event, TensorErrorV1* error) {
+  HIP_TRY(hipStreamWaitEvent(reinterpret_cast<hipStream_t>(stream), reinterpret_cast<hipEvent_t>(event), 0),
+          "hipStreamWaitEvent");
+  return ok(error);
+}
+
+int32_t tensor_hip_event_create(uint64_t* event, int32_t timing, TensorErrorV1* error) {
+  hipEvent_t e = nullptr;
+  HIP_TRY(hipEventCreateWithFlags(&e, timing ? hipEventDefault : hipEventDisableTiming),
+          "hipEventCreateWithFlags");
+  *event = reinterpret_cast<uint64_t>(e);
+  return ok(error);
+}
+
+int32_t tensor_hip_event_destroy(uint64_t event, TensorErrorV1* error) {
+  HIP_TRY(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)), "hipEventDestroy");
+  return ok(error);
+}
+
+int32_t tensor_hip_event_record(uint64_t event, uint64_t stream, TensorErrorV1* error) {
+  HIP_TRY(hipEventRecord(reinterpret_cast<hipEvent_t>(event), reinterpret_cast<hipStream_t>(stream)),
+          "hipEventRecord");
+  return ok(error);
+}
+
+int32_t tensor_hip_event_synchronize(uint64_t event, TensorErrorV1* error) {
+  HIP_TRY(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)), "hipEventSynchronize");
+  return ok(error);
+}
+
+int32_t tensor_hip_event_query(uint64_t event, int32_t* complete, TensorErrorV1* error) {
+  hipError_t status = hipEventQuery(reinterpret_cast<hipEvent_t>(event));
+  if (status == hipErrorNotReady) {
+    *complete = 0;
+    return ok(error);
+  }
+  if (status != hipSuccess) return hip_fail(error, status, "hipEventQuery");
+  *complete = 1;
+  return ok(error);
+}
+
+int32_t tensor_hip_event_elapsed(float* milliseconds, uint64_t start, uint64_t stop, TensorErrorV1* error) {
+  HIP_TRY(hipEventElapsedTime(milliseconds, reinterpret_cast<hipEvent_t>(start),
+                              reinterpret_cast<hipEvent_t>(stop)),
+          "hipEventElapsedTime");
+  return ok(error);
+}
+
+int32_t tensor_hip_capture_begin(uint64_t stream, TensorErrorV1* error) {
+  HIP_TRY(hipStreamBeginCapture(reinterpret_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal),
+          "hipStreamBeginCapture");
+  return ok(error);
+}
+
+int32_t tensor_hip_capture_end(uint64_t stream, uint64_t* graph_exec, TensorErrorV1* error) {
+  hipGraph_t graph = nullptr;
+  HIP_TRY(hipStreamEndCapture(reinterpret_cast<hipStream_t>(stream), &graph), "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  hipError_t status = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (status != hipSuccess) return hip_fail(error, status, "hipGraphInstantiate");
+  *graph_exec = reinterpret_cast<uint64_t>(exec);
+  return ok(error);
+}
+
+int32_t tensor_hip_graph_launch(uint64_t graph_exec, uint64_t stream, TensorErrorV1* error) {
+  HIP_TRY(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), reinterpret_cast<hipStream_t>(stream)),
+          "hipGraphLaunch");
+  return ok(error);
+}
+
+int32_t tensor_hip_graph_destroy(uint64_t graph_exec, TensorErrorV1* error) {
+  HIP_TRY(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+  return ok(error);
+}
+
+const char* tensor_hip_version(void) { return "tensor_hip 1.3 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,346 @@
+"""ROCm/HIP runtime provider for one MI355X (gfx950) device.
+
+Behavioural template: the reference CUDA provider
+(src/tensor/providers/cuda/device.py:16-448) — a session owns (or borrows) a
+stream, allocates buffers, loads executables, launches them asynchronously
+through the TensorCallV1 descriptor and records events.  Every device call goes
+through libtensor_hip.so (include/tensor_hip.h): the kernels are its
+TensorKernelV1 entry points and memory/streams/events are its runtime services.
+
+Executables are the library's built-in GGUF kernels, loaded by name
+(``device.load("gguf_linear", encoding="q4_k")``) or from a manifest dict.
+"""
+
+from __future__ import annotations
+
+import contextlib
+import ctypes as c
+
+import numpy as np
+
+from tensor_amd import _native
+from tensor_amd._native import HipError, TensorHipDeviceInfo
+from tensor_amd.runtime.abi import CAPABILITIES, DEVICE_ROCM, ErrorDescriptor, StreamDescriptor, check_requirement
+from tensor_amd.runtime.buffer import Buffer
+from tensor_amd.runtime.event import Event
+from tensor_amd.runtime.executable import Executable
+from tensor_amd.runtime.session import Session
+
+
+def device_count() -> int:
+    count = c.c_int32()
+    _native.call("tensor_hip_device_count", c.byref(count))
+    return count.value
+
+
+class Device(Session):
+    device_type = DEVICE_ROCM
+    error = HipError
+    capabilities = CAPABILITIES | {"events", "async_launch", "external_streams", "graphs"}
+
+    def __init__(self, ordinal: int = 0, *, stream: int | None = None):
+        if type(ordinal) is not int or ordinal < 0:
+            raise ValueError("ordinal must be a non-negative integer")
+        if stream is not None and (type(stream) is not int or not 0 <= stream < 1 << 64):
+            raise ValueError("stream must be a HIP stream integer handle")
+        self.ordinal = ordinal
+        self._external_stream = stream
+        self.owns_stream = stream is None
+        count = device_count()
+        if ordinal >= count:
+            raise ValueError(f"HIP device {ordinal} is not present ({count} visible)")
+        props = TensorHipDeviceInfo()
+        _native.call("tensor_hip_device_info", ordinal, c.byref(props))
+        arch = props.arch.decode()
+        self.info = {
+            "ordinal": ordinal,
+            "name": props.name.decode(),
+            "arch": arch.split(":")[0],
+            "arch_features": arch,
+            "provider": "hip",
+            "compute_units": props.compute_units,
+            "clock_khz": props.clock_khz,
+            "memory_clock_khz": props.memory_clock_khz,
+            "memory_bus_width": props.memory_bus_width,
+            "total_memory": props.total_memory,
+            "l2_cache_bytes": props.l2_cache_bytes,
+            "warp_size": props.warp_size,
+        }
+        self.limits = {
+            "grid": list(props.max_grid),
+            "block": list(props.max_block),
+            "threads": props.max_threads_per_block,
+            "shared_memory_bytes": props.max_shared_memory_per_block,
+        }
+        self.stream = 0
+        self._buffers: set = set()
+        self._events: set = set()
+        self._consumers: set = set()
+        self._graphs: set = set()
+        self._generation = 0
+        self._open = False
+
+    # ------------------------------------------------------------ session --
+    def __enter__(self) -> "Device":
+        if self._open:
+            raise HipError("Device", 3, "device session is already open")
+        _native.call("tensor_hip_set_device", self.ordinal)
+        if self.owns_stream:
+            handle = c.c_uint64()
+            _native.call("tensor_hip_stream_create", c.byref(handle))
+            self.stream = handle.value
+        else:
+            self.stream = self._external_stream
+        self._generation += 1
+        self._start_session()
+        self._open = True
+        return self
+
+    def _check(self) -> None:
+        if not self._open:
+            raise HipError("Device", 3, "HIP device session is closed")
+        _native.call("tensor_hip_set_device", self.ordinal)
+
+    def stream_descriptor(self) -> StreamDescriptor:
+        return StreamDescriptor(DEVICE_ROCM, self.ordinal, self.stream)
+
+    def synchronize(self) -> None:
+        self._check()
+        _native.call("tensor_hip_stream_synchronize", self.stream)
+        for handle in self._consumers:
+            _native.call("tensor_hip_stream_synchronize", handle)
+
+    def _order_streams(self, producer: int, consumer: int) -> None:
+        if producer == consumer:
+            return
+        event = c.c_uint64()
+        _native.call("tensor_hip_event_create", c.byref(event), 0)
+        try:
+            _native.call("tensor_hip_event_record", event.value, producer)
+            _native.call("tensor_hip_stream_wait_event", consumer, event.value)
+        finally:
+            _native.call("tensor_hip_event_destroy", event.value)
+
+    def wait_for(self, producer_stream: int) -> None:
+        """Order this session's stream after work queued on another stream."""
+        self._check()
+        self._order_streams(int(producer_stream), self.stream)
+
+    def handoff(self, consumer_stream: int) -> None:
+        """Order another stream after work already queued on this session's stream."""
+        self._check()
+        self._order_streams(self.stream, int(consumer_stream))
+        self._consumers.add(int(consumer_stream))
+
+    # ------------------------------------------------------------ buffers --
+    def empty(self, shape, dtype="float32") -> Buffer:
+        self._check()
+        shape = (shape,) if isinstance(shape, int) else tuple(shape)
+        if not shape or any(type(size) is not int or size < 1 for size in shape):
+            raise ValueError("buffer shape must contain positive integers")
+        dtype = np.dtype(dtype)
+        if dtype.hasobject or dtype.itemsize < 1:
+            raise ValueError("buffer dtype must have a fixed byte size")
+        nbytes = dtype.itemsize
+        for extent in shape:
+            nbytes *= extent
+        address = c.c_uint64()
+        _native.call("tensor_hip_malloc", nbytes, c.byref(address))
+        buffer = Buffer(self, address.value, shape, dtype)
+        self._buffers.add(buffer)
+        return buffer
+
+    def from_numpy(self, array, dtype=None) -> Buffer:
+        host = np.ascontiguousarray(array, dtype=dtype)
+        buffer = self.empty(host.shape if host.shape else (1,), host.dtype)
+        try:
+            _native.call("tensor_hip_copy_htod", buffer.pointer, host.ctypes.data, host.nbytes, self.stream)
+            return buffer
+        except BaseException:
+            buffer.release()
+            raise
+
+    def upload(self, buffer: Buffer, array) -> Buffer:
+        """Overwrite a buffer's contents from host memory (synchronous)."""
+        buffer._check()
+        host = np.ascontiguousarray(array, dtype=buffer.dtype)
+        if host.nbytes != buffer.nbytes:
+            raise ValueError("upload needs exactly the buffer's storage size")
+        _native.call("tensor_hip_copy_htod", buffer.pointer, host.ctypes.data, host.nbytes, self.stream)
+        return buffer
+
+    def full(self, shape, fill_value, dtype="float32") -> Buffer:
+        return self.from_numpy(np.full(shape, fill_value, dtype=dtype))
+
+    def zeros(self, shape, dtype="float32") -> Buffer:
+        buffer = self.empty(shape, dtype)
+        try:
+            _native.call("tensor_hip_fill_u8", buffer.pointer, 0, buffer.nbytes, self.stream)
+            return buffer
+        except BaseException:
+            buffer.release()
+            raise
+
+    def ones(self, shape, dtype="float32") -> Buffer:
+        return self.full(shape, 1, dtype)
+
+    def randn(self, shape, dtype="float32", *, seed=None) -> Buffer:
+        return self.from_numpy(np.random.default_rng(seed).standard_normal(shape).astype(dtype))
+
+    def arange(self, stop: int, dtype="float32") -> Buffer:
+        return self.from_numpy(np.arange(stop, dtype=dtype))
+
+    def fill_bytes(self, buffer: Buffer, value: int) -> None:
+        """Set every byte of a buffer (ordered on the stream)."""
+        buffer._check()
+        _native.call("tensor_hip_fill_u8", buffer.pointer, int(value) & 0xFF, buffer.nbytes, self.stream)
+
+    def _download(self, buffer: Buffer):
+        result = np.empty(buffer.shape, dtype=buffer.dtype)
+        _native.call("tensor_hip_copy_dtoh", result.ctypes.data, buffer.pointer, buffer.nbytes, self.stream)
+        return result
+
+    def _copy(self, destination: Buffer, source: Buffer) -> None:
+        if destination.pointer != source.pointer:
+            _native.call("tensor_hip_copy_dtod", destination.pointer, source.pointer, source.nbytes, self.stream)
+
+    def _copy_columns(self, destination: Buffer, source: Buffer, offset: int) -> None:
+        if (source.pointer < destination.pointer + destination.nbytes
+                and destination.pointer < source.pointer + source.nbytes):
+            if source.pointer == destination.pointer and source.shape == destination.shape and offset == 0:
+                return
+            raise ValueError("overlapping column copies are unsupported")
+        width = source.dtype.itemsize
+        _native.call(
+            "tensor_hip_copy_2d",
+            destination.pointer + offset * width, destination.shape[1] * width,
+            source.pointer, source.shape[1] * width,
+            source.shape[1] * width, source.shape[0], self.stream,
+        )
+
+    def _dispose_buffer(self, buffer: Buffer) -> None:
+        if buffer._owner is not None:
+            release = getattr(buffer._owner, "release", None)
+            if release is not None:
+                release()
+            buffer._owner = None
+        else:
+            _native.call("tensor_hip_free", buffer.pointer)
+
+    # -------------------------------------------------------- executables --
+    def load(self, artifact, **options) -> Executable:
+        """Load a built-in GGUF executable by kernel name or manifest dict."""
+        from tensor_amd.gguf.kernels import manifest as gguf_manifest
+
+        self._check()
+        if isinstance(artifact, str):
+            manifest = gguf_manifest(artifact, **options)
+        elif isinstance(artifact, dict):
+            if options:
+                raise ValueError("options apply only to kernels loaded by name")
+            manifest = artifact
+        else:
+            raise TypeError("artifact must be a built-in kernel name or a manifest dict")
+        if manifest.get("provider") != "hip":
+            raise ValueError("artifact requires a different runtime provider")
+        check_requirement(manifest["runtime_abi"], self.capabilities)
+        if manifest.get("target", self.info["arch"]) != self.info["arch"]:
+            raise ValueError(f"artifact target {manifest['target']} does not match device {self.info['arch']}")
+        function = _native.kernel(manifest["entrypoint"])
+        return Executable(self, manifest, _native.library(), function, None)
+
+    def _unload_executable(self, executable) -> None:
+        pass  # entry points live for the life of the process-wide library
+
+    def _launch(self, executable, call) -> None:
+        self._check()
+        error = ErrorDescriptor()
+        status = executable.function(c.byref(call.descriptor), c.byref(error))
+        if status:
+            raise HipError(executable.manifest["entrypoint"], status, error.message.decode(errors="replace"))
+
+    # -------------------------------------------------------------- events --
+    def record_event(self, *, timing: bool = False) -> Event:
+        self._check()
+        handle = c.c_uint64()
+        _native.call("tensor_hip_event_create", c.byref(handle), int(timing))
+        try:
+            _native.call("tensor_hip_event_record", handle.value, self.stream)
+        except BaseException:
+            _native.call("tensor_hip_event_destroy", handle.value)
+            raise
+        event = Event(self, handle.value)
+        self._events.add(event)
+        return event
+
+    def wait(self, event: Event) -> None:
+        self._check()
+        event._check(self)
+        _native.call("tensor_hip_stream_wait_event", self.stream, event.handle)
+
+    def elapsed_ms(self, start: Event, stop: Event) -> float:
+        """Milliseconds between two timing events recorded on this stream."""
+        start._check(self)
+        stop._check(self)
+        value = c.c_float()
+        _native.call("tensor_hip_event_elapsed", c.byref(value), start.handle, stop.handle)
+        return value.value
+
+    def _synchronize_event(self, event: Event) -> None:
+        _native.call("tensor_hip_event_synchronize", event.handle)
+
+    def _dispose_event(self, event: Event) -> None:
+        _native.call("tensor_hip_event_destroy", event.handle)
+
+    # -------------------------------------------------------------- graphs --
+    def graph(self, callback):
+        """Capture the launches ``callback()`` enqueues into a replayable graph."""
+        from tensor_amd.providers.hip_graph import HipGraph
+
+        return HipGraph(self, callback)
+
+    # ------------------------------------------------------------ teardown --
+    def _cleanup(self) -> None:
+        errors = []
+
+        def attempt(function, *arguments):
+            try:
+                function(*arguments)
+            except HipError as exc:
+                errors.append(exc)
+
+        if self._open:
+            attempt(_native.call, "tensor_hip_set_device", self.ordinal)
+            attempt(_native.call, "tensor_hip_stream_synchronize", self.stream)
+            for handle in self._consumers:
+                attempt(_native.call, "tensor_hip_stream_synchronize", handle)
+        for graph in list(self._graphs):
+            attempt(graph._dispose)
+        for event in list(self._events):
+            attempt(event.release)
+        for buffer in list(self._buffers):
+            attempt(buffer._dispose)
+        for executable in list(getattr(self, "_executables", {}).values()):
+            attempt(executable._dispose)
+        if self._open and self.owns_stream and self.stream:
+            attempt(_native.call, "tensor_hip_stream_destroy", self.stream)
+        self._open = False
+        self._buffers.clear()
+        self._events.clear()
+        self._consumers.clear()
+        self._graphs.clear()
+        self.stream = 0
+        if errors:
+            raise errors[0]
+
+    def __exit__(self, exc_type, exc, tb) -> None:
+        try:
+            self._cleanup()
+        except HipError:
+            if exc_type is None:
+                raise
+
+    @contextlib.contextmanager
+    def session(self):
+        with self:
+            yield self

@@ -1,0 +1,43 @@
+"""Seeded inputs shared by the GPU parity tests and the benchmark checks."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from tensor_amd.gguf import quant as Q
+
+SLAB_ROWS = 2048
+
+
+def weight(n: int, k: int, encoding, seed: int) -> np.ndarray:
+    """Raw GGUF rows [n, row_bytes].  Up to SLAB_ROWS rows are drawn from
+    N(0, 0.02) and quantized; taller matrices repeat that slab, so full-size
+    shapes (a 151936-row LM head) stay cheap to build on the host."""
+    code = Q.ggml_type(encoding)
+    rows = min(n, SLAB_ROWS)
+    slab = Q.sample_weight(rows, k, code, seed=seed)
+    if rows == n:
+        return slab
+    reps = -(-n // rows)
+    return np.ascontiguousarray(np.tile(slab, (reps, 1))[:n])
+
+
+def activation(m: int, k: int, seed: int) -> np.ndarray:
+    return Q.sample_activation(m, k, seed=seed)
+
+
+def random_blocks(encoding, n: int, k: int, seed: int, scale: float = 0.05) -> np.ndarray:
+    """Random block bytes (every bit pattern of the code fields) with finite fp16 scales."""
+    code = Q.ggml_type(encoding)
+    qk, size = Q.GEOMETRY[code]
+    rng = np.random.default_rng(seed)
+    blocks = n * k // qk
+    raw = rng.integers(0, 256, size=(blocks, size), dtype=np.uint8)
+    halves = (rng.standard_normal((blocks, 2)) * scale).astype(np.float16).view(np.uint8).reshape(blocks, 4)
+    if code in (Q.Q4_0, Q.Q8_0):
+        raw[:, 0:2] = halves[:, 0:2]
+    elif code == Q.Q4_K:
+        raw[:, 0:4] = halves
+    else:
+        raw[:, 208:210] = halves[:, 0:2]
+    return raw.reshape(n, -1)

@@ -1,0 +1,218 @@
+"""C-ABI contract of libtensor_hip.so, checked on the CPU.
+
+Mirrors the reference's descriptor-tampering tests
+(tests/runtime/test_runtime_abi.py:33-44, :89-104; src/tensor/native/host.cpp:78-83):
+every malformed call is rejected with the right status before any device
+state is touched, so none of these calls needs a GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes as c
+import re
+from pathlib import Path
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+from tensor_amd import _native
+from tensor_amd.gguf import kernels
+from tensor_amd.runtime import abi
+from tensor_amd.runtime.signature import bind_shapes
+
+ROOT = Path(__file__).resolve().parents[1]
+OK, ERR_ABI, ERR_ARG, ERR_PROVIDER = 0, 1, 2, 3
+
+
+def test_descriptor_sizes():
+    assert [c.sizeof(s) for s in (abi.BufferDescriptor, abi.Argument, abi.StreamDescriptor,
+                                  abi.CallDescriptor, abi.ErrorDescriptor, abi.WorkspaceRequirements,
+                                  abi.ExecutableDescriptor, abi.EventDescriptor)] == [48, 64, 16, 72, 512, 24, 64, 40]
+
+
+def declared_functions():
+    names = []
+    for header in sorted((ROOT / "include").rglob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names += re.findall(r"^\s*(?:int32_t|const char\s*\*)\s*\*?\s*(\w+)\s*\(", text, flags=re.M)
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.library()
+    names = declared_functions()
+    assert "tensor_gguf_gemv_v1" in names and "tensor_hip_malloc" in names
+    missing = [name for name in names if not hasattr(lib, name)]
+    assert not missing, missing
+    assert set(_native.KERNELS) | set(_native.SERVICES) | {"tensor_hip_version"} == set(names)
+
+
+class Call:
+    """A well-formed 4-argument linear call with fake (never dereferenced) addresses."""
+
+    def __init__(self, m=1, n=64, k=512, type_=12, out_dtype=10, block=144, qk=256):
+        self.shapes = [(m, k), (n, k // qk * block), (m, n)]
+        dtypes = [10, 3, out_dtype]
+        items = [2, 1, 2 if out_dtype == 10 else 4]
+        self.keep = []
+        self.args = (abi.Argument * 4)()
+        for i, (shape, dtype, item) in enumerate(zip(self.shapes, dtypes, items)):
+            shp = (c.c_int64 * 2)(*shape)
+            strides = (c.c_int64 * 2)(shape[1] * item, item)
+            self.keep += [shp, strides]
+            self.args[i].kind = 1
+            self.args[i].dtype = dtype
+            self.args[i].buffer = abi.BufferDescriptor(0x10000 * (i + 1), shape[0] * shape[1] * item, shp, strides,
+                                                       2, dtype, 10, 0)
+        self.args[3].kind = 2
+        self.args[3].dtype = 7
+        self.args[3].scalar = type_
+        self.call = abi.CallDescriptor(1, 72, self.args, 4, 0, (c.c_uint32 * 3)(1, 1, 1),
+                                       (c.c_uint32 * 3)(256, 1, 1), 0, abi.StreamDescriptor(10, 0, 0))
+
+    def run(self, entry="tensor_gguf_gemv_v1"):
+        error = abi.ErrorDescriptor()
+        error.message = b"x" * 507
+        status = _native.kernel(entry)(c.byref(self.call), c.byref(error))
+        return status, error.message.decode()
+
+
+def tamper(**changes):
+    call = Call(**changes.pop("shape", {}))
+    for path, value in changes.items():
+        target = call
+        parts = path.split(".")
+        for part in parts[:-1]:
+            target = target[int(part)] if part.isdigit() else getattr(target, part)
+        setattr(target, parts[-1], value)
+    return call
+
+
+@pytest.mark.parametrize("mutation,code,needle", [
+    ({"call.abi_version": 2}, ERR_ABI, "ABI"),
+    ({"call.struct_size": 8}, ERR_ABI, "ABI"),
+    ({"call.flags": 1}, ERR_ARG, "argument count or flags"),
+    ({"call.argument_count": 3}, ERR_ARG, "argument count or flags"),
+    ({"call.stream.device_type": 1}, ERR_PROVIDER, "ROCm stream"),
+    ({"args.3.scalar": 5}, ERR_ARG, "unsupported GGML type"),
+    ({"args.3.scalar": (1 << 32) | 12}, ERR_ARG, "noncanonical"),
+    ({"args.3.kind": 1}, ERR_ARG, "type: wrong argument kind"),
+    ({"args.0.dtype": 11}, ERR_ARG, "x: wrong argument kind or dtype"),
+    ({"args.0.buffer.byte_size": 4}, ERR_ARG, "x: insufficient buffer storage"),
+    ({"args.0.buffer.address": 0x10008}, ERR_ARG, "x: invalid buffer descriptor"),
+    ({"args.1.buffer.device_type": 2}, ERR_ARG, "w: invalid buffer descriptor"),
+    ({"args.1.buffer.device_ordinal": 1}, ERR_ARG, "w: invalid buffer descriptor"),
+    ({"args.2.buffer.rank": 3}, ERR_ARG, "out: invalid buffer descriptor"),
+    ({"args.2.kind": 2}, ERR_ARG, "out: wrong argument kind"),
+])
+def test_malformed_calls_are_rejected(mutation, code, needle):
+    status, message = tamper(**mutation).run()
+    assert status == code, message
+    assert needle in message
+    assert len(message) < 507  # NUL-terminated, overwritten
+
+
+def test_stride_and_shape_mismatches():
+    call = Call()
+    call.keep[1][1] = 8  # x element stride of 8 bytes
+    assert call.run() == (ERR_ARG, "x: shape, stride or size mismatch")
+    call = Call(n=64, k=512)
+    call.keep[2][1] = 144 * 3  # w rows hold 3 super-blocks but K needs 2
+    call.args[1].buffer.byte_size = 64 * 144 * 3
+    call.keep[3][0] = 144 * 3
+    assert call.run()[0] == ERR_ARG
+    call = Call(m=2, n=64)
+    call.keep[4][0] = 3  # out rows != M
+    call.args[2].buffer.byte_size = 3 * 64 * 2
+    assert call.run() == (ERR_ARG, "out: shape, stride or size mismatch")
+
+
+def test_k_must_be_whole_blocks():
+    call = Call(k=512)
+    call.keep[0][1] = 300
+    call.keep[1][0] = 600
+    call.args[0].buffer.byte_size = 600
+    assert call.run()[0] == ERR_ARG
+
+
+def test_gemv_row_limit_but_gemm_accepts():
+    status, message = Call(m=9).run("tensor_gguf_gemv_v1")
+    assert status == ERR_ARG and "at most 8" in message
+
+
+def test_null_call():
+    error = abi.ErrorDescriptor()
+    assert _native.kernel("tensor_gguf_gemv_v1")(None, c.byref(error)) == ERR_ABI
+    assert _native.kernel("tensor_gguf_dequant_v1")(None, None) == ERR_ABI
+
+
+def test_dequant_argument_checks():
+    call = Call()
+    args = (abi.Argument * 3)(call.args[1], call.args[2], call.args[3])
+    call.call.arguments = args
+    call.call.argument_count = 3
+    # out [1, 64] does not match w [64, 288] -> rejected
+    status, message = call.run("tensor_gguf_dequant_v1")
+    assert status == ERR_ARG and "out" in message
+
+
+# --------------------------------------------------------- manifest binding --
+
+def fake(shape, dtype):
+    return SimpleNamespace(shape=tuple(shape), dtype=np.dtype(dtype))
+
+
+@pytest.mark.parametrize("encoding,qk,block", [("q4_k", 256, 144), ("q6_k", 256, 210), ("q8_0", 32, 34), ("q4_0", 32, 18)])
+def test_manifest_binds_gguf_shapes(encoding, qk, block):
+    manifest = kernels.manifest("gguf_linear", encoding)
+    x, w, out = fake((4, 4096), "float16"), fake((128, 4096 // qk * block), "uint8"), fake((4, 128), "float16")
+    symbols, values = bind_shapes(manifest, {"x": x, "w": w, "out": out})
+    assert symbols == {"M": 4, "K": 4096, "N": 128}
+    with pytest.raises(ValueError):
+        bind_shapes(manifest, {"x": x, "w": fake((128, 4096 // qk * block + block), "uint8"), "out": out})
+    with pytest.raises(ValueError):
+        bind_shapes(manifest, {"x": fake((4, qk + qk // 2), "float16"), "w": fake((128, block), "uint8"),
+                               "out": out})
+    assert manifest["constants"]["type"] == Q_TYPES[encoding]
+
+
+Q_TYPES = {"q4_0": 2, "q8_0": 8, "q4_k": 12, "q6_k": 14}
+
+
+def test_gemv_manifest_domain():
+    manifest = kernels.manifest("gguf_gemv", "q4_k", out_dtype="float32")
+    bind_shapes(manifest, {"x": fake((8, 256), "float16"), "w": fake((2, 144), "uint8"), "out": fake((8, 2), "float32")})
+    with pytest.raises(ValueError, match="outside"):
+        bind_shapes(manifest, {"x": fake((9, 256), "float16"), "w": fake((2, 144), "uint8"),
+                               "out": fake((9, 2), "float32")})
+
+
+def test_bound_call_carries_constant_type_scalar():
+    manifest = kernels.manifest("gguf_linear", "q6_k")
+    device = SimpleNamespace(stream_descriptor=lambda: abi.StreamDescriptor(10, 0, 0))
+    buffers = {}
+    for name, shape, dtype in (("x", (1, 256), "float16"), ("w", (3, 210), "uint8"), ("out", (1, 3), "float16")):
+        b = SimpleNamespace(shape=shape, dtype=np.dtype(dtype))
+        b._descriptor = abi.BufferDescriptor(0x1000, 0, None, None, 2, abi.DTYPES[dtype], 10, 0)
+        buffers[name] = b
+    symbols, values = bind_shapes(manifest, buffers)
+    launch = {"grid": [1, 1, 1], "block": [256, 1, 1], "shared_memory_bytes": 0}
+    call = abi.BoundCall(device, manifest, values, symbols, launch, validated=True)
+    assert [a.kind for a in call.arguments] == [1, 1, 1, 2]
+    assert call.arguments[3].dtype == abi.DTYPES["uint32"] and call.arguments[3].scalar == 14
+    assert call.descriptor.stream.device_type == 10
+
+
+def test_unknown_kernel_and_encoding():
+    with pytest.raises(ValueError):
+        kernels.manifest("gguf_conv", "q4_k")
+    with pytest.raises(ValueError):
+        kernels.manifest("gguf_linear", "q5_k")
+    with pytest.raises(ValueError):
+        kernels.manifest("gguf_linear", "q4_k", out_dtype="bfloat16")
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_native.NativeLibraryError, match="not built"):
+        _native.library(tmp_path / "libtensor_hip.so")

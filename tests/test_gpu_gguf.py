@@ -1,0 +1,201 @@
+"""GPU parity of the HIP GGUF kernels against the CPU oracle, through the C ABI.
+
+Every call goes Device.load -> Executable -> BoundCall -> TensorCallV1 ->
+libtensor_hip.so.  Bars (BASELINE): dequantized weights bit-exact; GEMV and
+GEMM outputs within relative L2 <= 2e-3 of the oracle (decode: fp32 operands,
+benchmark.py:466-472; prefill: fp16-rounded operands, benchmark.py:473-477).
+Input families follow the reference's qualification (benchmark.py:499-555):
+random, the same input scaled by -1.5, zeros, outputs pre-filled with NaN, and
+one captured graph replayed after its inputs change.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import gguf_ref as R
+from tensor_amd.gguf import quant as Q
+from tests import gguf_cases as cases
+
+pytestmark = pytest.mark.gpu
+
+TOLERANCE = 2e-3  # relative L2
+ENCODINGS = ("q4_k", "q6_k", "q8_0", "q4_0")
+
+
+def note(*parts):
+    print("[case]", *parts, flush=True)
+
+
+def run_linear(device, kernel, encoding, x, raw, out_dtype):
+    exe = device.load(kernel, encoding=encoding, out_dtype=out_dtype)
+    xb, wb = device.from_numpy(x), device.from_numpy(raw)
+    out = device.empty((x.shape[0], raw.shape[0]), out_dtype)
+    device.fill_bytes(out, 0xFF)  # NaN in both fp16 and fp32
+    exe.launch(xb, wb, out)
+    result = out.to_numpy()
+    for b in (xb, wb, out):
+        b.release()
+    return result
+
+
+# ---------------------------------------------------------------- dequant --
+
+@pytest.mark.parametrize("encoding", ENCODINGS)
+@pytest.mark.parametrize("source", ["quantized", "random_bits"])
+def test_dequant_bit_exact(hip_device, c_oracle, encoding, source):
+    code = Q.ggml_type(encoding)
+    n, k = 96, 3 * 256  # three super-blocks per row: odd Q6_K block alignment
+    note("dequant", encoding, source, n, k)
+    raw = cases.weight(n, k, encoding, 11) if source == "quantized" else cases.random_blocks(encoding, n, k, 12)
+    expected = c_oracle.dequantize(raw, code, n, k)
+    wb = hip_device.from_numpy(raw)
+    for dtype in ("float32", "float16"):
+        exe = hip_device.load("gguf_dequant", encoding=encoding, out_dtype=dtype)
+        out = hip_device.empty((n, k), dtype)
+        hip_device.fill_bytes(out, 0xFF)
+        exe.launch(wb, out)
+        got = out.to_numpy()
+        want = expected if dtype == "float32" else expected.astype(np.float16)
+        view = np.uint32 if dtype == "float32" else np.uint16
+        assert np.array_equal(got.view(view), want.view(view)), f"{encoding} {dtype}"
+        out.release()
+    wb.release()
+
+
+def test_dequant_fp16_subnormals(hip_device, c_oracle):
+    """Tiny scales push decoded values into fp16's subnormal range; RNE must keep them."""
+    n, k = 32, 512
+    raw = cases.random_blocks("q4_k", n, k, 13, scale=2e-6)
+    expected = c_oracle.dequantize(raw, Q.Q4_K, n, k).astype(np.float16)
+    assert np.any((expected != 0) & (np.abs(expected) < np.float16(6.1e-5)))
+    exe = hip_device.load("gguf_dequant", encoding="q4_k", out_dtype="float16")
+    wb = hip_device.from_numpy(raw)
+    out = exe(wb, K=k)
+    assert np.array_equal(out.to_numpy().view(np.uint16), expected.view(np.uint16))
+    out.release()
+    wb.release()
+
+
+# ------------------------------------------------------------------- GEMV --
+
+@pytest.mark.parametrize("encoding", ENCODINGS)
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
+def test_gemv_parity_small(hip_device, encoding, m):
+    code = Q.ggml_type(encoding)
+    n, k = 301, 2048 + 512  # ragged row count, K not a multiple of a full lane step
+    note("gemv", encoding, m, n, k)
+    raw = cases.weight(n, k, encoding, 20 + m)
+    x = cases.activation(m, k, 30 + m)
+    expected = R.gemv_reference(x, raw, code, n, k)
+    for out_dtype in ("float32", "float16"):
+        got = run_linear(hip_device, "gguf_gemv", encoding, x, raw, out_dtype)
+        assert not np.isnan(got).any()
+        err = R.relative_l2(got, expected)
+        assert err <= TOLERANCE, (encoding, m, out_dtype, err)
+        if out_dtype == "float32":
+            assert err <= 2e-4, (encoding, m, err)
+
+
+@pytest.mark.parametrize("encoding,n,k,m,out_dtype", [
+    ("q4_k", 12288, 4096, 1, "float16"),   # C2 gate/up
+    ("q4_k", 4096, 12288, 1, "float16"),   # C2 down
+    ("q4_k", 12288, 4096, 4, "float16"),
+    ("q4_k", 4096, 12288, 8, "float16"),
+    ("q6_k", 151936, 4096, 1, "float32"),  # C3 LM head, fp32 logits
+    ("q6_k", 4096, 12288, 1, "float16"),   # C5 down (Q6_K)
+    ("q8_0", 4096, 4096, 1, "float16"),    # C1 shape
+])
+def test_gemv_parity_baseline_shapes(hip_device, c_oracle, encoding, n, k, m, out_dtype):
+    code = Q.ggml_type(encoding)
+    note("gemv-full", encoding, n, k, m, out_dtype)
+    raw = cases.weight(n, k, encoding, 40)
+    x = cases.activation(m, k, 41)
+    c_oracle.set_threads(16)
+    expected = c_oracle.linear(x, raw, code, n, k)
+    got = run_linear(hip_device, "gguf_gemv", encoding, x, raw, out_dtype)
+    assert R.relative_l2(got, expected) <= TOLERANCE
+
+
+@pytest.mark.parametrize("encoding", ["q4_k", "q6_k"])
+def test_gemv_input_families_and_graph_replay(hip_device, encoding):
+    """One captured graph, replayed after x changes: random, x*-1.5, zeros."""
+    code = Q.ggml_type(encoding)
+    n, k, m = 1024, 4096, 1
+    note("gemv-graph", encoding)
+    raw = cases.weight(n, k, encoding, 50)
+    x = cases.activation(m, k, 51)
+    exe = hip_device.load("gguf_gemv", encoding=encoding, out_dtype="float32")
+    xb, wb = hip_device.from_numpy(x), hip_device.from_numpy(raw)
+    out = hip_device.empty((m, n), "float32")
+    call = exe.bind(xb, wb, out)
+    graph = hip_device.graph(call.launch)
+    try:
+        for family, xs in (("random", x), ("fresh_scaled", (x.astype(np.float32) * -1.5).astype(np.float16)),
+                           ("zero", np.zeros_like(x))):
+            hip_device.upload(xb, xs)
+            hip_device.fill_bytes(out, 0xFF)
+            graph.replay()
+            got = out.to_numpy()
+            expected = R.gemv_reference(xs, raw, code, n, k)
+            if family == "zero":
+                assert np.array_equal(got, np.zeros_like(got)), family
+            else:
+                assert R.relative_l2(got, expected) <= TOLERANCE, family
+    finally:
+        graph.close()
+        for b in (xb, wb, out):
+            b.release()
+
+
+def test_linear_dispatch_matches_both_kernels(hip_device):
+    n, k = 256, 1024
+    raw = cases.weight(n, k, "q4_k", 60)
+    for m in (1, 8, 9, 64):
+        x = cases.activation(m, k, 61 + m)
+        got = run_linear(hip_device, "gguf_linear", "q4_k", x, raw, "float32")
+        expected = R.gemv_reference(x, raw, Q.Q4_K, n, k) if m <= 8 else R.gemm_reference(x, raw, Q.Q4_K, n, k)
+        assert R.relative_l2(got, expected) <= TOLERANCE, m
+
+
+# ------------------------------------------------------------------- GEMM --
+
+@pytest.mark.parametrize("encoding", ENCODINGS)
+@pytest.mark.parametrize("m", [1, 17, 128, 300])
+def test_gemm_parity_small(hip_device, encoding, m):
+    code = Q.ggml_type(encoding)
+    n, k = 384 + 64, 1024
+    note("gemm", encoding, m, n, k)
+    raw = cases.weight(n, k, encoding, 70 + m)
+    x = cases.activation(m, k, 80 + m)
+    expected = R.gemm_reference(x, raw, code, n, k)
+    for out_dtype in ("float32", "float16"):
+        got = run_linear(hip_device, "gguf_gemm", encoding, x, raw, out_dtype)
+        assert not np.isnan(got).any()
+        err = R.relative_l2(got, expected)
+        assert err <= TOLERANCE, (encoding, m, out_dtype, err)
+        if out_dtype == "float32":
+            assert err <= 1e-5, (encoding, m, err)
+
+
+@pytest.mark.parametrize("encoding,m,n,k", [
+    ("q4_k", 512, 12288, 4096),   # C4
+    ("q6_k", 256, 4096, 12288),   # C5 down at M=256
+])
+def test_gemm_parity_baseline_shapes(hip_device, c_oracle, encoding, m, n, k):
+    code = Q.ggml_type(encoding)
+    note("gemm-full", encoding, m, n, k)
+    raw = cases.weight(n, k, encoding, 90)
+    x = cases.activation(m, k, 91)
+    c_oracle.set_threads(16)
+    expected = c_oracle.linear(x, raw, code, n, k, prefill=True)
+    got = run_linear(hip_device, "gguf_gemm", encoding, x, raw, "float16")
+    assert R.relative_l2(got, expected) <= TOLERANCE
+
+
+def test_gemm_zero_input_gives_exact_zero(hip_device):
+    raw = cases.weight(128, 512, "q4_k", 95)
+    x = np.zeros((64, 512), np.float16)
+    got = run_linear(hip_device, "gguf_gemm", "q4_k", x, raw, "float32")
+    assert np.array_equal(got, np.zeros_like(got))

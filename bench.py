@@ -197,6 +197,10 @@ def main():
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-details", action="store_true", help="headline only")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
+    parser.add_argument("--calibrate", action="store_true",
+                        help="first run 5 device copies of 256 MiB (a known-size copy kernel for PMC scaling)")
+    parser.add_argument("--eager-only", action="store_true",
+                        help="stop after the eager warmup launches (for per-dispatch counter runs)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -211,6 +215,15 @@ def main():
     device = tx.Device(0, provider="hip")
     with device:
         log("device", device.info["name"], device.info["arch_features"], "CUs", device.info["compute_units"])
+        if args.calibrate:
+            source = device.zeros((256 << 20,), "uint8")
+            target = device.empty((256 << 20,), "uint8")
+            for _ in range(5):
+                target.copy_from(source)
+            device.synchronize()
+            source.release()
+            target.release()
+            log("calibration: 5 device copies of", 256 << 20, "bytes")
         # ---- headline: C2 Q4_K GEMV M=1, gate + up + down per step
         per_step_weights = 2 * weight_bytes("q4_k", 12288, 4096) + weight_bytes("q4_k", 4096, 12288)
         copies = copies_for(per_step_weights)
@@ -224,6 +237,10 @@ def main():
             launch()
         device.synchronize()
         log("warmup done", args.warmup, "steps")
+        if args.eager_only:
+            for layer in mlp:
+                layer.release()
+            return 0
         seconds = time_graph(device, rotated_launches(mlp, args.steps), replays=3)
         value = step_bytes * args.steps / seconds / 1e9
         log(f"headline {value:.1f} GB/s, {seconds / args.steps * 1e6:.2f} us/step")

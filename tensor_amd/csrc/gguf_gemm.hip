@@ -3,21 +3,32 @@
 // benchmarks/kernels/showcase/kernels.py:114-119; restated by the Triton
 // gguf kernel at triton_kernels.py:185-211).
 //
-// gfx950 design: a 256-thread workgroup owns a BM x BN output tile.  Per K
-// step it stages the fp16 activation tile and the weight tile, decoded from
-// raw GGUF blocks straight into LDS as fp16 (same arithmetic as the
-// dequantizer, so the staged weights are bit-exact fp16(dequant(W))), then
-// each wave runs v_mfma_f32_16x16x32_f16 over its sub-tile with fp32
-// accumulators held in registers.
+// gfx950 design.  A workgroup of WM x WN waves owns a BM x BN output tile and
+// walks K in steps of BK = 64 elements:
+//
+//   * The next step's activation tile and raw GGUF bytes are prefetched into
+//     registers while the current step's MFMAs run.
+//   * Weights are dequantized straight from those registers into fp16 LDS
+//     tiles with the reference's fp32 arithmetic (every product exact, one
+//     rounding), so the staged weights are bit-exact fp16(dequant(W)).
+//   * LDS tiles are double-buffered: one barrier per K step.  Rows are padded
+//     by 16 bytes so the b128 fragment reads of a wave spread over the banks.
+//   * Each wave computes a 64 x (16 NT) sub-tile with v_mfma_f32_16x16x32_f16
+//     (lane l supplies row/column l % 16 and k = 8 (l / 16) .. + 7; the 16 x 16
+//     result gives lane l rows 4 (l / 16) .. + 3 of column l % 16).
+//
+// Q4_K weights take a dedicated path (header and quant bytes prefetched, two
+// to four threads per weight row); the other encodings decode 8-element
+// groups with the shared per-element decoder.
 #include "gguf_decode.h"
 #include "gguf_launch.h"
 
 namespace tensor_gguf {
 
 namespace gemm {
-constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int LDS_STRIDE = BK + 8;  // halves; 16-byte skew between rows
-constexpr int THREADS = 256;
+constexpr int BK = 64;
+constexpr int PAD = 8;  // halves of padding per LDS row
+constexpr int LDS_ROW = BK + PAD;
 }  // namespace gemm
 
 __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
@@ -25,81 +36,153 @@ __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
 }
 
-// MFMA 16x16x32 fp16 operand layout (wave64): lane l supplies row/column
-// l % 16 and the 8 consecutive k values 8*(l/16) .. 8*(l/16)+7; the 16x16 fp32
-// result gives lane l rows 4*(l/16) .. +3 of column l % 16.
-template <int TYPE, typename OutT>
-__global__ __launch_bounds__(256) void gemm_kernel(const _Float16* __restrict__ x,
-                                                   const uint8_t* __restrict__ w,
-                                                   OutT* __restrict__ out, int M, int N, int K) {
+// Exact Q4_K dequantization of four codes held in the bytes of one dword
+// (each byte's nibble already isolated in its low four bits).
+__device__ __forceinline__ void q4k_dequant4(uint32_t codes, float ds, float dm, uint32_t& lo_pair, uint32_t& hi_pair) {
+  const float a = ds * (float)(codes & 0xFFu) - dm;
+  const float b = ds * (float)((codes >> 8) & 0xFFu) - dm;
+  const float c = ds * (float)((codes >> 16) & 0xFFu) - dm;
+  const float d = ds * (float)(codes >> 24) - dm;
+  lo_pair = pack_half2(a, b);
+  hi_pair = pack_half2(c, d);
+}
+
+template <int TYPE, int BM, int BN, int WM, int WN, typename OutT>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_v2(const _Float16* __restrict__ x,
+                                                        const uint8_t* __restrict__ w,
+                                                        OutT* __restrict__ out, int M, int N, int K) {
   using namespace gemm;
+  constexpr int THREADS = WM * WN * 64;
+  constexpr int NT = BN / WN / 16;             // 16-column MFMA tiles per wave
+  static_assert(BM / WM == 64, "each wave covers 64 rows of M");
+  static_assert(NT * 16 * WN == BN, "BN must split into 16-column tiles per wave");
   constexpr int QK = (TYPE == kQ4_K || TYPE == kQ6_K) ? 256 : 32;
   constexpr int BYTES = TYPE == kQ4_K ? 144 : TYPE == kQ6_K ? 210 : TYPE == kQ8_0 ? 34 : 18;
-  __shared__ __attribute__((aligned(16))) _Float16 xs[BM * LDS_STRIDE];
-  __shared__ __attribute__((aligned(16))) _Float16 ws[BN * LDS_STRIDE];
+  // activation tile: BM rows x BK halves = BM * 8 chunks of 16 bytes
+  constexpr int X_LOADS = BM * 8 / THREADS;
+  static_assert(X_LOADS * THREADS == BM * 8, "activation tile must split evenly");
+  // Q4_K: TPR threads per weight row, each owning 32 / TPR quant bytes of the step's pair
+  constexpr int TPR = THREADS / BN;
+  static_assert(TYPE != kQ4_K || (TPR * BN == THREADS && (TPR == 1 || TPR == 2 || TPR == 4)),
+                "Q4_K tiles need 1, 2 or 4 threads per weight row");
+  constexpr int QBYTES = TYPE == kQ4_K ? 32 / TPR : 16;
+  // generic decoder: BN rows x 8 groups of 8 elements
+  constexpr int G_LOADS = (BN * 8 + THREADS - 1) / THREADS;
+
+  __shared__ __attribute__((aligned(16))) _Float16 xs[2][BM * LDS_ROW];
+  __shared__ __attribute__((aligned(16))) _Float16 ws[2][BN * LDS_ROW];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave / WN) * 64, wn = (wave % WN) * (16 * NT);
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;  // 2 x 2 waves of 64 x 64
   const size_t row_bytes = (size_t)(K / QK) * BYTES;
+  const int steps = (K + BK - 1) / BK;
 
-  float4_t acc[4][4];
+  // ---- prefetch registers
+  uint4 xr[X_LOADS];
+  uint4 hd;                       // Q4_K header of this thread's weight row
+  uint32_t qw[QBYTES / 4];        // Q4_K quant bytes of this thread's slice
+  const int wrow = tid / (TYPE == kQ4_K ? TPR : 1), wpart = tid % (TYPE == kQ4_K ? TPR : 1);
+  const uint8_t* wbase = w + (size_t)min(n0 + wrow, N - 1) * row_bytes;
+
+  auto prefetch = [&](int step) {
+    const int k0 = step * BK;
+#pragma unroll
+    for (int i = 0; i < X_LOADS; ++i) {
+      const int c = i * THREADS + tid, r = c >> 3, c8 = (c & 7) * 8;
+      xr[i] = (m0 + r < M && k0 + c8 < K) ? *reinterpret_cast<const uint4*>(x + (size_t)(m0 + r) * K + k0 + c8)
+                                          : make_uint4(0, 0, 0, 0);
+    }
+    if (TYPE == kQ4_K && wrow < BN) {
+      const uint8_t* blk = wbase + (size_t)(k0 >> 8) * 144;
+      hd = load16(blk);
+      const uint8_t* q = blk + 16 + 32 * ((k0 >> 6) & 3) + QBYTES * wpart;
+#pragma unroll
+      for (int i = 0; i < QBYTES / 4; ++i) qw[i] = load4(q + 4 * i);
+    }
+  };
+
+  auto stage = [&](int step, int buf) {
+    const int k0 = step * BK;
+#pragma unroll
+    for (int i = 0; i < X_LOADS; ++i) {
+      const int c = i * THREADS + tid, r = c >> 3, c8 = (c & 7) * 8;
+      *reinterpret_cast<uint4*>(&xs[buf][r * LDS_ROW + c8]) = xr[i];
+    }
+    if (TYPE == kQ4_K) {
+      if (wrow < BN) {
+        // pair j = step % 4: low nibbles are sub-block 2j, high nibbles 2j+1
+        const int j = (k0 >> 6) & 3;
+        int sc_lo, mn_lo, sc_hi, mn_hi;
+        q4k_scale_pair(hd.y, hd.z, hd.w, j, sc_lo, mn_lo, sc_hi, mn_hi);
+        const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
+        const float ds_lo = d * (float)sc_lo, dm_lo = dmin * (float)mn_lo;
+        const float ds_hi = d * (float)sc_hi, dm_hi = dmin * (float)mn_hi;
+        _Float16* dst = &ws[buf][wrow * LDS_ROW + QBYTES * wpart];
+#pragma unroll
+        for (int i = 0; i < QBYTES / 4; ++i) {
+          uint32_t l0, l1, h0, h1;
+          q4k_dequant4(qw[i] & 0x0F0F0F0Fu, ds_lo, dm_lo, l0, l1);
+          q4k_dequant4((qw[i] >> 4) & 0x0F0F0F0Fu, ds_hi, dm_hi, h0, h1);
+          *reinterpret_cast<uint2*>(dst + 4 * i) = make_uint2(l0, l1);
+          *reinterpret_cast<uint2*>(dst + 32 + 4 * i) = make_uint2(h0, h1);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < G_LOADS; ++i) {
+        const int c = i * THREADS + tid;
+        if (c < BN * 8) {
+          const int r = c >> 3, c8 = (c & 7) * 8, kk = k0 + c8;
+          uint4 v = make_uint4(0, 0, 0, 0);  // a K tail shorter than BK reads as zeros
+          if (kk < K) {
+            const uint8_t* blk = w + (size_t)min(n0 + r, N - 1) * row_bytes + (size_t)(kk / QK) * BYTES;
+            float f[8];
+            decode8<TYPE>(blk, kk % QK, f);
+            v = make_uint4(pack_half2(f[0], f[1]), pack_half2(f[2], f[3]), pack_half2(f[4], f[5]),
+                           pack_half2(f[6], f[7]));
+          }
+          *reinterpret_cast<uint4*>(&ws[buf][r * LDS_ROW + c8]) = v;
+        }
+      }
+    }
+  };
+
+  float4_t acc[4][NT];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NT; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = 0; k0 < K; k0 += BK) {
-    // activation tile: BM rows x BK halves, 16 B per thread-iteration
-#pragma unroll
-    for (int it = 0; it < (BM * BK / 8) / THREADS; ++it) {
-      const int idx = it * THREADS + tid;
-      const int r = idx / (BK / 8), c8 = (idx % (BK / 8)) * 8;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (m0 + r < M && k0 + c8 < K)
-        v = *reinterpret_cast<const uint4*>(x + (size_t)(m0 + r) * K + k0 + c8);
-      *reinterpret_cast<uint4*>(&xs[r * LDS_STRIDE + c8]) = v;
-    }
-    // weight tile: BN rows x BK elements decoded to fp16
-#pragma unroll
-    for (int it = 0; it < (BN * BK / 8) / THREADS; ++it) {
-      const int idx = it * THREADS + tid;
-      const int r = idx / (BK / 8), c8 = (idx % (BK / 8)) * 8;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      const int kk = k0 + c8;
-      if (n0 + r < N && kk < K) {
-        const uint8_t* block = w + (size_t)(n0 + r) * row_bytes + (size_t)(kk / QK) * BYTES;
-        float f[8];
-        decode8<TYPE>(block, kk % QK, f);
-        v = make_uint4(pack_half2(f[0], f[1]), pack_half2(f[2], f[3]), pack_half2(f[4], f[5]),
-                       pack_half2(f[6], f[7]));
-      }
-      *reinterpret_cast<uint4*>(&ws[r * LDS_STRIDE + c8]) = v;
-    }
-    __syncthreads();
+  prefetch(0);
+  stage(0, 0);
+  __syncthreads();
+  for (int step = 0; step < steps; ++step) {
+    const int buf = step & 1;
+    if (step + 1 < steps) prefetch(step + 1);
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 32) {
-      half8_t a[4], b[4];
       const int koff = kk + 8 * (lane >> 4);
+      half8_t a[4], b[NT];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        a[i] = *reinterpret_cast<const half8_t*>(&xs[(wm + 16 * i + (lane & 15)) * LDS_STRIDE + koff]);
+        a[i] = *reinterpret_cast<const half8_t*>(&xs[buf][(wm + 16 * i + (lane & 15)) * LDS_ROW + koff]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        b[j] = *reinterpret_cast<const half8_t*>(&ws[(wn + 16 * j + (lane & 15)) * LDS_STRIDE + koff]);
+      for (int j = 0; j < NT; ++j)
+        b[j] = *reinterpret_cast<const half8_t*>(&ws[buf][(wn + 16 * j + (lane & 15)) * LDS_ROW + koff]);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NT; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
+    if (step + 1 < steps) stage(step + 1, buf ^ 1);
     __syncthreads();
   }
-  // D layout: lane holds rows 4*(lane/16)+e of column lane%16 of each 16x16 tile
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NT; ++j) {
       const int col = n0 + wn + 16 * j + (lane & 15);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -109,30 +192,31 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16* __restrict__ 
     }
 }
 
+template <int TYPE, int BM, int BN, int WM, int WN, typename OutT>
+static hipError_t launch_tile(const GemvArgs& a, hipStream_t stream) {
+  const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM), block(WM * WN * 64);
+  hipLaunchKernelGGL((gemm_v2<TYPE, BM, BN, WM, WN, OutT>), grid, block, 0, stream,
+                     static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w),
+                     static_cast<OutT*>(a.out), a.m, a.n, a.k);
+  return hipGetLastError();
+}
+
+template <int TYPE, typename OutT>
+static hipError_t launch_type(const GemvArgs& a, hipStream_t stream) {
+  // 128 x 128 tiles; 256 x 128 once M is large enough to fill the chip with them
+  if (a.m >= 1024) return launch_tile<TYPE, 256, 128, 4, 2, OutT>(a, stream);
+  return launch_tile<TYPE, 128, 128, 2, 2, OutT>(a, stream);
+}
+
 template <typename OutT>
 static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream) {
-  using namespace gemm;
-  const _Float16* x = static_cast<const _Float16*>(a.x);
-  const uint8_t* w = static_cast<const uint8_t*>(a.w);
-  OutT* out = static_cast<OutT*>(a.out);
-  const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM), block(THREADS);
   switch (a.type) {
-    case kQ4_K:
-      hipLaunchKernelGGL((gemm_kernel<kQ4_K, OutT>), grid, block, 0, stream, x, w, out, a.m, a.n, a.k);
-      break;
-    case kQ6_K:
-      hipLaunchKernelGGL((gemm_kernel<kQ6_K, OutT>), grid, block, 0, stream, x, w, out, a.m, a.n, a.k);
-      break;
-    case kQ8_0:
-      hipLaunchKernelGGL((gemm_kernel<kQ8_0, OutT>), grid, block, 0, stream, x, w, out, a.m, a.n, a.k);
-      break;
-    case kQ4_0:
-      hipLaunchKernelGGL((gemm_kernel<kQ4_0, OutT>), grid, block, 0, stream, x, w, out, a.m, a.n, a.k);
-      break;
-    default:
-      return hipErrorInvalidValue;
+    case kQ4_K: return launch_type<kQ4_K, OutT>(a, stream);
+    case kQ6_K: return launch_type<kQ6_K, OutT>(a, stream);
+    case kQ8_0: return launch_type<kQ8_0, OutT>(a, stream);
+    case kQ4_0: return launch_type<kQ4_0, OutT>(a, stream);
+    default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 hipError_t launch_gemm(const GemvArgs& a, hipStream_t stream) {

@@ -28,6 +28,9 @@ struct DequantArgs {
 constexpr int kGemvMaxM = 8;
 
 hipError_t launch_gemv(const GemvArgs& args, hipStream_t stream);
+// Q4_K fast paths (LDS dot2 kernel for M = 1, MFMA kernel for M >= 2); sets
+// *handled to false when the shape is not covered by them.
+hipError_t launch_gemv_q4k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 hipError_t launch_dequant(const DequantArgs& args, hipStream_t stream);
 hipError_t launch_gemm(const GemvArgs& args, hipStream_t stream);
 

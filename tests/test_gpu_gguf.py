@@ -81,10 +81,11 @@ def test_dequant_fp16_subnormals(hip_device, c_oracle):
 # ------------------------------------------------------------------- GEMV --
 
 @pytest.mark.parametrize("encoding", ENCODINGS)
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
-def test_gemv_parity_small(hip_device, encoding, m):
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("k", [2560, 8192])
+def test_gemv_parity_small(hip_device, encoding, m, k):
     code = Q.ggml_type(encoding)
-    n, k = 301, 2048 + 512  # ragged row count, K not a multiple of a full lane step
+    n = 301  # ragged row count; K = 2560 is not a multiple of a full lane step
     note("gemv", encoding, m, n, k)
     raw = cases.weight(n, k, encoding, 20 + m)
     x = cases.activation(m, k, 30 + m)

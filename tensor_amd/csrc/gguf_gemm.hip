@@ -201,167 +201,11 @@ static hipError_t launch_tile(const GemvArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// ----------------------------------------------------- Q4_K, pipelined ---
-//
-// Q4_K specialisation of the same tile algorithm with a deeper pipeline:
-// two register sets of raw bytes (step s+1 being staged while step s+2 is in
-// flight), the LDS double buffer as two arrays so the compiler can overlap
-// the staging stores with the fragment reads of the other buffer, and the
-// step written as one straight-line region in which sched_group_barrier
-// interleaves each MFMA with dequant VALU work, LDS stores and global loads.
-
-namespace q4k_pipe {
-constexpr int BK = 64, ROW = 80;  // halves per LDS row (16-byte aligned, padded)
-
-template <int XL, int QB>
-struct Raw {
-  uint4 x[XL];
-  uint4 hd;
-  uint32_t q[QB / 4];
-};
-}  // namespace q4k_pipe
-
-template <int BM, int BN, int WM, int WN, typename OutT>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_q4k_pipe(const _Float16* __restrict__ x,
-                                                              const uint8_t* __restrict__ w,
-                                                              OutT* __restrict__ out, int M, int N, int K) {
-  using namespace q4k_pipe;
-  constexpr int THREADS = WM * WN * 64;
-  constexpr int MT = BM / WM / 16, NT = BN / WN / 16;
-  constexpr int XL = BM * 8 / THREADS;      // 16-byte activation chunks per thread per step
-  constexpr int TPR = THREADS / BN;         // threads per weight row
-  constexpr int QB = 32 / TPR;              // quant bytes per thread per step
-  static_assert(XL * THREADS == BM * 8 && TPR * BN == THREADS && (TPR == 1 || TPR == 2 || TPR == 4), "tile shape");
-  using RawT = Raw<XL, QB>;
-  __shared__ __attribute__((aligned(16))) _Float16 xs0[BM * ROW], xs1[BM * ROW];
-  __shared__ __attribute__((aligned(16))) _Float16 ws0[BN * ROW], ws1[BN * ROW];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = (wave / WN) * (16 * MT), wn = (wave % WN) * (16 * NT);
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int wrow = tid / TPR, wpart = tid % TPR;
-  const uint8_t* wbase = w + (size_t)min(n0 + wrow, N - 1) * (size_t)(K >> 8) * 144;
-  const int steps = K / BK;  // a multiple of 4: K is whole super-blocks
-
-  auto load = [&](RawT& r, int step) {
-    const int k0 = step * BK;
-#pragma unroll
-    for (int i = 0; i < XL; ++i) {
-      const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
-      r.x[i] = (m0 + row < M) ? *reinterpret_cast<const uint4*>(x + (size_t)(m0 + row) * K + k0 + c8)
-                              : make_uint4(0, 0, 0, 0);
-    }
-    const uint8_t* blk = wbase + (size_t)(k0 >> 8) * 144;
-    r.hd = load16(blk);
-    const uint8_t* q = blk + 16 + 32 * ((k0 >> 6) & 3) + QB * wpart;
-#pragma unroll
-    for (int i = 0; i < QB / 4; ++i) r.q[i] = load4(q + 4 * i);
-  };
-
-  auto store = [&](const RawT& r, _Float16* xs, _Float16* ws, int step) {
-#pragma unroll
-    for (int i = 0; i < XL; ++i) {
-      const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
-      *reinterpret_cast<uint4*>(&xs[row * ROW + c8]) = r.x[i];
-    }
-    // pair j = step % 4: low nibbles are sub-block 2j, high nibbles 2j+1
-    int sc_lo, mn_lo, sc_hi, mn_hi;
-    q4k_scale_pair(r.hd.y, r.hd.z, r.hd.w, step & 3, sc_lo, mn_lo, sc_hi, mn_hi);
-    const float d = half_bits_to_float(r.hd.x), dmin = half_bits_to_float(r.hd.x >> 16);
-    const float ds_lo = d * (float)sc_lo, dm_lo = dmin * (float)mn_lo;
-    const float ds_hi = d * (float)sc_hi, dm_hi = dmin * (float)mn_hi;
-    _Float16* dst = &ws[wrow * ROW + QB * wpart];
-#pragma unroll
-    for (int i = 0; i < QB / 4; ++i) {
-      uint32_t l0, l1, h0, h1;
-      q4k_dequant4(r.q[i] & 0x0F0F0F0Fu, ds_lo, dm_lo, l0, l1);
-      q4k_dequant4((r.q[i] >> 4) & 0x0F0F0F0Fu, ds_hi, dm_hi, h0, h1);
-      *reinterpret_cast<uint2*>(dst + 4 * i) = make_uint2(l0, l1);
-      *reinterpret_cast<uint2*>(dst + 32 + 4 * i) = make_uint2(h0, h1);
-    }
-  };
-
-  float4_t acc[MT][NT];
-#pragma unroll
-  for (int i = 0; i < MT; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-  // one K step: fragment reads of (xs, ws), then MFMAs interleaved with the
-  // staging of `staged` into (xn, wnext) and the prefetch of `fetch_step`
-  auto step_body = [&](const _Float16* xs, const _Float16* ws, _Float16* xn, _Float16* wnext, const RawT& staged,
-                       int staged_step, RawT& fetched, int fetch_step) {
-    half8_t a[2][MT], b[2][NT];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int koff = 32 * kk + 8 * (lane >> 4);
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-        a[kk][i] = *reinterpret_cast<const half8_t*>(&xs[(wm + 16 * i + (lane & 15)) * ROW + koff]);
-#pragma unroll
-      for (int j = 0; j < NT; ++j)
-        b[kk][j] = *reinterpret_cast<const half8_t*>(&ws[(wn + 16 * j + (lane & 15)) * ROW + koff]);
-    }
-    store(staged, xn, wnext, staged_step);
-    load(fetched, fetch_step);
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < NT; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[kk][i], b[kk][j], acc[i][j], 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 2 * MT * NT; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two VALU
-      if (i % 4 == 0) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // an LDS store
-      if (i % 4 == 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a global load
-    }
-  };
-
-  RawT ra, rb;
-  load(ra, 0);
-  load(rb, 1);
-  store(ra, xs0, ws0, 0);
-  __syncthreads();
-  for (int step = 0; step < steps; step += 2) {
-    // even step: compute buffer 0, stage step+1 into buffer 1, fetch step+2
-    step_body(xs0, ws0, xs1, ws1, rb, step + 1, ra, min(step + 2, steps - 1));
-    __syncthreads();
-    // odd step: compute buffer 1, stage step+2 into buffer 0, fetch step+3
-    // (past the end the staged and fetched data are clamped copies, never read)
-    step_body(xs1, ws1, xs0, ws0, ra, min(step + 2, steps - 1), rb, min(step + 3, steps - 1));
-    __syncthreads();
-  }
-#pragma unroll
-  for (int i = 0; i < MT; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int col = n0 + wn + 16 * j + (lane & 15);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = m0 + wm + 16 * i + 4 * (lane >> 4) + e;
-        if (row < M && col < N) store_out<OutT>(out, (size_t)row * N + col, acc[i][j][e]);
-      }
-    }
-}
-
-template <int BM, int BN, int WM, int WN, typename OutT>
-static hipError_t launch_q4k_pipe(const GemvArgs& a, hipStream_t stream) {
-  const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM), block(WM * WN * 64);
-  hipLaunchKernelGGL((gemm_q4k_pipe<BM, BN, WM, WN, OutT>), grid, block, 0, stream,
-                     static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w),
-                     static_cast<OutT*>(a.out), a.m, a.n, a.k);
-  return hipGetLastError();
-}
-
 template <int TYPE, typename OutT>
 static hipError_t launch_type(const GemvArgs& a, hipStream_t stream) {
-  if (TYPE == kQ4_K) {
-    if (a.m > 128) return launch_q4k_pipe<256, 128, 4, 2, OutT>(a, stream);
-    return launch_q4k_pipe<128, 128, 2, 2, OutT>(a, stream);
-  }
+  bool handled = false;
+  const hipError_t status = launch_gemm_pipe(a, stream, &handled);
+  if (handled) return status;
   // 128 x 128 tiles; 256 x 128 once M is large enough to fill the chip with them
   if (a.m >= 1024) return launch_tile<TYPE, 256, 128, 4, 2, OutT>(a, stream);
   return launch_tile<TYPE, 128, 128, 2, 2, OutT>(a, stream);

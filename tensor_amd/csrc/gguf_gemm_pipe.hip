@@ -1,0 +1,261 @@
+// Pipelined fused dequant-GEMM for the K-quants (Q4_K, Q6_K) on gfx950:
+// out[m, n] = sum_k fp16(x[m, k]) * fp16(W[n, k]), fp32 accumulation
+// (reference kernel: AKAS _packed, benchmarks/kernels/showcase/kernels.py:114-119;
+//  Triton restatement triton_kernels.py:185-211).
+//
+// Same tile algorithm as the generic kernel in gguf_gemm.hip (BM x BN
+// workgroup tile, BK = 64 steps, LDS-staged fp16 tiles, 16x16x32 fp16 MFMA
+// with fp32 accumulators) with a deeper software pipeline:
+//
+//   * two register sets of raw bytes: step s+1 is dequantized into LDS while
+//     step s+2 is in flight from HBM and step s is multiplied;
+//   * the LDS double buffer as two arrays, so the compiler may overlap the
+//     staging stores of one buffer with the fragment reads of the other;
+//   * each step is one straight-line region in which sched_group_barrier
+//     interleaves every MFMA with dequant VALU work, an LDS store or a global
+//     load, keeping the matrix pipe fed while the VALU decodes.
+//
+// Weights are dequantized with the reference's fp32 arithmetic (every product
+// exact, one rounding) and converted to fp16 with round-to-nearest-even, so
+// the staged tiles are bit-exact fp16(dequant(W)).
+//   Q4_K (triton_kernels.py:143-162): a step is one 32-byte quant pair j of a
+//     super-block, 64 codes: low nibbles = sub-block 2j, high = 2j+1.
+//   Q6_K (triton_kernels.py:163-180): a step covers quarters 2(s%2), 2(s%2)+1
+//     of half h = (s%4)/2: the 64 low-nibble bytes of ql for that half (nibble
+//     s%2), the 32 qh bytes of the half (2 bits per quarter) and 4 scales.
+#include "gguf_common.h"
+#include "gguf_launch.h"
+
+namespace tensor_gguf {
+namespace pipe {
+
+constexpr int BK = 64, ROW = 80;  // halves per LDS row (16-byte aligned, padded)
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+  return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+
+// fp16 pairs of scale * code + bias for the four byte codes of `codes`.
+__device__ __forceinline__ uint2 affine4(uint32_t codes, float scale, float bias) {
+  return make_uint2(pack2(fmaf(scale, (float)(codes & 0xFFu), bias), fmaf(scale, (float)((codes >> 8) & 0xFFu), bias)),
+                    pack2(fmaf(scale, (float)((codes >> 16) & 0xFFu), bias), fmaf(scale, (float)(codes >> 24), bias)));
+}
+
+template <int TYPE, int TPR>
+struct Geometry;
+
+// Q4_K: TPR threads per weight row share the 32 quant bytes of the step's pair.
+template <int TPR>
+struct Geometry<kQ4_K, TPR> {
+  static constexpr int QB = 32 / TPR;  // quant bytes per thread
+  static constexpr int W0 = QB / 4, W1 = 4;  // dwords: quants, header
+};
+
+// Q6_K: TPR threads per weight row, each EPT = 64 / TPR consecutive elements.
+template <int TPR>
+struct Geometry<kQ6_K, TPR> {
+  static constexpr int EPT = 64 / TPR;
+  static constexpr int W0 = EPT / 4, W1 = EPT / 4 + 2;  // ql dwords; qh dwords + scales + d
+};
+
+template <int XL, int W0, int W1>
+struct Raw {
+  uint4 x[XL];
+  uint32_t a[W0];
+  uint32_t b[W1];
+};
+
+}  // namespace pipe
+
+template <int TYPE, int BM, int BN, int WM, int WN, typename OutT>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_pipe(const _Float16* __restrict__ x,
+                                                          const uint8_t* __restrict__ w,
+                                                          OutT* __restrict__ out, int M, int N, int K) {
+  using namespace pipe;
+  constexpr int THREADS = WM * WN * 64;
+  constexpr int MT = BM / WM / 16, NT = BN / WN / 16;
+  constexpr int XL = BM * 8 / THREADS;  // 16-byte activation chunks per thread per step
+  constexpr int TPR = THREADS / BN;     // threads per weight row
+  static_assert(XL * THREADS == BM * 8 && TPR * BN == THREADS && (TPR == 1 || TPR == 2 || TPR == 4), "tile shape");
+  using G = Geometry<TYPE, TPR>;
+  using RawT = Raw<XL, G::W0, G::W1>;
+  constexpr int BYTES = TYPE == kQ4_K ? 144 : 210;
+  __shared__ __attribute__((aligned(16))) _Float16 xs0[BM * ROW], xs1[BM * ROW];
+  __shared__ __attribute__((aligned(16))) _Float16 ws0[BN * ROW], ws1[BN * ROW];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave / WN) * (16 * MT), wn = (wave % WN) * (16 * NT);
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int wrow = tid / TPR, wpart = tid % TPR;
+  const uint8_t* wbase = w + (size_t)min(n0 + wrow, N - 1) * (size_t)(K >> 8) * BYTES;
+  const int steps = K / BK;  // a multiple of 4: K is whole super-blocks
+
+  auto load = [&](RawT& r, int step) {
+    const int k0 = step * BK;
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
+      r.x[i] = (m0 + row < M) ? *reinterpret_cast<const uint4*>(x + (size_t)(m0 + row) * K + k0 + c8)
+                              : make_uint4(0, 0, 0, 0);
+    }
+    const uint8_t* blk = wbase + (size_t)(k0 >> 8) * BYTES;
+    if constexpr (TYPE == kQ4_K) {
+      const uint4 hd = load16(blk);
+      r.b[0] = hd.x; r.b[1] = hd.y; r.b[2] = hd.z; r.b[3] = hd.w;
+      const uint8_t* q = blk + 16 + 32 * (step & 3) + G::QB * wpart;
+#pragma unroll
+      for (int i = 0; i < G::W0; ++i) r.a[i] = load4(q + 4 * i);
+    } else {
+      const int h = (step & 3) >> 1, e0 = G::EPT * wpart;  // element offset inside the step
+      const int quarter = 2 * (step & 1) + (e0 >> 5), l0 = e0 & 31;
+      const uint8_t* ql = blk + 64 * h + e0;
+      const uint8_t* qh = blk + 128 + 32 * h + l0;
+#pragma unroll
+      for (int i = 0; i < G::W0; ++i) {
+        r.a[i] = load4(ql + 4 * i);
+        r.b[i] = load4(qh + 4 * i);
+      }
+      r.b[G::W0] = load4(blk + 192 + 8 * h + 2 * quarter);  // scales 2q .. 2q+3 of this half
+      r.b[G::W0 + 1] = load4(blk + 206);                    // high half: d
+    }
+  };
+
+  auto store = [&](const RawT& r, _Float16* xs, _Float16* ws, int step) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
+      *reinterpret_cast<uint4*>(&xs[row * ROW + c8]) = r.x[i];
+    }
+    if constexpr (TYPE == kQ4_K) {
+      int sc_lo, mn_lo, sc_hi, mn_hi;
+      q4k_scale_pair(r.b[1], r.b[2], r.b[3], step & 3, sc_lo, mn_lo, sc_hi, mn_hi);
+      const float d = half_bits_to_float(r.b[0]), dmin = half_bits_to_float(r.b[0] >> 16);
+      // d*sc*q - dmin*m: the product is exact, the subtraction rounds once
+      const float ds_lo = d * (float)sc_lo, dm_lo = -(dmin * (float)mn_lo);
+      const float ds_hi = d * (float)sc_hi, dm_hi = -(dmin * (float)mn_hi);
+      _Float16* dst = &ws[wrow * ROW + G::QB * wpart];
+#pragma unroll
+      for (int i = 0; i < G::W0; ++i) {
+        *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(r.a[i] & 0x0F0F0F0Fu, ds_lo, dm_lo);
+        *reinterpret_cast<uint2*>(dst + 32 + 4 * i) = affine4((r.a[i] >> 4) & 0x0F0F0F0Fu, ds_hi, dm_hi);
+      }
+    } else {
+      const int e0 = G::EPT * wpart;
+      const int quarter = 2 * (step & 1) + (e0 >> 5), l0 = e0 & 31;
+      const float d = half_bits_to_float(r.b[G::W0 + 1] >> 16);
+      _Float16* dst = &ws[wrow * ROW + e0];
+#pragma unroll
+      for (int i = 0; i < G::W0; ++i) {
+        // 6-bit codes of elements l0 + 4i .. + 3 of this quarter
+        const uint32_t lo = (r.a[i] >> (4 * (step & 1))) & 0x0F0F0F0Fu;
+        const uint32_t hi = ((r.b[i] >> (2 * quarter)) & 0x03030303u) << 4;
+        // scale index 8h + 2 quarter + l / 16: byte l / 16 of the dword loaded at 2 quarter
+        const float sc = (float)(int8_t)(r.b[G::W0] >> (8 * ((l0 + 4 * i) >> 4)));
+        // (q - 32) * sc * d == q * (sc d) - 32 (sc d): exact, one fused rounding
+        const float scd = sc * d;
+        *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(lo | hi, scd, -32.0f * scd);
+      }
+    }
+  };
+
+  float4_t acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  // one K step: fragment reads of (xs, ws), then MFMAs interleaved with the
+  // staging of `staged` into (xn, wnext) and the prefetch of `fetch_step`
+  auto step_body = [&](const _Float16* xs, const _Float16* ws, _Float16* xn, _Float16* wnext, const RawT& staged,
+                       int staged_step, RawT& fetched, int fetch_step) {
+    half8_t a[2][MT], b[2][NT];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int koff = 32 * kk + 8 * (lane >> 4);
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+        a[kk][i] = *reinterpret_cast<const half8_t*>(&xs[(wm + 16 * i + (lane & 15)) * ROW + koff]);
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        b[kk][j] = *reinterpret_cast<const half8_t*>(&ws[(wn + 16 * j + (lane & 15)) * ROW + koff]);
+    }
+    store(staged, xn, wnext, staged_step);
+    load(fetched, fetch_step);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[kk][i], b[kk][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2 * MT * NT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two VALU
+      if (i % 4 == 0) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // an LDS store
+      if (i % 4 == 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a global load
+    }
+  };
+
+  RawT ra, rb;
+  load(ra, 0);
+  load(rb, 1);
+  store(ra, xs0, ws0, 0);
+  __syncthreads();
+  for (int step = 0; step < steps; step += 2) {
+    // even step: compute buffer 0, stage step+1 into buffer 1, fetch step+2
+    step_body(xs0, ws0, xs1, ws1, rb, step + 1, ra, min(step + 2, steps - 1));
+    __syncthreads();
+    // odd step: compute buffer 1, stage step+2 into buffer 0, fetch step+3
+    // (past the end the staged and fetched data are clamped copies, never read)
+    step_body(xs1, ws1, xs0, ws0, ra, min(step + 2, steps - 1), rb, min(step + 3, steps - 1));
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int col = n0 + wn + 16 * j + (lane & 15);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = m0 + wm + 16 * i + 4 * (lane >> 4) + e;
+        if (row < M && col < N) store_out<OutT>(out, (size_t)row * N + col, acc[i][j][e]);
+      }
+    }
+}
+
+template <int TYPE, int BM, int BN, int WM, int WN, typename OutT>
+static hipError_t launch_pipe(const GemvArgs& a, hipStream_t stream) {
+  const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM), block(WM * WN * 64);
+  hipLaunchKernelGGL((gemm_pipe<TYPE, BM, BN, WM, WN, OutT>), grid, block, 0, stream,
+                     static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w),
+                     static_cast<OutT*>(a.out), a.m, a.n, a.k);
+  return hipGetLastError();
+}
+
+// Largest tile that still gives the 256 CUs work: the workgroup count of a
+// tile must reach kMinBlocks, else the next smaller tile is taken.
+constexpr long kMinBlocks = 160;
+
+static long tile_blocks(const GemvArgs& a, int bm, int bn) {
+  return (long)((a.m + bm - 1) / bm) * (long)((a.n + bn - 1) / bn);
+}
+
+template <int TYPE, typename OutT>
+static hipError_t launch_type(const GemvArgs& a, hipStream_t stream) {
+  if (tile_blocks(a, 256, 128) >= kMinBlocks) return launch_pipe<TYPE, 256, 128, 4, 2, OutT>(a, stream);
+  if (tile_blocks(a, 128, 128) >= kMinBlocks) return launch_pipe<TYPE, 128, 128, 2, 2, OutT>(a, stream);
+  if (tile_blocks(a, 128, 64) >= kMinBlocks) return launch_pipe<TYPE, 128, 64, 2, 2, OutT>(a, stream);
+  return launch_pipe<TYPE, 64, 64, 1, 2, OutT>(a, stream);
+}
+
+hipError_t launch_gemm_pipe(const GemvArgs& a, hipStream_t stream, bool* handled) {
+  *handled = true;
+  if (a.type == kQ4_K) return a.out_half ? launch_type<kQ4_K, _Float16>(a, stream) : launch_type<kQ4_K, float>(a, stream);
+  if (a.type == kQ6_K) return a.out_half ? launch_type<kQ6_K, _Float16>(a, stream) : launch_type<kQ6_K, float>(a, stream);
+  *handled = false;
+  return hipSuccess;
+}
+
+}  // namespace tensor_gguf

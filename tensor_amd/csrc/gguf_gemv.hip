@@ -366,9 +366,10 @@ static hipError_t launch_out(const GemvArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t stream) {
-  if (a.type == kQ4_K) {
+  if (a.type == kQ4_K || a.type == kQ6_K) {
     bool handled = false;
-    const hipError_t status = launch_gemv_q4k_fast(a, stream, &handled);
+    const hipError_t status = a.type == kQ4_K ? launch_gemv_q4k_fast(a, stream, &handled)
+                                              : launch_gemv_q6k_fast(a, stream, &handled);
     if (handled) return status;
   }
   return a.out_half ? launch_out<_Float16>(a, stream) : launch_out<float>(a, stream);

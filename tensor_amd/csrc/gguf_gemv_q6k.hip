@@ -1,0 +1,143 @@
+// Q6_K decode GEMV fast path (gfx950) for M = 1 and K a multiple of 4096,
+// the LM-head and down-projection shapes: out[n] = sum_k x[k] * W[n, k].
+//
+// A 256-thread workgroup issues the loads of its rows first, then stages x
+// once in LDS (padded 16 B per 128 B, conflict-free b128 reads) behind a
+// single barrier, so the activation vector is read from L2 once per 16 (or 8)
+// rows instead of once per wave.  Lane plan as the generic kernel: four lanes
+// per 210-byte super-block (half hh, 16-element offset l0), sixteen
+// super-blocks per step; each lane rebuilds its 64 six-bit codes with byte
+// masks and multiplies "1024 + q" fp16 codes with v_dot2_f32_f16, removing
+// the 1056 bias (1024 + 32) once per 16-element scale group.
+//
+// Block format: benchmarks/kernels/showcase/triton_kernels.py:163-180.
+#include "gguf_common.h"
+#include "gguf_launch.h"
+
+namespace tensor_gguf {
+
+constexpr int kQ6Waves = 4;
+
+__device__ __forceinline__ float q6_wave_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true));
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+template <int R, int STEPS, typename OutT>
+__global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6k_lds(const _Float16* __restrict__ x,
+                                                              const uint8_t* __restrict__ w,
+                                                              OutT* __restrict__ out, int n_rows) {
+  constexpr int K = STEPS * 4096;
+  constexpr int ROW_BYTES = STEPS * 16 * 210;
+  __shared__ __attribute__((aligned(16))) uint8_t xlds[K * 2 + K / 4];
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * kQ6Waves + (threadIdx.x >> 6)) * R;
+  const int slot = lane >> 2, part = lane & 3, hh = part >> 1, l0 = 16 * (part & 1);
+  uint4 qa[R][STEPS], qb[R][STEPS], qh[R][STEPS];
+  uint2 sc8[R][STEPS];
+  uint32_t dw[R][STEPS];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint8_t* wr = w + (size_t)min(row0 + r, n_rows - 1) * ROW_BYTES + slot * 210;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const uint8_t* block = wr + s * 16 * 210;
+      qa[r][s] = load16(block + 64 * hh + l0);
+      qb[r][s] = load16(block + 64 * hh + 32 + l0);
+      qh[r][s] = load16(block + 128 + 32 * hh + l0);
+      sc8[r][s] = load8(block + 192 + 8 * hh);
+      dw[r][s] = load4(block + 206);  // high half: d
+    }
+  }
+  for (int c = threadIdx.x; c < K / 8; c += kQ6Waves * 64)
+    *reinterpret_cast<uint4*>(xlds + 16 * c + 16 * (c >> 3)) = load16(reinterpret_cast<const uint8_t*>(x) + 16 * c);
+  __syncthreads();
+  if (row0 >= n_rows) return;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    // the four 16-element runs 128 hh + 32 c + l0 (c = 0..3), one scale group each
+    uint4 xs[4][2];
+    float sx[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int ch = ((s * 16 + slot) * 256 + 128 * hh + 32 * c + l0) >> 3;
+      xs[c][0] = *reinterpret_cast<const uint4*>(xlds + 16 * ch + 16 * (ch >> 3));
+      xs[c][1] = *reinterpret_cast<const uint4*>(xlds + 16 * (ch + 1) + 16 * ((ch + 1) >> 3));
+      sx[c] = sum16(xs[c][0], xs[c][1]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t A = word(qa[r][s], u), B = word(qb[r][s], u), H = word(qh[r][s], u);
+        uint32_t q[4];
+        q[0] = (A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u);
+        q[1] = (B & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u);
+        q[2] = ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
+        q[3] = ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          a[c] = dot2(magic01(q[c]), word(xs[c][u >> 1], 2 * (u & 1)), a[c]);
+          a[c] = dot2(magic23(q[c]), word(xs[c][u >> 1], 2 * (u & 1) + 1), a[c]);
+        }
+      }
+      // scale of run c: byte 2c + l0/16 of the 8 scale bytes of this half
+      const float d = half_bits_to_float(dw[r][s] >> 16);
+      const int p = part & 1;
+      const float ds0 = d * (float)(int8_t)(sc8[r][s].x >> (8 * p));
+      const float ds1 = d * (float)(int8_t)(sc8[r][s].x >> (8 * (2 + p)));
+      const float ds2 = d * (float)(int8_t)(sc8[r][s].y >> (8 * p));
+      const float ds3 = d * (float)(int8_t)(sc8[r][s].y >> (8 * (2 + p)));
+      float v = acc[r];
+      v = fmaf(ds0, a[0] - 1056.0f * sx[0], v);
+      v = fmaf(ds1, a[1] - 1056.0f * sx[1], v);
+      v = fmaf(ds2, a[2] - 1056.0f * sx[2], v);
+      v = fmaf(ds3, a[3] - 1056.0f * sx[3], v);
+      acc[r] = v;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float v = q6_wave_sum(acc[r]);
+    if (lane == 0 && row0 + r < n_rows) store_out<OutT>(out, (size_t)(row0 + r), v);
+  }
+}
+
+template <int R, int STEPS, typename OutT>
+static hipError_t launch_q6k(const GemvArgs& a, hipStream_t stream) {
+  constexpr int per_block = kQ6Waves * R;
+  hipLaunchKernelGGL((gemv_q6k_lds<R, STEPS, OutT>), dim3((a.n + per_block - 1) / per_block), dim3(kQ6Waves * 64), 0,
+                     stream, static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w),
+                     static_cast<OutT*>(a.out), a.n);
+  return hipGetLastError();
+}
+
+template <typename OutT>
+static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream, bool* handled) {
+  *handled = true;
+  switch (a.k) {
+    case 4096: return launch_q6k<4, 1, OutT>(a, stream);
+    case 8192: return launch_q6k<2, 2, OutT>(a, stream);
+    case 12288: return launch_q6k<2, 3, OutT>(a, stream);
+    default: *handled = false; return hipSuccess;
+  }
+}
+
+hipError_t launch_gemv_q6k_fast(const GemvArgs& a, hipStream_t stream, bool* handled) {
+  if (a.m != 1) {
+    *handled = false;
+    return hipSuccess;
+  }
+  return a.out_half ? launch_typed<_Float16>(a, stream, handled) : launch_typed<float>(a, stream, handled);
+}
+
+}  // namespace tensor_gguf

@@ -31,7 +31,12 @@ hipError_t launch_gemv(const GemvArgs& args, hipStream_t stream);
 // Q4_K fast paths (LDS dot2 kernel for M = 1, MFMA kernel for M >= 2); sets
 // *handled to false when the shape is not covered by them.
 hipError_t launch_gemv_q4k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
+// Q6_K fast path (LDS-staged x, M = 1, K in {4096, 8192, 12288}).
+hipError_t launch_gemv_q6k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 hipError_t launch_dequant(const DequantArgs& args, hipStream_t stream);
 hipError_t launch_gemm(const GemvArgs& args, hipStream_t stream);
+// Pipelined dequant-GEMM for Q4_K and Q6_K (K a multiple of 256); sets
+// *handled to false for the encodings it does not cover.
+hipError_t launch_gemm_pipe(const GemvArgs& args, hipStream_t stream, bool* handled);
 
 }  // namespace tensor_gguf

@@ -195,6 +195,21 @@ def test_gemm_parity_baseline_shapes(hip_device, c_oracle, encoding, m, n, k):
     assert R.relative_l2(got, expected) <= TOLERANCE
 
 
+@pytest.mark.parametrize("encoding", ["q4_k", "q6_k"])
+@pytest.mark.parametrize("m,n", [(384, 7168), (256, 9984), (40, 1000)])
+def test_gemm_tile_configurations(hip_device, c_oracle, encoding, m, n):
+    """Shapes that select the 128x128, 128x64 and 64x64 (ragged N) workgroup tiles."""
+    code = Q.ggml_type(encoding)
+    k = 512
+    note("gemm-tiles", encoding, m, n, k)
+    raw = cases.weight(n, k, encoding, 93)
+    x = cases.activation(m, k, 94)
+    c_oracle.set_threads(16)
+    expected = c_oracle.linear(x, raw, code, n, k, prefill=True)
+    got = run_linear(hip_device, "gguf_gemm", encoding, x, raw, "float32")
+    assert R.relative_l2(got, expected) <= 1e-5
+
+
 def test_gemm_zero_input_gives_exact_zero(hip_device):
     raw = cases.weight(128, 512, "q4_k", 95)
     x = np.zeros((64, 512), np.float16)

@@ -75,6 +75,42 @@ class Linear:
             b.release()
 
 
+class GroupLinear:
+    """Matrices sharing one activation input, launched as one grouped GEMV call."""
+
+    def __init__(self, device, encoding, m, shapes, out_dtype, copies, seed, x=None):
+        from tests import gguf_cases as cases
+
+        k = shapes[0][1]
+        assert all(sk == k for _, sk in shapes)
+        self.device, self.encoding, self.m, self.k = device, encoding, m, k
+        self.weights = []
+        for i, (n, _) in enumerate(shapes):
+            raw = cases.weight(n, k, encoding, seed + 2 * i)
+            first = device.from_numpy(raw)
+            self.weights.append([first] + [device.empty(raw.shape, "uint8").copy_from(first)
+                                           for _ in range(copies - 1)])
+        self.x = x if x is not None else device.from_numpy(cases.activation(m, k, seed + 1))
+        self.outs = [device.empty((m, n), out_dtype) for n, _ in shapes]
+        self.exe = device.load("gguf_gemv_group", encoding=encoding, out_dtype=out_dtype, count=len(shapes))
+        self.calls = []
+        for c in range(copies):
+            args = [self.x]
+            for ws, out in zip(self.weights, self.outs):
+                args += [ws[c], out]
+            self.calls.append(self.exe.bind(*args))
+        itemsize = np.dtype(out_dtype).itemsize
+        self.bytes = sum(weight_bytes(encoding, n, k) + itemsize * m * n for n, _ in shapes) + 2 * m * k
+        self.flops = sum(2 * m * n * k for n, _ in shapes)
+
+    def release(self):
+        for ws in self.weights:
+            for b in ws:
+                b.release()
+        for b in self.outs:
+            b.release()
+
+
 def copies_for(bytes_per_rotation_unit):
     return max(2, math.ceil(ROTATION_BYTES / bytes_per_rotation_unit))
 
@@ -224,14 +260,14 @@ def main():
             source.release()
             target.release()
             log("calibration: 5 device copies of", 256 << 20, "bytes")
-        # ---- headline: C2 Q4_K GEMV M=1, gate + up + down per step
+        # ---- headline: C2 Q4_K GEMV M=1, one decode MLP per step: gate + up as one
+        # grouped launch (they share x), then down
         per_step_weights = 2 * weight_bytes("q4_k", 12288, 4096) + weight_bytes("q4_k", 4096, 12288)
         copies = copies_for(per_step_weights)
         log("headline weights", per_step_weights, "B per step,", copies, "rotated copies")
-        gate = Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 1)
-        up = Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 3, x=gate.x)
+        gate_up = GroupLinear(device, "q4_k", 1, [(12288, 4096), (12288, 4096)], "float16", copies, 1)
         down = Linear(device, "gguf_gemv", "q4_k", 1, 4096, 12288, "float16", copies, 5)
-        mlp = [gate, up, down]
+        mlp = [gate_up, down]
         step_bytes = sum(layer.bytes for layer in mlp)
         for launch in rotated_launches(mlp, args.warmup):
             launch()
@@ -245,10 +281,10 @@ def main():
         value = step_bytes * args.steps / seconds / 1e9
         log(f"headline {value:.1f} GB/s, {seconds / args.steps * 1e6:.2f} us/step")
 
-        # ---- roofline of the dominant kernel: Q4_K GEMV 12288 x 4096, M=1
+        # ---- roofline of the dominant kernel: the grouped gate + up GEMV, 2 x 12288 x 4096, M=1
         launches = 200
-        kernel_s = time_graph(device, [gate.calls[i % copies].launch for i in range(launches)]) / launches
-        achieved = gate.bytes / kernel_s / 1e9
+        kernel_s = time_graph(device, [gate_up.calls[i % copies].launch for i in range(launches)]) / launches
+        achieved = gate_up.bytes / kernel_s / 1e9
         roofline = {
             "bound": "hbm",
             "achieved": round(achieved, 1),
@@ -256,15 +292,15 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "gemv_q4k<M=1> 12288x4096 fp16 out",
+            "kernel": "gemv_q4k_m1<STEPS=1, MATS=2> gate+up 2 x 12288x4096, M=1, fp16 out",
             "avg_us": round(kernel_s * 1e6, 3),
-            "algorithmic_bytes": gate.bytes,
+            "algorithmic_bytes": gate_up.bytes,
         }
         log(f"roofline kernel {kernel_s * 1e6:.2f} us -> {achieved:.1f} GB/s")
 
         details = {}
         if not args.no_details:
-            details = run_details(device, gate.x, log)
+            details = run_details(device, gate_up.x, log)
         for layer in mlp:
             layer.release()
 
@@ -283,7 +319,7 @@ def main():
         "data": "synthetic: seeded N(0,0.02) weights quantized to Q4_K, N(0,1) fp16 activations",
         "config": {
             "workload": "C2 Q4_K decode GEMV, M=1, Qwen3-8B MLP step = gate 12288x4096 + up 12288x4096 "
-                        "+ down 4096x12288, fp16 out, weights rotated through "
+                        "(one grouped launch sharing x) + down 4096x12288, fp16 out, weights rotated through "
                         f"{copies} copies ({copies * per_step_weights >> 20} MiB)",
             "M": 1,
             "hidden": 4096,
@@ -311,6 +347,21 @@ def run_details(device, x4096, log):
         details[name] = {"us": round(seconds * 1e6, 3), "GB/s": round(gbs, 1),
                          "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
         log(name, details[name])
+        layer.release()
+
+    # the headline step as three single-matrix launches (gate, up, down)
+    copies = copies_for(2 * weight_bytes("q4_k", 12288, 4096) + weight_bytes("q4_k", 4096, 12288))
+    mlp = [Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 1, x=x4096),
+           Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 3, x=x4096),
+           Linear(device, "gguf_gemv", "q4_k", 1, 4096, 12288, "float16", copies, 5)]
+    steps = 50
+    seconds = time_graph(device, rotated_launches(mlp, steps)) / steps
+    step_bytes = sum(layer.bytes for layer in mlp)
+    details["C2_step_m1_three_launches"] = {"us": round(seconds * 1e6, 3),
+                                            "GB/s": round(step_bytes / seconds / 1e9, 1),
+                                            "hbm_frac": round(step_bytes / seconds / 1e9 / HBM_PEAK_GBS, 4)}
+    log("C2_step_m1_three_launches", details["C2_step_m1_three_launches"])
+    for layer in mlp:
         layer.release()
 
     for m in (1, 4, 8):
@@ -350,6 +401,22 @@ def run_details(device, x4096, log):
         log(f"C5_layer_m{m}", details[f"C5_layer_m{m}"])
         for layer in layers:
             layer.release()
+    # C5 at M=1 the way a decode step runs it: q + k + v grouped, o, gate + up grouped, down
+    copies = copies_for(layer_weights)
+    x = device.from_numpy(np.zeros((1, 4096), np.float16) + np.float16(0.5))
+    layers = [GroupLinear(device, "q4_k", 1, [(4096, 4096), (1024, 4096), (1024, 4096)], "float16", copies, 40, x=x),
+              Linear(device, "gguf_gemv", "q4_k", 1, 4096, 4096, "float16", copies, 46, x=x),
+              GroupLinear(device, "q4_k", 1, [(12288, 4096), (12288, 4096)], "float16", copies, 48, x=x),
+              Linear(device, "gguf_gemv", "q6_k", 1, 4096, 12288, "float16", copies, 52)]
+    steps = 20
+    seconds = time_graph(device, rotated_launches(layers, steps)) / steps
+    total_bytes = sum(layer.bytes for layer in layers)
+    details["C5_layer_m1_grouped"] = {"us": round(seconds * 1e6, 2), "GB/s": round(total_bytes / seconds / 1e9, 1),
+                                      "launches": 4}
+    log("C5_layer_m1_grouped", details["C5_layer_m1_grouped"])
+    for layer in layers:
+        layer.release()
+    x.release()
     return details
 
 

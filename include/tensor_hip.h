@@ -77,6 +77,23 @@ int32_t tensor_gguf_gemm_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 int32_t tensor_gguf_linear_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 
 /*
+ * Grouped decode GEMV: out_i[m, n] = sum_k x[m, k] * dequant(W_i)[n, k] for
+ * 1 <= c <= TENSOR_GGUF_GEMV_GROUP_MAX matrices that share the activations x
+ * (a decoder's gate and up projections, or q, k and v).  No counterpart in the
+ * reference: there every linear is its own gemv_packed launch
+ * (benchmarks/kernels/showcase/kernels.py:114-119).  The group is one launch
+ * of the Q4_K M = 1 kernel when K is a multiple of 4096; for other encodings
+ * and shapes it is c launches of tensor_gguf_gemv_v1's kernels in order on the
+ * stream.  Arguments, in order:
+ *   0        x     buffer fp16  [M, K], 1 <= M <= TENSOR_GGUF_GEMV_MAX_M
+ *   2i+1     w_i   buffer uint8 [N_i, K/QK*BLOCK]
+ *   2i+2     out_i buffer [M, N_i], one dtype (fp16 or fp32) for all i
+ *   2c+1     type  scalar uint32 GGML type id, shared by the group
+ */
+#define TENSOR_GGUF_GEMV_GROUP_MAX 3
+int32_t tensor_gguf_gemv_group_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/*
  * Dequantize raw GGUF rows: out[n, k] = dequant(W)[n, k], exact in fp32 and
  * round-to-nearest-even in fp16 (block decoding of
  * benchmarks/kernels/showcase/triton_kernels.py:134-181, the decode_ggml

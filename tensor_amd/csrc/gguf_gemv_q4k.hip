@@ -2,14 +2,14 @@
 //
 // Two kernels replace the generic VALU GEMV for Q4_K:
 //
-//  * M = 1, K a multiple of 4096: gemv_q4k_lds.  A 512-thread workgroup stages
-//    x once in LDS (padded 16 B per 128 B so the wave's b128 reads are
-//    conflict-free) while the weight loads of its 16 rows are already in
-//    flight.  Lane = (super-block slot 0..15, quant pair j 0..3): each lane
-//    decodes 64 codes per row and super-block, unpacks its two sub-blocks'
-//    6-bit scale/min pairs once, and accumulates with v_dot2_f32_f16 on
-//    "1024 + q" (low nibbles) and "1024 + 16 q" (high nibbles, left in place)
-//    fp16 codes; the bias is removed per sub-block with the sum of x.
+//  * M = 1, K a multiple of 4096: gemv_q4k_m1.  A 1024-thread workgroup owns
+//    16 rows, one per wave, of one matrix of a group of up to three matrices
+//    that share x (gate + up, q + k + v).  It loads x first, then all of its
+//    weight bytes, and stages x once in LDS together with the per-sub-block
+//    sums of x.  Lane = (super-block slot 0..15, quant pair j 0..3): each lane
+//    decodes 64 codes per row and 4096-column step, widens them to subnormal
+//    fp16 codes with bit masks only, accumulates with v_dot2_f32_f16 and
+//    applies d * sc once per sub-block and dmin * m with the sum of x.
 //
 //  * 2 <= M <= 8: gemv_q4k_mfma.  A wave computes a 16-row tile with
 //    v_mfma_f32_16x16x32_f16: the weights are the B operand (lane l holds row
@@ -65,90 +65,103 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 
 // ------------------------------------------------------- M = 1, LDS x ---
 
-template <int STEPS>
-struct Q4KRow {
-  uint4 hd[STEPS], q0[STEPS], q1[STEPS];
-};
+// Widening by bit masks alone: q & 0x000F000F is the fp16 pair (q0 * 2^-24,
+// q2 * 2^-24) -- subnormal fp16 values are exact and v_dot2_f32_f16 multiplies
+// them exactly -- and q & 0x00F000F0 the pair (16 q0, 16 q2) * 2^-24 of the high
+// nibbles.  Codes of bytes 0 and 2 pair with x[4u] and x[4u+2], so x is staged
+// in LDS with the halves of every 4-element group reordered (x0, x2, x1, x3).
+constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
 
-template <int STEPS>
-__device__ __forceinline__ float q4k_row_dot(const Q4KRow<STEPS>& d, const uint4 (&xs)[STEPS][8],
-                                             const float (&sx)[STEPS][2], const PairSelect& sel) {
+// One wave = one weight row; 16 waves = 16 consecutive rows of one matrix of
+// the group.  The activation vector is loaded first, then every weight load of
+// the wave, so that on each CU the small x load is not queued behind weight
+// traffic; a compiler barrier keeps the weight loads from sinking below the
+// x staging, and the workgroup barrier fences LDS only, so decoding starts as
+// soon as this wave's own bytes have arrived.
+template <int STEPS, int MATS, typename OutT>
+__global__ __launch_bounds__(kM1Waves * 64) void gemv_q4k_m1(const _Float16* __restrict__ x, GemvGroup<OutT> g) {
+  constexpr int K = STEPS * 4096, ROW_BYTES = STEPS * 16 * 144, T = kM1Waves * 64;
+  constexpr int XC = (K / 8 + T - 1) / T;  // 16-byte x chunks per thread
+  __shared__ __attribute__((aligned(16))) uint8_t xlds[K * 2 + K / 4];
+  __shared__ __attribute__((aligned(16))) float sxl[K / 32];
+  const int lane = threadIdx.x & 63;
+  int mat = 0, block = blockIdx.x;
+#pragma unroll
+  for (int i = 1; i < MATS; ++i) {
+    if (block < g.blocks[i - 1]) break;
+    block -= g.blocks[i - 1];
+    mat = i;
+  }
+  const int n_rows = g.n[mat];
+  const int row = block * kM1Waves + (threadIdx.x >> 6);
+  const int slot = lane >> 2, j = lane & 3;
+
+  uint4 xr[XC];
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    if (c < K / 8) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * c);
+  }
+  const uint8_t* wl = g.w[mat] + (size_t)min(row, n_rows - 1) * ROW_BYTES + slot * 144;
+  const uint8_t* wq = wl + 32 * j;
+  uint4 hd[STEPS], q0[STEPS], q1[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    hd[s] = load16(wl + s * 2304);
+    q0[s] = load16(wq + s * 2304 + 16);
+    q1[s] = load16(wq + s * 2304 + 32);
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    if (c < K / 8) {
+      const uint4 v = xr[i];
+      // sum of the 32 x of sub-block c / 4 over the four chunks c = 4 s' .. 4 s' + 3
+      float p = sum16(v, make_uint4(0, 0, 0, 0));
+      p += __shfl_xor(p, 1, 64);
+      p += __shfl_xor(p, 2, 64);
+      if ((c & 3) == 0) sxl[c >> 2] = p;
+      // chunk c (16 B) -> LDS byte 16 c + 16 (c / 8): padding keeps the b128 reads conflict-free
+      *reinterpret_cast<uint4*>(xlds + 16 * c + 16 * (c >> 3)) =
+          make_uint4(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.y, v.x, 0x07060302u),
+                     __builtin_amdgcn_perm(v.w, v.z, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  if (row >= n_rows) return;
+
+  const PairSelect sel(j);
   float total = 0.f;
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
+    const int c0 = ((s * 16 + slot) * 256 + 64 * j) >> 3;
+    uint4 xs[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xs[i] = *reinterpret_cast<const uint4*>(xlds + 16 * (c0 + i) + 16 * ((c0 + i) >> 3));
+    const float2 sx = *reinterpret_cast<const float2*>(&sxl[(s * 16 + slot) * 8 + 2 * j]);
     float al = 0.f, ah = 0.f;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const uint32_t q = word(u < 4 ? d.q0[s] : d.q1[s], u & 3);
-      const uint32_t lo = q & 0x0F0F0F0Fu, hi = q & 0xF0F0F0F0u;
-      al = dot2(magic01(lo), word(xs[s][u >> 1], 2 * (u & 1)), al);
-      al = dot2(magic23(lo), word(xs[s][u >> 1], 2 * (u & 1) + 1), al);
-      ah = dot2(magic01(hi), word(xs[s][4 + (u >> 1)], 2 * (u & 1)), ah);
-      ah = dot2(magic23(hi), word(xs[s][4 + (u >> 1)], 2 * (u & 1) + 1), ah);
+      const uint32_t q = word(u < 4 ? q0[s] : q1[s], u & 3), t = q >> 8;
+      al = dot2(q & 0x000F000Fu, word(xs[u >> 1], 2 * (u & 1)), al);
+      al = dot2(t & 0x000F000Fu, word(xs[u >> 1], 2 * (u & 1) + 1), al);
+      ah = dot2(q & 0x00F000F0u, word(xs[4 + (u >> 1)], 2 * (u & 1)), ah);
+      ah = dot2(t & 0x00F000F0u, word(xs[4 + (u >> 1)], 2 * (u & 1) + 1), ah);
     }
     uint32_t scs, mns;
-    sel.codes(d.hd[s], scs, mns);
-    const float dd = half_bits_to_float(d.hd[s].x), dmin = half_bits_to_float(d.hd[s].x >> 16);
-    const float ds_lo = dd * (float)(scs & 0xFF), ds_hi = dd * (float)(scs >> 8) * 0.0625f;
-    const float dm_lo = dmin * (float)(mns & 0xFF), dm_hi = dmin * (float)(mns >> 8);
-    // al = sum x (1024 + q), ah = sum x (1024 + 16 q)
-    total = fmaf(ds_lo, al - 1024.0f * sx[s][0], total);
-    total = fmaf(-dm_lo, sx[s][0], total);
-    total = fmaf(ds_hi, ah - 1024.0f * sx[s][1], total);
-    total = fmaf(-dm_hi, sx[s][1], total);
+    sel.codes(hd[s], scs, mns);
+    const float dd = half_bits_to_float(hd[s].x), dmin = half_bits_to_float(hd[s].x >> 16);
+    // al = 2^-24 sum x q (sub-block 2j), ah = 2^-20 sum x q (sub-block 2j+1)
+    total = fmaf(dd * (float)(scs & 0xFF) * kTwo24, al, total);
+    total = fmaf(dd * (float)(scs >> 8) * kTwo20, ah, total);
+    total = fmaf(-dmin * (float)(mns & 0xFF), sx.x, total);
+    total = fmaf(-dmin * (float)(mns >> 8), sx.y, total);
   }
-  return total;
-}
-
-constexpr int kLdsWaves = 8, kLdsRows = 2;
-
-template <int STEPS, typename OutT>
-__global__ __launch_bounds__(kLdsWaves * 64) void gemv_q4k_lds(const _Float16* __restrict__ x,
-                                                               const uint8_t* __restrict__ w,
-                                                               OutT* __restrict__ out, int n_rows) {
-  constexpr int K = STEPS * 4096;
-  constexpr int ROW_BYTES = STEPS * 16 * 144;
-  __shared__ __attribute__((aligned(16))) uint8_t xlds[K * 2 + K / 4];
-  const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * kLdsWaves + (threadIdx.x >> 6)) * kLdsRows;
-  const int slot = lane >> 2, j = lane & 3;
-  const uint8_t* wl = w + slot * 144;  // super-block start
-  const uint8_t* wq = wl + 32 * j;     // this lane's 32 quant bytes at +16
-  Q4KRow<STEPS> rd[kLdsRows];
-#pragma unroll
-  for (int r = 0; r < kLdsRows; ++r) {
-    const size_t base = (size_t)min(row0 + r, n_rows - 1) * ROW_BYTES;
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      rd[r].hd[s] = load16(wl + base + s * 2304);
-      rd[r].q0[s] = load16(wq + base + s * 2304 + 16);
-      rd[r].q1[s] = load16(wq + base + s * 2304 + 32);
-    }
-  }
-  // x chunk c (16 B) -> LDS byte 16 c + 16 (c / 8)
-  for (int c = threadIdx.x; c < K / 8; c += kLdsWaves * 64)
-    *reinterpret_cast<uint4*>(xlds + 16 * c + 16 * (c >> 3)) = load16(reinterpret_cast<const uint8_t*>(x) + 16 * c);
-  __syncthreads();
-  if (row0 >= n_rows) return;
-  uint4 xs[STEPS][8];
-#pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    const int c0 = ((s * 16 + slot) * 256 + 64 * j) >> 3;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xs[s][i] = *reinterpret_cast<const uint4*>(xlds + 16 * (c0 + i) + 16 * ((c0 + i) >> 3));
-  }
-  float sx[STEPS][2];
-#pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    sx[s][0] = sum16(xs[s][0], xs[s][1]) + sum16(xs[s][2], xs[s][3]);
-    sx[s][1] = sum16(xs[s][4], xs[s][5]) + sum16(xs[s][6], xs[s][7]);
-  }
-  const PairSelect sel(j);
-#pragma unroll
-  for (int r = 0; r < kLdsRows; ++r) {
-    const float v = wave_sum_dpp(q4k_row_dot<STEPS>(rd[r], xs, sx, sel));
-    if (lane == 0 && row0 + r < n_rows) store_out<OutT>(out, (size_t)(row0 + r), v);
-  }
+  const float v = wave_sum_dpp(total);
+  if (lane == 0) store_out<OutT>(g.out[mat], (size_t)row, v);
 }
 
 // ------------------------------------------------------- 2 <= M, MFMA ---
@@ -233,20 +246,35 @@ __global__ __launch_bounds__(SPLIT * 64) void gemv_q4k_mfma(const _Float16* __re
 
 // ---------------------------------------------------------------- launch ---
 
-template <typename OutT>
-static hipError_t launch_lds(const GemvArgs& a, hipStream_t stream) {
-  const _Float16* x = static_cast<const _Float16*>(a.x);
-  const uint8_t* w = static_cast<const uint8_t*>(a.w);
-  OutT* out = static_cast<OutT*>(a.out);
-  const dim3 grid((a.n + kLdsWaves * kLdsRows - 1) / (kLdsWaves * kLdsRows)), block(kLdsWaves * 64);
-  switch (a.k / 4096) {
-    case 1: hipLaunchKernelGGL((gemv_q4k_lds<1, OutT>), grid, block, 0, stream, x, w, out, a.n); break;
-    case 2: hipLaunchKernelGGL((gemv_q4k_lds<2, OutT>), grid, block, 0, stream, x, w, out, a.n); break;
-    case 3: hipLaunchKernelGGL((gemv_q4k_lds<3, OutT>), grid, block, 0, stream, x, w, out, a.n); break;
-    case 4: hipLaunchKernelGGL((gemv_q4k_lds<4, OutT>), grid, block, 0, stream, x, w, out, a.n); break;
+template <int MATS, typename OutT>
+static hipError_t launch_m1(const _Float16* x, const GemvGroup<OutT>& g, int k, hipStream_t stream) {
+  const dim3 grid(g.blocks[0] + (MATS > 1 ? g.blocks[1] : 0) + (MATS > 2 ? g.blocks[2] : 0)), block(kM1Waves * 64);
+  switch (k / 4096) {
+    case 1: hipLaunchKernelGGL((gemv_q4k_m1<1, MATS, OutT>), grid, block, 0, stream, x, g); break;
+    case 2: hipLaunchKernelGGL((gemv_q4k_m1<2, MATS, OutT>), grid, block, 0, stream, x, g); break;
+    case 3: hipLaunchKernelGGL((gemv_q4k_m1<3, MATS, OutT>), grid, block, 0, stream, x, g); break;
+    case 4: hipLaunchKernelGGL((gemv_q4k_m1<4, MATS, OutT>), grid, block, 0, stream, x, g); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <typename OutT>
+static hipError_t launch_m1_group(const GemvArgs* a, int count, hipStream_t stream) {
+  GemvGroup<OutT> g{};
+  for (int i = 0; i < count; ++i) {
+    g.w[i] = static_cast<const uint8_t*>(a[i].w);
+    g.out[i] = static_cast<OutT*>(a[i].out);
+    g.n[i] = a[i].n;
+    g.blocks[i] = (a[i].n + kM1Waves - 1) / kM1Waves;
+  }
+  const _Float16* x = static_cast<const _Float16*>(a[0].x);
+  switch (count) {
+    case 1: return launch_m1<1, OutT>(x, g, a[0].k, stream);
+    case 2: return launch_m1<2, OutT>(x, g, a[0].k, stream);
+    case 3: return launch_m1<3, OutT>(x, g, a[0].k, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int M, typename OutT>
@@ -266,7 +294,7 @@ static hipError_t launch_mfma(const GemvArgs& a, hipStream_t stream) {
 template <typename OutT>
 static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream, bool* handled) {
   *handled = true;
-  if (a.m == 1 && a.k % 4096 == 0 && a.k <= 4 * 4096) return launch_lds<OutT>(a, stream);
+  if (a.m == 1 && a.k % 4096 == 0 && a.k <= 4 * 4096) return launch_m1_group<OutT>(&a, 1, stream);
   switch (a.m) {
     case 2: return launch_mfma<2, OutT>(a, stream);
     case 3: return launch_mfma<3, OutT>(a, stream);
@@ -281,6 +309,12 @@ static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream, bool* hand
 
 hipError_t launch_gemv_q4k_fast(const GemvArgs& a, hipStream_t stream, bool* handled) {
   return a.out_half ? launch_typed<_Float16>(a, stream, handled) : launch_typed<float>(a, stream, handled);
+}
+
+bool gemv_q4k_group_supported(int m, int k) { return m == 1 && k % 4096 == 0 && k <= 4 * 4096; }
+
+hipError_t launch_gemv_q4k_group(const GemvArgs* a, int count, hipStream_t stream) {
+  return a[0].out_half ? launch_m1_group<_Float16>(a, count, stream) : launch_m1_group<float>(a, count, stream);
 }
 
 }  // namespace tensor_gguf

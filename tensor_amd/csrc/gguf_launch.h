@@ -27,10 +27,28 @@ struct DequantArgs {
 // Largest M the decode GEMV entry accepts.
 constexpr int kGemvMaxM = 8;
 
+// Largest number of matrices one grouped decode GEMV launch covers.
+constexpr int kGemvGroupMax = 3;
+// Waves (= rows) per workgroup of the M = 1 Q4_K kernel.
+constexpr int kM1Waves = 16;
+
+// Matrices of one grouped launch: they share x and K; blocks[i] workgroups
+// cover matrix i.
+template <typename OutT>
+struct GemvGroup {
+  const uint8_t* w[kGemvGroupMax];
+  OutT* out[kGemvGroupMax];
+  int n[kGemvGroupMax];
+  int blocks[kGemvGroupMax];
+};
+
 hipError_t launch_gemv(const GemvArgs& args, hipStream_t stream);
 // Q4_K fast paths (LDS dot2 kernel for M = 1, MFMA kernel for M >= 2); sets
 // *handled to false when the shape is not covered by them.
 hipError_t launch_gemv_q4k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
+// Grouped M = 1 Q4_K GEMV: `count` (<= kGemvGroupMax) matrices sharing x and K in one launch.
+bool gemv_q4k_group_supported(int m, int k);
+hipError_t launch_gemv_q4k_group(const GemvArgs* args, int count, hipStream_t stream);
 // Q6_K fast path (LDS-staged x, M = 1, K in {4096, 8192, 12288}).
 hipError_t launch_gemv_q6k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 hipError_t launch_dequant(const DequantArgs& args, hipStream_t stream);

@@ -152,6 +152,59 @@ int32_t linear_call(const TensorCallV1* call, TensorErrorV1* error, Op op) {
   return TENSOR_OK;
 }
 
+// Grouped decode GEMV: x shared by `count` (w, out) pairs, arguments
+// [x, w0, out0, .., w(c-1), out(c-1), type].
+int32_t group_call(const TensorCallV1* call, TensorErrorV1* error) {
+  ok(error);
+  if (!call || call->abi_version != TENSOR_ABI_VERSION || call->struct_size < sizeof(TensorCallV1))
+    return fail(error, TENSOR_ERROR_ABI, "unsupported call ABI");
+  const uint32_t argc = call->argument_count;
+  if (argc < 4 || argc > 2 + 2 * tensor_gguf::kGemvGroupMax || argc % 2)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "invalid argument count or flags");
+  if (int32_t s = check_call(call, argc, error)) return s;
+  const int count = (int)(argc - 2) / 2;
+  const int ordinal = call->stream.device_ordinal;
+  const TensorArgumentV1* a = call->arguments;
+  Format format;
+  if (int32_t s = check_type(a[argc - 1], &format, error)) return s;
+  if (int32_t s = check_matrix(a[0], "x", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT16, error)) return s;
+  const int64_t m = a[0].buffer.shape[0], k = a[0].buffer.shape[1];
+  if (m > tensor_gguf::kGemvMaxM)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "x: decode GEMV takes at most %d rows", tensor_gguf::kGemvMaxM);
+  if (k % format.qk) return fail(error, TENSOR_ERROR_ARGUMENT, "x: K is not a multiple of the block size");
+  tensor_gguf::GemvArgs args[tensor_gguf::kGemvGroupMax];
+  for (int i = 0; i < count; ++i) {
+    const TensorArgumentV1& w = a[1 + 2 * i];
+    const TensorArgumentV1& out = a[2 + 2 * i];
+    if (int32_t s = check_matrix(w, "w", ordinal, TENSOR_UINT8, TENSOR_UINT8, error)) return s;
+    if (int32_t s = check_matrix(out, "out", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT32, error)) return s;
+    const int64_t n = w.buffer.shape[0];
+    if (w.buffer.shape[1] != k / format.qk * format.bytes)
+      return fail(error, TENSOR_ERROR_ARGUMENT, "w%d: shape, stride or size mismatch", i);
+    if (out.buffer.shape[0] != m || out.buffer.shape[1] != n || out.dtype != a[2].dtype)
+      return fail(error, TENSOR_ERROR_ARGUMENT, "out%d: shape, stride, size or dtype mismatch", i);
+    args[i].x = reinterpret_cast<const void*>(a[0].buffer.address);
+    args[i].w = reinterpret_cast<const void*>(w.buffer.address);
+    args[i].out = reinterpret_cast<void*>(out.buffer.address);
+    args[i].type = (int)a[argc - 1].scalar;
+    args[i].m = (int)m;
+    args[i].n = (int)n;
+    args[i].k = (int)k;
+    args[i].out_half = out.dtype == TENSOR_FLOAT16;
+  }
+  if (int32_t s = check_device(call, error)) return s;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
+  hipError_t status = hipSuccess;
+  if (args[0].type == (int)TENSOR_GGML_Q4_K && tensor_gguf::gemv_q4k_group_supported((int)m, (int)k)) {
+    status = tensor_gguf::launch_gemv_q4k_group(args, count, stream);
+  } else {
+    // no grouped kernel for this shape or encoding: one launch per matrix, same stream order
+    for (int i = 0; i < count && status == hipSuccess; ++i) status = tensor_gguf::launch_gemv(args[i], stream);
+  }
+  if (status != hipSuccess) return hip_fail(error, status, "GGUF grouped GEMV launch");
+  return TENSOR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -166,6 +219,10 @@ int32_t tensor_gguf_gemm_v1(const TensorCallV1* call, TensorErrorV1* error) {
 
 int32_t tensor_gguf_linear_v1(const TensorCallV1* call, TensorErrorV1* error) {
   return linear_call(call, error, Op::kLinear);
+}
+
+int32_t tensor_gguf_gemv_group_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  return group_call(call, error);
 }
 
 int32_t tensor_gguf_dequant_v1(const TensorCallV1* call, TensorErrorV1* error) {

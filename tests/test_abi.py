@@ -157,6 +157,77 @@ def test_dequant_argument_checks():
     assert status == ERR_ARG and "out" in message
 
 
+class GroupCall:
+    """A well-formed grouped GEMV call [x, (w_i, out_i)..., type] with fake addresses."""
+
+    def __init__(self, rows=(64, 32), m=1, k=512, type_=12, block=144, qk=256):
+        count = len(rows)
+        shapes = [(m, k)]
+        dtypes, items = [10], [2]
+        for n in rows:
+            shapes += [(n, k // qk * block), (m, n)]
+            dtypes += [3, 10]
+            items += [1, 2]
+        self.keep = []
+        self.args = (abi.Argument * (2 * count + 2))()
+        for i, (shape, dtype, item) in enumerate(zip(shapes, dtypes, items)):
+            shp = (c.c_int64 * 2)(*shape)
+            strides = (c.c_int64 * 2)(shape[1] * item, item)
+            self.keep += [shp, strides]
+            self.args[i].kind = 1
+            self.args[i].dtype = dtype
+            self.args[i].buffer = abi.BufferDescriptor(0x10000 * (i + 1), shape[0] * shape[1] * item, shp, strides,
+                                                       2, dtype, 10, 0)
+        last = 2 * count + 1
+        self.args[last].kind = 2
+        self.args[last].dtype = 7
+        self.args[last].scalar = type_
+        self.call = abi.CallDescriptor(1, 72, self.args, 2 * count + 2, 0, (c.c_uint32 * 3)(1, 1, 1),
+                                       (c.c_uint32 * 3)(256, 1, 1), 0, abi.StreamDescriptor(10, 0, 0))
+
+    def run(self):
+        error = abi.ErrorDescriptor()
+        status = _native.kernel("tensor_gguf_gemv_group_v1")(c.byref(self.call), c.byref(error))
+        return status, error.message.decode()
+
+
+def test_group_call_argument_checks():
+    call = GroupCall(rows=(64, 32, 16))
+    call.call.argument_count = 7  # odd: not [x, pairs..., type]
+    assert call.run() == (ERR_ARG, "invalid argument count or flags")
+    call = GroupCall(rows=(64, 32))
+    call.call.argument_count = 10  # beyond three matrices
+    assert call.run()[0] == ERR_ARG
+    call = GroupCall(rows=(64, 32))
+    call.keep[8][1] = 31  # out1 columns != N1 (a consistent [1, 31] descriptor)
+    call.keep[9][0] = 31 * 2
+    call.args[4].buffer.byte_size = 31 * 2
+    assert call.run() == (ERR_ARG, "out1: shape, stride, size or dtype mismatch")
+    call = GroupCall(rows=(64, 32), m=9)
+    status, message = call.run()
+    assert status == ERR_ARG and "at most 8" in message
+    call = GroupCall(rows=(64,))
+    call.args[3].scalar = 5
+    status, message = call.run()
+    assert status == ERR_ARG and "unsupported GGML type" in message
+
+
+def test_group_manifest_binds_each_matrix():
+    manifest = kernels.manifest("gguf_gemv_group", "q4_k", "float16", count=3)
+    assert manifest["outputs"] == ["out0", "out1", "out2"]
+    k = 4096
+    buffers = {"x": fake((1, k), "float16")}
+    for i, n in enumerate((4096, 1024, 1024)):
+        buffers[f"w{i}"] = fake((n, k // 256 * 144), "uint8")
+        buffers[f"out{i}"] = fake((1, n), "float16")
+    symbols, _ = bind_shapes(manifest, buffers)
+    assert symbols == {"M": 1, "K": 4096, "N0": 4096, "N1": 1024, "N2": 1024}
+    with pytest.raises(ValueError):
+        kernels.manifest("gguf_gemv_group", "q4_k", count=4)
+    with pytest.raises(ValueError):
+        kernels.manifest("gguf_gemv", "q4_k", count=2)
+
+
 # --------------------------------------------------------- manifest binding --
 
 def fake(shape, dtype):

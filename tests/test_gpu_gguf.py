@@ -119,6 +119,59 @@ def test_gemv_parity_baseline_shapes(hip_device, c_oracle, encoding, n, k, m, ou
     assert R.relative_l2(got, expected) <= TOLERANCE
 
 
+@pytest.mark.parametrize("encoding,m,k", [
+    ("q4_k", 1, 4096),    # one launch of the grouped M = 1 kernel
+    ("q4_k", 1, 12288),   # three 4096-column steps per row
+    ("q4_k", 4, 4096),    # M > 1: one launch per matrix
+    ("q6_k", 1, 4096),    # no grouped kernel: one launch per matrix
+    ("q8_0", 2, 2560),
+])
+@pytest.mark.parametrize("count", [1, 2, 3])
+def test_gemv_group_parity(hip_device, encoding, m, k, count):
+    """Grouped GEMV (x shared by up to three matrices) against the oracle, matrix by matrix."""
+    code = Q.ggml_type(encoding)
+    rows = (301, 77, 1040)[:count]  # ragged: the last workgroup of each matrix is partial
+    note("gemv-group", encoding, m, k, rows)
+    x = cases.activation(m, k, 60 + count)
+    raws = [cases.weight(n, k, encoding, 61 + i) for i, n in enumerate(rows)]
+    for out_dtype in ("float16", "float32"):
+        exe = hip_device.load("gguf_gemv_group", encoding=encoding, out_dtype=out_dtype, count=count)
+        xb = hip_device.from_numpy(x)
+        wbs = [hip_device.from_numpy(r) for r in raws]
+        outs = [hip_device.empty((m, n), out_dtype) for n in rows]
+        args = [xb]
+        for wb, out in zip(wbs, outs):
+            hip_device.fill_bytes(out, 0xFF)
+            args += [wb, out]
+        exe.launch(*args)
+        for i, (raw, out, n) in enumerate(zip(raws, outs, rows)):
+            got = out.to_numpy()
+            assert not np.isnan(got).any(), (i, out_dtype)
+            err = R.relative_l2(got, R.gemv_reference(x, raw, code, n, k))
+            assert err <= TOLERANCE, (encoding, i, out_dtype, err)
+            if out_dtype == "float32":
+                assert err <= 2e-4, (encoding, i, err)
+        for b in [xb, *wbs, *outs]:
+            b.release()
+
+
+def test_gemv_group_matches_single_launches(hip_device):
+    """gate + up as one grouped launch equals two gguf_gemv launches bit for bit."""
+    k, rows = 4096, (12288, 12288)
+    note("gemv-group-vs-single", rows, k)
+    x = cases.activation(1, k, 70)
+    raws = [cases.weight(n, k, "q4_k", 71 + i) for i, n in enumerate(rows)]
+    group = hip_device.load("gguf_gemv_group", encoding="q4_k", out_dtype="float16", count=2)
+    xb = hip_device.from_numpy(x)
+    wbs = [hip_device.from_numpy(r) for r in raws]
+    gate, up = group(xb, wbs[0], wbs[1])
+    single = [run_linear(hip_device, "gguf_gemv", "q4_k", x, r, "float16") for r in raws]
+    assert np.array_equal(gate.to_numpy().view(np.uint16), single[0].view(np.uint16))
+    assert np.array_equal(up.to_numpy().view(np.uint16), single[1].view(np.uint16))
+    for b in [xb, *wbs, gate, up]:
+        b.release()
+
+
 @pytest.mark.parametrize("encoding", ["q4_k", "q6_k"])
 def test_gemv_input_families_and_graph_replay(hip_device, encoding):
     """One captured graph, replayed after x changes: random, x*-1.5, zeros."""

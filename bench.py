@@ -115,6 +115,35 @@ def copies_for(bytes_per_rotation_unit):
     return max(2, math.ceil(ROTATION_BYTES / bytes_per_rotation_unit))
 
 
+TIMING = "graph"  # set from --timing in main()
+
+
+def time_launches(device, launches, replays=3):
+    """Median seconds of one pass over ``launches`` (callables), timed with HIP events on the
+    launch stream: replayed from one captured HIP graph (``--timing graph``) or enqueued
+    eagerly on the stream (``--timing eager``)."""
+    if TIMING == "eager":
+        return time_eager(device, launches, replays)
+    return time_graph(device, launches, replays)
+
+
+def time_eager(device, launches, replays=3):
+    for launch in launches:
+        launch()
+    device.synchronize()
+    samples = []
+    for _ in range(replays):
+        start = device.record_event(timing=True)
+        for launch in launches:
+            launch()
+        stop = device.record_event(timing=True)
+        stop.synchronize()
+        samples.append(device.elapsed_ms(start, stop) * 1e-3)
+        start.release()
+        stop.release()
+    return statistics.median(samples)
+
+
 def time_graph(device, launches, replays=3):
     """Capture ``launches`` (callables) into one graph; return the median seconds of one replay."""
     graph = device.graph(lambda: [launch() for launch in launches])
@@ -235,6 +264,8 @@ def main():
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--calibrate", action="store_true",
                         help="first run 5 device copies of 256 MiB (a known-size copy kernel for PMC scaling)")
+    parser.add_argument("--timing", choices=("graph", "eager"), default="graph",
+                        help="replay each timed sequence from a captured HIP graph, or enqueue it eagerly")
     parser.add_argument("--eager-only", action="store_true",
                         help="stop after the eager warmup launches (for per-dispatch counter runs)")
     args = parser.parse_args()
@@ -244,6 +275,8 @@ def main():
         return 2
     if args.steps < 1 or args.warmup < 0:
         parser.error("steps must be >= 1 and warmup >= 0")
+    global TIMING
+    TIMING = args.timing
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import tensor_amd as tx
@@ -277,13 +310,13 @@ def main():
             for layer in mlp:
                 layer.release()
             return 0
-        seconds = time_graph(device, rotated_launches(mlp, args.steps), replays=3)
+        seconds = time_launches(device, rotated_launches(mlp, args.steps), replays=3)
         value = step_bytes * args.steps / seconds / 1e9
         log(f"headline {value:.1f} GB/s, {seconds / args.steps * 1e6:.2f} us/step")
 
         # ---- roofline of the dominant kernel: the grouped gate + up GEMV, 2 x 12288 x 4096, M=1
         launches = 200
-        kernel_s = time_graph(device, [gate_up.calls[i % copies].launch for i in range(launches)]) / launches
+        kernel_s = time_launches(device, [gate_up.calls[i % copies].launch for i in range(launches)]) / launches
         achieved = gate_up.bytes / kernel_s / 1e9
         roofline = {
             "bound": "hbm",
@@ -342,7 +375,7 @@ def run_details(device, x4096, log):
     def gemv_case(name, encoding, m, n, k, out_dtype, launches=60):
         copies = copies_for(weight_bytes(encoding, n, k))
         layer = Linear(device, "gguf_gemv", encoding, m, n, k, out_dtype, copies, 7 + m)
-        seconds = time_graph(device, [layer.calls[i % copies].launch for i in range(launches)]) / launches
+        seconds = time_launches(device, [layer.calls[i % copies].launch for i in range(launches)]) / launches
         gbs = layer.bytes / seconds / 1e9
         details[name] = {"us": round(seconds * 1e6, 3), "GB/s": round(gbs, 1),
                          "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
@@ -355,7 +388,7 @@ def run_details(device, x4096, log):
            Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 3, x=x4096),
            Linear(device, "gguf_gemv", "q4_k", 1, 4096, 12288, "float16", copies, 5)]
     steps = 50
-    seconds = time_graph(device, rotated_launches(mlp, steps)) / steps
+    seconds = time_launches(device, rotated_launches(mlp, steps)) / steps
     step_bytes = sum(layer.bytes for layer in mlp)
     details["C2_step_m1_three_launches"] = {"us": round(seconds * 1e6, 3),
                                             "GB/s": round(step_bytes / seconds / 1e9, 1),
@@ -371,7 +404,7 @@ def run_details(device, x4096, log):
 
     def gemm_case(name, encoding, m, n, k, launches=10):
         layer = Linear(device, "gguf_gemm", encoding, m, n, k, "float16", 2, 9)
-        seconds = time_graph(device, [layer.calls[i % 2].launch for i in range(launches)]) / launches
+        seconds = time_launches(device, [layer.calls[i % 2].launch for i in range(launches)]) / launches
         tflops = layer.flops / seconds / 1e12
         details[name] = {"us": round(seconds * 1e6, 2), "TFLOP/s": round(tflops, 2),
                          "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
@@ -390,7 +423,7 @@ def run_details(device, x4096, log):
         copies = copies_for(layer_weights) if m == 1 else 2
         layers = [Linear(device, kernel, e, m, n, k, "float16", copies, 20 + i) for i, (_, e, n, k) in enumerate(shapes)]
         steps = 20 if m == 1 else 4
-        seconds = time_graph(device, rotated_launches(layers, steps)) / steps
+        seconds = time_launches(device, rotated_launches(layers, steps)) / steps
         total_bytes = sum(layer.bytes for layer in layers)
         total_flops = sum(layer.flops for layer in layers)
         details[f"C5_layer_m{m}"] = {
@@ -409,7 +442,7 @@ def run_details(device, x4096, log):
               GroupLinear(device, "q4_k", 1, [(12288, 4096), (12288, 4096)], "float16", copies, 48, x=x),
               Linear(device, "gguf_gemv", "q6_k", 1, 4096, 12288, "float16", copies, 52)]
     steps = 20
-    seconds = time_graph(device, rotated_launches(layers, steps)) / steps
+    seconds = time_launches(device, rotated_launches(layers, steps)) / steps
     total_bytes = sum(layer.bytes for layer in layers)
     details["C5_layer_m1_grouped"] = {"us": round(seconds * 1e6, 2), "GB/s": round(total_bytes / seconds / 1e9, 1),
                                       "launches": 4}

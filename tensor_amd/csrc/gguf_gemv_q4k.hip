@@ -23,6 +23,8 @@
 //    across the waves of a workgroup and the partial tiles meet in LDS.
 //
 // Block format and element formula: benchmarks/kernels/showcase/triton_kernels.py:143-162.
+#include <algorithm>
+
 #include "gguf_common.h"
 #include "gguf_launch.h"
 
@@ -244,6 +246,128 @@ __global__ __launch_bounds__(SPLIT * 64) void gemv_q4k_mfma(const _Float16* __re
   }
 }
 
+// Multi-tile variant for 2 <= M <= 8 when x fits in LDS (M * K <= kMtMaxMK).
+// A workgroup of W waves owns TILES 16-row tiles; wave w takes the S
+// super-blocks [w S, w S + S) of every tile.  The workgroup first loads all of
+// x, then every weight byte of every wave (pinned above a compiler barrier),
+// and only then stages x in LDS, so the activations are not queued behind the
+// weight stream on the CU.  Per super-block a wave reads its x operands from
+// LDS once and reuses them for all TILES tiles; the K-split partial tiles meet
+// in LDS and are summed in a fixed order.
+constexpr int kMtMaxMK = 65536;     // x of up to 128 KiB in LDS
+constexpr int kMtRowPad = 16;       // bytes after each LDS row of x: rows start in different banks
+
+template <int M, int TILES, int S, typename OutT>
+__global__ __launch_bounds__(1024) void gemv_q4k_mt(const _Float16* __restrict__ x, const uint8_t* __restrict__ w,
+                                                    OutT* __restrict__ out, int n_rows, int k) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int W = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int blocks = k >> 8;
+  const size_t row_bytes = (size_t)blocks * 144;
+  const int xrow_bytes = 2 * k + kMtRowPad;
+  float* partial = reinterpret_cast<float*>(lds);  // [W][TILES][64][4], over x once every wave is done with it
+  constexpr int XCH = 8;  // 16-byte x chunks per thread (M * K / 8 chunks over >= 512 threads)
+  const int chunks = M * k / 8;
+
+  uint4 xr[XCH];
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) {
+    const int c = threadIdx.x + i * (int)blockDim.x;
+    if (c < chunks) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * (size_t)c);
+  }
+  uint4 hd[TILES][S], q0[TILES][S], q1[TILES][S];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) {
+    const int row = min((blockIdx.x * TILES + t) * 16 + n, n_rows - 1);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int b = min(wv * S + s, blocks - 1);
+      const uint8_t* blk = w + (size_t)row * row_bytes + (size_t)b * 144;
+      hd[t][s] = load16(blk);
+      q0[t][s] = load16(blk + 16 + 32 * g);
+      q1[t][s] = load16(blk + 32 + 32 * g);
+    }
+  }
+  asm volatile("" ::: "memory");
+  const int chunks_per_row = k / 8;
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) {
+    const int c = threadIdx.x + i * (int)blockDim.x;
+    if (c < chunks) {
+      const int m = c / chunks_per_row, cc = c - m * chunks_per_row;
+      *reinterpret_cast<uint4*>(lds + m * xrow_bytes + 16 * cc) = xr[i];
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+
+  const PairSelect sel(g);
+  const bool xrow = n < M;  // as the A operand this lane holds activation row m = n
+  const uint8_t* xl = lds + (xrow ? n : 0) * xrow_bytes + 128 * g;
+  float4v_t acc[TILES], accmin[TILES];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) acc[t] = accmin[t] = float4v_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int b = wv * S + s;
+    if (b >= blocks) break;
+    uint4 xa[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      xa[i] = xrow ? *reinterpret_cast<const uint4*>(xl + 512 * b + 16 * i) : make_uint4(0, 0, 0, 0);
+    const float sx_lo = sum16(xa[0], xa[1]) + sum16(xa[2], xa[3]);
+    const float sx_hi = sum16(xa[4], xa[5]) + sum16(xa[6], xa[7]);
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      uint32_t scs, mns;
+      sel.codes(hd[t][s], scs, mns);
+      const float sc_lo = (float)(scs & 0xFF), sc_hi = (float)(scs >> 8);
+      // low: (1024 + q) sc - 1024 sc = sc q;  high: (1024 + 16 q) sc / 16 - 64 sc = sc q  (exact)
+      const uint32_t mul_lo = half2_splat(sc_lo), add_lo = half2_splat(-1024.0f * sc_lo);
+      const uint32_t mul_hi = half2_splat(sc_hi * 0.0625f), add_hi = half2_splat(-64.0f * sc_hi);
+      float4v_t cs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int v = 2 * (u & 3);
+        const uint32_t wa = word(v < 4 ? q0[t][s] : q1[t][s], v & 3), wb = word(v < 4 ? q0[t][s] : q1[t][s], (v & 3) + 1);
+        const uint32_t mask = u < 4 ? 0x0F0F0F0Fu : 0xF0F0F0F0u;
+        const uint32_t mul = u < 4 ? mul_lo : mul_hi, add = u < 4 ? add_lo : add_hi;
+        const uint32_t ca = wa & mask, cb = wb & mask;
+        const uint4 bv = make_uint4(pk_fma(magic01(ca), mul, add), pk_fma(magic23(ca), mul, add),
+                                    pk_fma(magic01(cb), mul, add), pk_fma(magic23(cb), mul, add));
+        cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, xa[u]),
+                                                    __builtin_bit_cast(half8_t, bv), cs, 0, 0, 0);
+      }
+      const float d = half_bits_to_float(hd[t][s].x), dmin = half_bits_to_float(hd[t][s].x >> 16);
+      acc[t] += d * cs;
+      accmin[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(sx_lo, dmin * (float)(mns & 0xFF), accmin[t], 0, 0, 0);
+      accmin[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(sx_hi, dmin * (float)(mns >> 8), accmin[t], 0, 0, 0);
+    }
+  }
+  __syncthreads();  // every wave has read its last x operands
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) {
+    const float4v_t total = acc[t] - accmin[t];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) partial[((wv * TILES + t) * 64 + lane) * 4 + i] = total[i];
+  }
+  __syncthreads();
+  // wave t sums tile t over the W K-slices in order and stores it
+  for (int t = wv; t < TILES; t += W) {
+    const int col = (blockIdx.x * TILES + t) * 16 + n;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = 0.f;
+      for (int p = 0; p < W; ++p) v += partial[((p * TILES + t) * 64 + lane) * 4 + i];
+      const int m = 4 * g + i;
+      if (m < M && col < n_rows) store_out<OutT>(out, (size_t)m * n_rows + col, v);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- launch ---
 
 template <int MATS, typename OutT>
@@ -291,18 +415,44 @@ static hipError_t launch_mfma(const GemvArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <int M, int TILES, int S, typename OutT>
+static hipError_t launch_mt_cfg(const GemvArgs& a, hipStream_t stream) {
+  const int blocks = a.k / 256, waves = (blocks + S - 1) / S;
+  const int tiles = (a.n + 16 * TILES - 1) / (16 * TILES);
+  const size_t lds = std::max((size_t)M * (2 * a.k + kMtRowPad), (size_t)waves * TILES * 64 * 4 * sizeof(float));
+  hipLaunchKernelGGL((gemv_q4k_mt<M, TILES, S, OutT>), dim3(tiles), dim3(waves * 64), lds, stream,
+                     static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out),
+                     a.n, a.k);
+  return hipGetLastError();
+}
+
+// x in LDS when it fits; 2 super-blocks per wave up to K = 8192, 3 up to K = 12288.
+template <int M, typename OutT>
+static hipError_t launch_mt(const GemvArgs& a, hipStream_t stream, bool* handled) {
+  const int blocks = a.k / 256;
+  const int s = blocks <= 32 ? 2 : 3, waves = (blocks + s - 1) / s;
+  // the kernel assumes at most 16 waves and at most 8 x chunks per thread
+  *handled = a.k % 256 == 0 && M * a.k <= kMtMaxMK && waves <= 16 && M * a.k / 8 <= waves * 64 * 8;
+  if (!*handled) return hipSuccess;
+  const bool wide = a.n >= 8192;
+  if (s == 2) return wide ? launch_mt_cfg<M, 2, 2, OutT>(a, stream) : launch_mt_cfg<M, 1, 2, OutT>(a, stream);
+  return wide ? launch_mt_cfg<M, 2, 3, OutT>(a, stream) : launch_mt_cfg<M, 1, 3, OutT>(a, stream);
+}
+
 template <typename OutT>
 static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream, bool* handled) {
   *handled = true;
   if (a.m == 1 && a.k % 4096 == 0 && a.k <= 4 * 4096) return launch_m1_group<OutT>(&a, 1, stream);
+  hipError_t status = hipSuccess;
+  bool mt = false;
   switch (a.m) {
-    case 2: return launch_mfma<2, OutT>(a, stream);
-    case 3: return launch_mfma<3, OutT>(a, stream);
-    case 4: return launch_mfma<4, OutT>(a, stream);
-    case 5: return launch_mfma<5, OutT>(a, stream);
-    case 6: return launch_mfma<6, OutT>(a, stream);
-    case 7: return launch_mfma<7, OutT>(a, stream);
-    case 8: return launch_mfma<8, OutT>(a, stream);
+    case 2: status = launch_mt<2, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<2, OutT>(a, stream); return status;
+    case 3: status = launch_mt<3, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<3, OutT>(a, stream); return status;
+    case 4: status = launch_mt<4, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<4, OutT>(a, stream); return status;
+    case 5: status = launch_mt<5, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<5, OutT>(a, stream); return status;
+    case 6: status = launch_mt<6, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<6, OutT>(a, stream); return status;
+    case 7: status = launch_mt<7, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<7, OutT>(a, stream); return status;
+    case 8: status = launch_mt<8, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<8, OutT>(a, stream); return status;
     default: *handled = false; return hipSuccess;
   }
 }

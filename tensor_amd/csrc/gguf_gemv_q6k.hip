@@ -1,10 +1,10 @@
 // Q6_K decode GEMV fast path (gfx950) for M = 1 and K a multiple of 4096,
 // the LM-head and down-projection shapes: out[n] = sum_k x[k] * W[n, k].
 //
-// A 256-thread workgroup issues the loads of its rows first, then stages x
-// once in LDS (padded 16 B per 128 B, conflict-free b128 reads) behind a
-// single barrier, so the activation vector is read from L2 once per 16 (or 8)
-// rows instead of once per wave.  Lane plan as the generic kernel: four lanes
+// A workgroup of 8 waves, one row each, loads the activation vector first, then
+// every weight byte of its rows, and stages x once in LDS (padded 16 B per
+// 128 B, conflict-free b128 reads) behind a single LDS-only barrier, so the
+// activation vector is read from L2 once per 8 rows instead of once per wave.  Lane plan as the generic kernel: four lanes
 // per 210-byte super-block (half hh, 16-element offset l0), sixteen
 // super-blocks per step; each lane rebuilds its 64 six-bit codes with byte
 // masks and multiplies "1024 + q" fp16 codes with v_dot2_f32_f16, removing
@@ -16,8 +16,6 @@
 
 namespace tensor_gguf {
 
-constexpr int kQ6Waves = 4;
-
 __device__ __forceinline__ float q6_wave_sum(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
   v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
@@ -28,16 +26,26 @@ __device__ __forceinline__ float q6_wave_sum(float v) {
   return v;
 }
 
-template <int R, int STEPS, typename OutT>
-__global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6k_lds(const _Float16* __restrict__ x,
-                                                              const uint8_t* __restrict__ w,
-                                                              OutT* __restrict__ out, int n_rows) {
+template <int R, int STEPS, int WAVES, typename OutT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __restrict__ x,
+                                                           const uint8_t* __restrict__ w,
+                                                           OutT* __restrict__ out, int n_rows) {
   constexpr int K = STEPS * 4096;
   constexpr int ROW_BYTES = STEPS * 16 * 210;
+  constexpr int T = WAVES * 64, XC = (K / 8 + T - 1) / T;  // 16-byte x chunks per thread
   __shared__ __attribute__((aligned(16))) uint8_t xlds[K * 2 + K / 4];
   const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * kQ6Waves + (threadIdx.x >> 6)) * R;
+  const int row0 = (blockIdx.x * WAVES + (threadIdx.x >> 6)) * R;
   const int slot = lane >> 2, part = lane & 3, hh = part >> 1, l0 = 16 * (part & 1);
+  // x first, then every weight load of the wave, pinned above a compiler barrier: on each CU
+  // the small x load is not queued behind weight traffic, and the workgroup barrier below
+  // fences LDS only, so decoding starts as soon as this wave's own bytes have arrived
+  uint4 xr[XC];
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    if (c < K / 8) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * c);
+  }
   uint4 qa[R][STEPS], qb[R][STEPS], qh[R][STEPS];
   uint2 sc8[R][STEPS];
   uint32_t dw[R][STEPS];
@@ -54,9 +62,15 @@ __global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6k_lds(const _Float16* __
       dw[r][s] = load4(block + 206);  // high half: d
     }
   }
-  for (int c = threadIdx.x; c < K / 8; c += kQ6Waves * 64)
-    *reinterpret_cast<uint4*>(xlds + 16 * c + 16 * (c >> 3)) = load16(reinterpret_cast<const uint8_t*>(x) + 16 * c);
-  __syncthreads();
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    if (c < K / 8) *reinterpret_cast<uint4*>(xlds + 16 * c + 16 * (c >> 3)) = xr[i];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   if (row0 >= n_rows) return;
   float acc[R];
 #pragma unroll
@@ -112,10 +126,10 @@ __global__ __launch_bounds__(kQ6Waves * 64) void gemv_q6k_lds(const _Float16* __
   }
 }
 
-template <int R, int STEPS, typename OutT>
+template <int R, int STEPS, int WAVES, typename OutT>
 static hipError_t launch_q6k(const GemvArgs& a, hipStream_t stream) {
-  constexpr int per_block = kQ6Waves * R;
-  hipLaunchKernelGGL((gemv_q6k_lds<R, STEPS, OutT>), dim3((a.n + per_block - 1) / per_block), dim3(kQ6Waves * 64), 0,
+  constexpr int per_block = WAVES * R;
+  hipLaunchKernelGGL((gemv_q6k_lds<R, STEPS, WAVES, OutT>), dim3((a.n + per_block - 1) / per_block), dim3(WAVES * 64), 0,
                      stream, static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w),
                      static_cast<OutT*>(a.out), a.n);
   return hipGetLastError();
@@ -125,9 +139,9 @@ template <typename OutT>
 static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream, bool* handled) {
   *handled = true;
   switch (a.k) {
-    case 4096: return launch_q6k<4, 1, OutT>(a, stream);
-    case 8192: return launch_q6k<2, 2, OutT>(a, stream);
-    case 12288: return launch_q6k<2, 3, OutT>(a, stream);
+    case 4096: return launch_q6k<1, 1, 8, OutT>(a, stream);
+    case 8192: return launch_q6k<1, 2, 8, OutT>(a, stream);
+    case 12288: return launch_q6k<1, 3, 8, OutT>(a, stream);
     default: *handled = false; return hipSuccess;
   }
 }

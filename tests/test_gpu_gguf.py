@@ -119,6 +119,29 @@ def test_gemv_parity_baseline_shapes(hip_device, c_oracle, encoding, n, k, m, ou
     assert R.relative_l2(got, expected) <= TOLERANCE
 
 
+@pytest.mark.parametrize("m,n,k", [
+    (8, 8200, 4096),    # two 16-row tiles per wave, ragged last tile pair
+    (5, 4100, 12288),   # three super-blocks per wave, x of 120 KiB in LDS
+    (3, 9000, 2560),    # five waves per workgroup (ten super-blocks)
+    (2, 40, 256),       # one super-block, one wave
+    (4, 8200, 512),     # two tiles per wave and a single wave: the wave stores both tiles
+    (8, 1024, 12288),   # x too large for LDS: the one-super-block-per-step kernel
+])
+def test_gemv_q4k_multirow_configurations(hip_device, m, n, k):
+    code = Q.ggml_type("q4_k")
+    note("gemv-multirow", m, n, k)
+    raw = cases.weight(n, k, "q4_k", 80 + m)
+    x = cases.activation(m, k, 90 + m)
+    expected = R.gemv_reference(x, raw, code, n, k)
+    for out_dtype in ("float16", "float32"):
+        got = run_linear(hip_device, "gguf_gemv", "q4_k", x, raw, out_dtype)
+        assert not np.isnan(got).any(), out_dtype
+        err = R.relative_l2(got, expected)
+        assert err <= TOLERANCE, (m, n, k, out_dtype, err)
+        if out_dtype == "float32":
+            assert err <= 2e-4, (m, n, k, err)
+
+
 @pytest.mark.parametrize("encoding,m,k", [
     ("q4_k", 1, 4096),    # one launch of the grouped M = 1 kernel
     ("q4_k", 1, 12288),   # three 4096-column steps per row

@@ -8,7 +8,8 @@
 // with fp32 accumulators) with a deeper software pipeline:
 //
 //   * two register sets of raw bytes: step s+1 is dequantized into LDS while
-//     step s+2 is in flight from HBM and step s is multiplied;
+//     step s+2 is in flight from HBM and step s is multiplied (a four-set ring
+//     measured no faster: the steps are not bound by load latency);
 //   * the LDS double buffer as two arrays, so the compiler may overlap the
 //     staging stores of one buffer with the fragment reads of the other;
 //   * each step is one straight-line region in which sched_group_barrier
@@ -59,21 +60,29 @@ struct Geometry<kQ6_K, TPR> {
   static constexpr int W0 = EPT / 4, W1 = EPT / 4 + 2;  // ql dwords; qh dwords + scales + d
 };
 
+// Raw bytes of one step in vector registers (vector values stay in VGPRs; arrays of
+// several sets were demoted to the stack). x: XL 16-byte activation chunks.
 template <int XL, int W0, int W1>
 struct Raw {
-  uint4 x[XL];
-  uint32_t a[W0];
-  uint32_t b[W1];
+  typedef uint32_t XV __attribute__((ext_vector_type(4 * XL)));
+  typedef uint32_t AV __attribute__((ext_vector_type(W0)));
+  typedef uint32_t BV __attribute__((ext_vector_type(W1)));
+  XV x;
+  AV a;
+  BV b;
 };
 
 }  // namespace pipe
 
-template <int TYPE, int BM, int BN, int WM, int WN, typename OutT>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_pipe(const _Float16* __restrict__ x,
-                                                          const uint8_t* __restrict__ w,
-                                                          OutT* __restrict__ out, int M, int N, int K) {
+// KS groups of WM x WN waves split K: group g takes steps [g S, g S + S), S = steps / KS,
+// with its own LDS staging buffers; the KS partial tiles are summed in LDS at the end
+// (KS = 1: the whole K range in one group).
+template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT>
+__global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const _Float16* __restrict__ x,
+                                                               const uint8_t* __restrict__ w,
+                                                               OutT* __restrict__ out, int M, int N, int K) {
   using namespace pipe;
-  constexpr int THREADS = WM * WN * 64;
+  constexpr int THREADS = WM * WN * 64;  // per K group
   constexpr int MT = BM / WM / 16, NT = BN / WN / 16;
   constexpr int XL = BM * 8 / THREADS;  // 16-byte activation chunks per thread per step
   constexpr int TPR = THREADS / BN;     // threads per weight row
@@ -81,23 +90,30 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_pipe(const _Float16* __rest
   using G = Geometry<TYPE, TPR>;
   using RawT = Raw<XL, G::W0, G::W1>;
   constexpr int BYTES = TYPE == kQ4_K ? 144 : 210;
-  __shared__ __attribute__((aligned(16))) _Float16 xs0[BM * ROW], xs1[BM * ROW];
-  __shared__ __attribute__((aligned(16))) _Float16 ws0[BN * ROW], ws1[BN * ROW];
+  constexpr int STAGE = 2 * (BM + BN) * ROW;  // halves of one group's double-buffered tiles
+  __shared__ __attribute__((aligned(16))) _Float16 stage[KS * STAGE];
+  const int group = threadIdx.x / THREADS;
+  _Float16* const xs0 = stage + group * STAGE;
+  _Float16* const xs1 = xs0 + BM * ROW;
+  _Float16* const ws0 = xs1 + BM * ROW;
+  _Float16* const ws1 = ws0 + BN * ROW;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x % THREADS, lane = tid & 63, wave = tid >> 6;
   const int wm = (wave / WN) * (16 * MT), wn = (wave % WN) * (16 * NT);
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int wrow = tid / TPR, wpart = tid % TPR;
   const uint8_t* wbase = w + (size_t)min(n0 + wrow, N - 1) * (size_t)(K >> 8) * BYTES;
-  const int steps = K / BK;  // a multiple of 4: K is whole super-blocks
+  // this group's steps; the host guarantees steps % (4 KS) == 0, so each group starts on a super-block
+  const int steps = K / BK / KS, first = group * steps;
 
   auto load = [&](RawT& r, int step) {
     const int k0 = step * BK;
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
       const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
-      r.x[i] = (m0 + row < M) ? *reinterpret_cast<const uint4*>(x + (size_t)(m0 + row) * K + k0 + c8)
-                              : make_uint4(0, 0, 0, 0);
+      // rows past M reload row M - 1: their products land in output rows that are never stored
+      const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)min(m0 + row, M - 1) * K + k0 + c8);
+      r.x[4 * i] = v.x; r.x[4 * i + 1] = v.y; r.x[4 * i + 2] = v.z; r.x[4 * i + 3] = v.w;
     }
     const uint8_t* blk = wbase + (size_t)(k0 >> 8) * BYTES;
     if constexpr (TYPE == kQ4_K) {
@@ -125,7 +141,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_pipe(const _Float16* __rest
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
       const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
-      *reinterpret_cast<uint4*>(&xs[row * ROW + c8]) = r.x[i];
+      *reinterpret_cast<uint4*>(&xs[row * ROW + c8]) = make_uint4(r.x[4 * i], r.x[4 * i + 1], r.x[4 * i + 2], r.x[4 * i + 3]);
     }
     if constexpr (TYPE == kQ4_K) {
       int sc_lo, mn_lo, sc_hi, mn_hi;
@@ -198,19 +214,42 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_pipe(const _Float16* __rest
     }
   };
 
+  // two register sets of raw bytes: step s+1 is staged into LDS while step s+2 is fetched
   RawT ra, rb;
-  load(ra, 0);
-  load(rb, 1);
-  store(ra, xs0, ws0, 0);
+  const int last = first + steps - 1;
+  load(ra, first);
+  load(rb, first + 1);
+  store(ra, xs0, ws0, first);
   __syncthreads();
-  for (int step = 0; step < steps; step += 2) {
-    // even step: compute buffer 0, stage step+1 into buffer 1, fetch step+2
-    step_body(xs0, ws0, xs1, ws1, rb, step + 1, ra, min(step + 2, steps - 1));
+  for (int step = first; step < first + steps; step += 2) {
+    // the last step stages and fetches clamped copies that are never read
+    step_body(xs0, ws0, xs1, ws1, rb, step + 1, ra, min(step + 2, last));
     __syncthreads();
-    // odd step: compute buffer 1, stage step+2 into buffer 0, fetch step+3
-    // (past the end the staged and fetched data are clamped copies, never read)
-    step_body(xs1, ws1, xs0, ws0, ra, min(step + 2, steps - 1), rb, min(step + 3, steps - 1));
+    step_body(xs1, ws1, xs0, ws0, ra, min(step + 2, last), rb, min(step + 3, last));
     __syncthreads();
+  }
+  if constexpr (KS > 1) {
+    // partial tiles of groups 1 .. KS-1 -> LDS (over the staging buffers), summed by group 0
+    float* red = reinterpret_cast<float*>(stage);
+    static_assert((KS - 1) * MT * NT * 4 * THREADS * 4 <= KS * STAGE * 2, "reduction buffer");
+    if (group > 0) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) red[(((group - 1) * MT + i) * NT + j) * 4 * THREADS + e * THREADS + tid] = acc[i][j][e];
+    }
+    __syncthreads();
+    if (group > 0) return;
+#pragma unroll
+    for (int g = 1; g < KS; ++g)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i][j][e] += red[(((g - 1) * MT + i) * NT + j) * 4 * THREADS + e * THREADS + tid];
   }
 #pragma unroll
   for (int i = 0; i < MT; ++i)
@@ -225,17 +264,20 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_pipe(const _Float16* __rest
     }
 }
 
-template <int TYPE, int BM, int BN, int WM, int WN, typename OutT>
+template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT>
 static hipError_t launch_pipe(const GemvArgs& a, hipStream_t stream) {
-  const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM), block(WM * WN * 64);
-  hipLaunchKernelGGL((gemm_pipe<TYPE, BM, BN, WM, WN, OutT>), grid, block, 0, stream,
+  const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM), block(WM * WN * 64 * KS);
+  hipLaunchKernelGGL((gemm_pipe<TYPE, BM, BN, WM, WN, KS, OutT>), grid, block, 0, stream,
                      static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w),
                      static_cast<OutT*>(a.out), a.m, a.n, a.k);
   return hipGetLastError();
 }
 
 // Largest tile that still gives the 256 CUs work: the workgroup count of a
-// tile must reach kMinBlocks, else the next smaller tile is taken.
+// tile must reach kMinBlocks, else a smaller tile is taken, and below 256 x 128
+// the K range is split over two or four wave groups of one workgroup so that
+// every SIMD holds at least one wave (measured at M = 256: 1.4x to 4x faster
+// than the unsplit tiles for the q/k/v/o, gate/up and down shapes).
 constexpr long kMinBlocks = 160;
 
 static long tile_blocks(const GemvArgs& a, int bm, int bn) {
@@ -244,10 +286,40 @@ static long tile_blocks(const GemvArgs& a, int bm, int bn) {
 
 template <int TYPE, typename OutT>
 static hipError_t launch_type(const GemvArgs& a, hipStream_t stream) {
-  if (tile_blocks(a, 256, 128) >= kMinBlocks) return launch_pipe<TYPE, 256, 128, 4, 2, OutT>(a, stream);
-  if (tile_blocks(a, 128, 128) >= kMinBlocks) return launch_pipe<TYPE, 128, 128, 2, 2, OutT>(a, stream);
-  if (tile_blocks(a, 128, 64) >= kMinBlocks) return launch_pipe<TYPE, 128, 64, 2, 2, OutT>(a, stream);
-  return launch_pipe<TYPE, 64, 64, 1, 2, OutT>(a, stream);
+  const int steps = a.k / pipe::BK;  // a multiple of 4 (K is whole super-blocks)
+  if (tile_blocks(a, 256, 128) >= kMinBlocks) return launch_pipe<TYPE, 256, 128, 4, 2, 1, OutT>(a, stream);
+  if (tile_blocks(a, 128, 128) >= kMinBlocks)
+    return steps % 8 == 0 ? launch_pipe<TYPE, 128, 128, 2, 2, 2, OutT>(a, stream)
+                          : launch_pipe<TYPE, 128, 128, 2, 2, 1, OutT>(a, stream);
+  if (steps % 16 == 0) return launch_pipe<TYPE, 64, 64, 1, 2, 4, OutT>(a, stream);
+  if (steps % 8 == 0) return launch_pipe<TYPE, 64, 64, 1, 2, 2, OutT>(a, stream);
+  if (tile_blocks(a, 128, 64) >= kMinBlocks) return launch_pipe<TYPE, 128, 64, 2, 2, 1, OutT>(a, stream);
+  return launch_pipe<TYPE, 64, 64, 1, 2, 1, OutT>(a, stream);
+}
+
+// Tile configuration by index, for sweeps: 0..3 the KS = 1 tiles above, 4..7 with K split
+// (LDS holds one double-buffered stage per group: 128 x 128 and 128 x 64 take KS <= 2, 64 x 64 KS <= 4).
+template <int TYPE, typename OutT>
+static hipError_t launch_config(const GemvArgs& a, hipStream_t stream, int config) {
+  const int steps = a.k / pipe::BK;
+  auto ks_ok = [&](int ks) { return steps % (4 * ks) == 0; };
+  switch (config) {
+    case 0: return launch_pipe<TYPE, 256, 128, 4, 2, 1, OutT>(a, stream);
+    case 1: return launch_pipe<TYPE, 128, 128, 2, 2, 1, OutT>(a, stream);
+    case 2: return launch_pipe<TYPE, 128, 64, 2, 2, 1, OutT>(a, stream);
+    case 3: return launch_pipe<TYPE, 64, 64, 1, 2, 1, OutT>(a, stream);
+    case 4: return ks_ok(2) ? launch_pipe<TYPE, 128, 128, 2, 2, 2, OutT>(a, stream) : hipErrorInvalidValue;
+    case 5: return ks_ok(2) ? launch_pipe<TYPE, 128, 64, 2, 2, 2, OutT>(a, stream) : hipErrorInvalidValue;
+    case 6: return ks_ok(2) ? launch_pipe<TYPE, 64, 64, 1, 2, 2, OutT>(a, stream) : hipErrorInvalidValue;
+    case 7: return ks_ok(4) ? launch_pipe<TYPE, 64, 64, 1, 2, 4, OutT>(a, stream) : hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemm_pipe_config(const GemvArgs& a, hipStream_t stream, int config) {
+  if (a.type == kQ4_K) return a.out_half ? launch_config<kQ4_K, _Float16>(a, stream, config) : launch_config<kQ4_K, float>(a, stream, config);
+  if (a.type == kQ6_K) return a.out_half ? launch_config<kQ6_K, _Float16>(a, stream, config) : launch_config<kQ6_K, float>(a, stream, config);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm_pipe(const GemvArgs& a, hipStream_t stream, bool* handled) {

@@ -56,5 +56,7 @@ hipError_t launch_gemm(const GemvArgs& args, hipStream_t stream);
 // Pipelined dequant-GEMM for Q4_K and Q6_K (K a multiple of 256); sets
 // *handled to false for the encodings it does not cover.
 hipError_t launch_gemm_pipe(const GemvArgs& args, hipStream_t stream, bool* handled);
+// One tile configuration of the pipelined GEMM by index (tile sweeps and tests).
+hipError_t launch_gemm_pipe_config(const GemvArgs& args, hipStream_t stream, int config);
 
 }  // namespace tensor_gguf

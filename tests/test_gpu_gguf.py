@@ -272,11 +272,18 @@ def test_gemm_parity_baseline_shapes(hip_device, c_oracle, encoding, m, n, k):
 
 
 @pytest.mark.parametrize("encoding", ["q4_k", "q6_k"])
-@pytest.mark.parametrize("m,n", [(384, 7168), (256, 9984), (40, 1000)])
-def test_gemm_tile_configurations(hip_device, c_oracle, encoding, m, n):
-    """Shapes that select the 128x128, 128x64 and 64x64 (ragged N) workgroup tiles."""
+@pytest.mark.parametrize("m,n,k", [
+    (384, 7168, 512),    # 128x128 tile, K split over 2 wave groups
+    (520, 4096, 512),    # 128x128, K split 2, ragged M
+    (384, 7168, 768),    # 128x128 unsplit (12 K steps do not split evenly)
+    (256, 9984, 768),    # 128x64 unsplit
+    (40, 1000, 768),     # 64x64 unsplit, ragged N
+    (40, 1000, 512),     # 64x64, K split 2
+    (256, 9984, 1024),   # 64x64, K split 4
+])
+def test_gemm_tile_configurations(hip_device, c_oracle, encoding, m, n, k):
+    """Shapes that select each workgroup tile and K split of the prefill kernel."""
     code = Q.ggml_type(encoding)
-    k = 512
     note("gemm-tiles", encoding, m, n, k)
     raw = cases.weight(n, k, encoding, 93)
     x = cases.activation(m, k, 94)

@@ -31,16 +31,27 @@ namespace tensor_gguf {
 namespace pipe {
 
 constexpr int BK = 64, ROW = 80;  // halves per LDS row (16-byte aligned, padded)
+constexpr float kTwo24 = 16777216.0f;
 
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
   const _Float16 ha = (_Float16)a, hb = (_Float16)b;
   return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
 }
 
-// fp16 pairs of scale * code + bias for the four byte codes of `codes`.
-__device__ __forceinline__ uint2 affine4(uint32_t codes, float scale, float bias) {
-  return make_uint2(pack2(fmaf(scale, (float)(codes & 0xFFu), bias), fmaf(scale, (float)((codes >> 8) & 0xFFu), bias)),
-                    pack2(fmaf(scale, (float)((codes >> 16) & 0xFFu), bias), fmaf(scale, (float)(codes >> 24), bias)));
+// fp16(scale * q + bias) for four codes q < 1024 given as fp16 subnormal pairs
+// p02 = (q0, q2) * 2^-24 and p13 = (q1, q3) * 2^-24 (a code masked into the low
+// bits of a half is that subnormal exactly). With scale24 = scale * 2^24 each
+// product is exactly scale * q, the fma rounds once to fp32 as fmaf(scale, q,
+// bias) does, and the result rounds to fp16: one v_fma_mix per element, the
+// pairs packed by the lo/hi forms of the instruction.
+__device__ __forceinline__ uint2 affine4(uint32_t p02, uint32_t p13, float scale24, float bias) {
+  const half2_t a = as_half2(p02), b = as_half2(p13);
+  half2_t e01, e23;
+  e01[0] = (_Float16)fmaf((float)a[0], scale24, bias);
+  e01[1] = (_Float16)fmaf((float)b[0], scale24, bias);
+  e23[0] = (_Float16)fmaf((float)a[1], scale24, bias);
+  e23[1] = (_Float16)fmaf((float)b[1], scale24, bias);
+  return make_uint2(__builtin_bit_cast(uint32_t, e01), __builtin_bit_cast(uint32_t, e23));
 }
 
 template <int TYPE, int TPR>
@@ -92,7 +103,9 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const _Float16* _
   constexpr int BYTES = TYPE == kQ4_K ? 144 : 210;
   constexpr int STAGE = 2 * (BM + BN) * ROW;  // halves of one group's double-buffered tiles
   __shared__ __attribute__((aligned(16))) _Float16 stage[KS * STAGE];
-  const int group = threadIdx.x / THREADS;
+  // wave-uniform (THREADS is a multiple of 64): keeps the step counter and the
+  // addressing derived from it in scalar registers
+  const int group = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x / THREADS);
   _Float16* const xs0 = stage + group * STAGE;
   _Float16* const xs1 = xs0 + BM * ROW;
   _Float16* const ws0 = xs1 + BM * ROW;
@@ -148,13 +161,15 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const _Float16* _
       q4k_scale_pair(r.b[1], r.b[2], r.b[3], step & 3, sc_lo, mn_lo, sc_hi, mn_hi);
       const float d = half_bits_to_float(r.b[0]), dmin = half_bits_to_float(r.b[0] >> 16);
       // d*sc*q - dmin*m: the product is exact, the subtraction rounds once
-      const float ds_lo = d * (float)sc_lo, dm_lo = -(dmin * (float)mn_lo);
-      const float ds_hi = d * (float)sc_hi, dm_hi = -(dmin * (float)mn_hi);
+      const float ds_lo = d * (float)sc_lo * kTwo24, dm_lo = -(dmin * (float)mn_lo);
+      const float ds_hi = d * (float)sc_hi * kTwo24, dm_hi = -(dmin * (float)mn_hi);
       _Float16* dst = &ws[wrow * ROW + G::QB * wpart];
 #pragma unroll
       for (int i = 0; i < G::W0; ++i) {
-        *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(r.a[i] & 0x0F0F0F0Fu, ds_lo, dm_lo);
-        *reinterpret_cast<uint2*>(dst + 32 + 4 * i) = affine4((r.a[i] >> 4) & 0x0F0F0F0Fu, ds_hi, dm_hi);
+        const uint32_t q = r.a[i];  // low nibbles: sub-block 2j, high nibbles: 2j+1
+        *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(q & 0x000F000Fu, (q >> 8) & 0x000F000Fu, ds_lo, dm_lo);
+        *reinterpret_cast<uint2*>(dst + 32 + 4 * i) =
+            affine4((q >> 4) & 0x000F000Fu, (q >> 12) & 0x000F000Fu, ds_hi, dm_hi);
       }
     } else {
       const int e0 = G::EPT * wpart;
@@ -166,11 +181,13 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const _Float16* _
         // 6-bit codes of elements l0 + 4i .. + 3 of this quarter
         const uint32_t lo = (r.a[i] >> (4 * (step & 1))) & 0x0F0F0F0Fu;
         const uint32_t hi = ((r.b[i] >> (2 * quarter)) & 0x03030303u) << 4;
+        const uint32_t q = lo | hi;
         // scale index 8h + 2 quarter + l / 16: byte l / 16 of the dword loaded at 2 quarter
         const float sc = (float)(int8_t)(r.b[G::W0] >> (8 * ((l0 + 4 * i) >> 4)));
         // (q - 32) * sc * d == q * (sc d) - 32 (sc d): exact, one fused rounding
         const float scd = sc * d;
-        *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(lo | hi, scd, -32.0f * scd);
+        *reinterpret_cast<uint2*>(dst + 4 * i) =
+            affine4(q & 0x003F003Fu, (q >> 8) & 0x003F003Fu, scd * kTwo24, -32.0f * scd);
       }
     }
   };

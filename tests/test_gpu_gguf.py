@@ -293,6 +293,28 @@ def test_gemm_tile_configurations(hip_device, c_oracle, encoding, m, n, k):
     assert R.relative_l2(got, expected) <= 1e-5
 
 
+@pytest.mark.parametrize("encoding", ["q4_k", "q6_k"])
+@pytest.mark.parametrize("k,n", [
+    (512, 10240),   # 256x128 tile
+    (1024, 2560),   # 128x128, K split 2
+    (512, 1024),    # 64x64, K split 2
+    (768, 320),     # 64x64 unsplit, ragged N
+])
+def test_gemm_one_hot_rows_give_dequantized_weights(hip_device, c_oracle, encoding, k, n):
+    """Row m of x selects column perm[m] of W, so out[m, n] = fp16(dequant(W))[n, perm[m]]
+    exactly: every staged weight of every code and scale is checked bit for bit."""
+    code = Q.ggml_type(encoding)
+    note("gemm-one-hot", encoding, k, n)
+    raw = cases.random_blocks(encoding, n, k, 96)
+    deq = c_oracle.dequantize(raw, code, n, k).astype(np.float16).astype(np.float32)
+    perm = np.random.default_rng(97).permutation(k)
+    x = np.zeros((k, k), np.float16)
+    x[np.arange(k), perm] = 1.0
+    got = run_linear(hip_device, "gguf_gemm", encoding, x, raw, "float32")
+    # the fp32 sum of one exact product and zeros is that product (a -0.0 weight reads +0.0)
+    assert np.array_equal(got, deq[:, perm].T), encoding
+
+
 def test_gemm_zero_input_gives_exact_zero(hip_device):
     raw = cases.weight(128, 512, "q4_k", 95)
     x = np.zeros((64, 512), np.float16)

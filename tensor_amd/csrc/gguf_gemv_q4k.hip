@@ -74,15 +74,16 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // in LDS with the halves of every 4-element group reordered (x0, x2, x1, x3).
 constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
 
-// One wave = one weight row; 16 waves = 16 consecutive rows of one matrix of
-// the group.  The activation vector is loaded first, then every weight load of
-// the wave, so that on each CU the small x load is not queued behind weight
-// traffic; a compiler barrier keeps the weight loads from sinking below the
-// x staging, and the workgroup barrier fences LDS only, so decoding starts as
-// soon as this wave's own bytes have arrived.
-template <int STEPS, int MATS, typename OutT>
-__global__ __launch_bounds__(kM1Waves * 64) void gemv_q4k_m1(const _Float16* __restrict__ x, GemvGroup<OutT> g) {
-  constexpr int K = STEPS * 4096, ROW_BYTES = STEPS * 16 * 144, T = kM1Waves * 64;
+// One wave = one weight row; the WAVES waves of a workgroup = WAVES
+// consecutive rows of one matrix of the group.  The activation vector is
+// loaded first, then every weight load of the wave, so that on each CU the
+// small x load is not queued behind weight traffic; a compiler barrier keeps
+// the weight loads from sinking below the x staging, and the workgroup
+// barrier fences LDS only, so decoding starts as soon as this wave's own
+// bytes have arrived.
+template <int STEPS, int WAVES, int MATS, typename OutT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __restrict__ x, GemvGroup<OutT> g) {
+  constexpr int K = STEPS * 4096, ROW_BYTES = STEPS * 16 * 144, T = WAVES * 64;
   constexpr int XC = (K / 8 + T - 1) / T;  // 16-byte x chunks per thread
   __shared__ __attribute__((aligned(16))) uint8_t xlds[K * 2 + K / 4];
   __shared__ __attribute__((aligned(16))) float sxl[K / 32];
@@ -95,7 +96,7 @@ __global__ __launch_bounds__(kM1Waves * 64) void gemv_q4k_m1(const _Float16* __r
     mat = i;
   }
   const int n_rows = g.n[mat];
-  const int row = block * kM1Waves + (threadIdx.x >> 6);
+  const int row = block * WAVES + (threadIdx.x >> 6);
   const int slot = lane >> 2, j = lane & 3;
 
   uint4 xr[XC];
@@ -140,25 +141,34 @@ __global__ __launch_bounds__(kM1Waves * 64) void gemv_q4k_m1(const _Float16* __r
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     const int c0 = ((s * 16 + slot) * 256 + 64 * j) >> 3;
-    uint4 xs[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xs[i] = *reinterpret_cast<const uint4*>(xlds + 16 * (c0 + i) + 16 * ((c0 + i) >> 3));
     const float2 sx = *reinterpret_cast<const float2*>(&sxl[(s * 16 + slot) * 8 + 2 * j]);
-    float al = 0.f, ah = 0.f;
+    // the two sub-blocks one after the other, so that only four x chunks are live at a time
+    float acc2[2] = {0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const uint32_t q = word(u < 4 ? q0[s] : q1[s], u & 3), t = q >> 8;
-      al = dot2(q & 0x000F000Fu, word(xs[u >> 1], 2 * (u & 1)), al);
-      al = dot2(t & 0x000F000Fu, word(xs[u >> 1], 2 * (u & 1) + 1), al);
-      ah = dot2(q & 0x00F000F0u, word(xs[4 + (u >> 1)], 2 * (u & 1)), ah);
-      ah = dot2(t & 0x00F000F0u, word(xs[4 + (u >> 1)], 2 * (u & 1) + 1), ah);
+    for (int h = 0; h < 2; ++h) {
+      uint4 xs[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = c0 + 4 * h + i;
+        xs[i] = *reinterpret_cast<const uint4*>(xlds + 16 * c + 16 * (c >> 3));
+      }
+      const uint32_t mask = h == 0 ? 0x000F000Fu : 0x00F000F0u;
+      float a = 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t q = word(u < 4 ? q0[s] : q1[s], u & 3), t = q >> 8;
+        a = dot2(q & mask, word(xs[u >> 1], 2 * (u & 1)), a);
+        a = dot2(t & mask, word(xs[u >> 1], 2 * (u & 1) + 1), a);
+      }
+      acc2[h] = a;
+      __builtin_amdgcn_sched_barrier(0);
     }
     uint32_t scs, mns;
     sel.codes(hd[s], scs, mns);
     const float dd = half_bits_to_float(hd[s].x), dmin = half_bits_to_float(hd[s].x >> 16);
-    // al = 2^-24 sum x q (sub-block 2j), ah = 2^-20 sum x q (sub-block 2j+1)
-    total = fmaf(dd * (float)(scs & 0xFF) * kTwo24, al, total);
-    total = fmaf(dd * (float)(scs >> 8) * kTwo20, ah, total);
+    // acc2[0] = 2^-24 sum x q (sub-block 2j), acc2[1] = 2^-20 sum x q (sub-block 2j+1)
+    total = fmaf(dd * (float)(scs & 0xFF) * kTwo24, acc2[0], total);
+    total = fmaf(dd * (float)(scs >> 8) * kTwo20, acc2[1], total);
     total = fmaf(-dmin * (float)(mns & 0xFF), sx.x, total);
     total = fmaf(-dmin * (float)(mns >> 8), sx.y, total);
   }
@@ -370,33 +380,52 @@ __global__ __launch_bounds__(1024) void gemv_q4k_mt(const _Float16* __restrict__
 
 // ---------------------------------------------------------------- launch ---
 
-template <int MATS, typename OutT>
+template <int WAVES, int MATS, typename OutT>
 static hipError_t launch_m1(const _Float16* x, const GemvGroup<OutT>& g, int k, hipStream_t stream) {
-  const dim3 grid(g.blocks[0] + (MATS > 1 ? g.blocks[1] : 0) + (MATS > 2 ? g.blocks[2] : 0)), block(kM1Waves * 64);
+  const dim3 grid(g.blocks[0] + (MATS > 1 ? g.blocks[1] : 0) + (MATS > 2 ? g.blocks[2] : 0)), block(WAVES * 64);
   switch (k / 4096) {
-    case 1: hipLaunchKernelGGL((gemv_q4k_m1<1, MATS, OutT>), grid, block, 0, stream, x, g); break;
-    case 2: hipLaunchKernelGGL((gemv_q4k_m1<2, MATS, OutT>), grid, block, 0, stream, x, g); break;
-    case 3: hipLaunchKernelGGL((gemv_q4k_m1<3, MATS, OutT>), grid, block, 0, stream, x, g); break;
-    case 4: hipLaunchKernelGGL((gemv_q4k_m1<4, MATS, OutT>), grid, block, 0, stream, x, g); break;
+    case 1: hipLaunchKernelGGL((gemv_q4k_m1<1, WAVES, MATS, OutT>), grid, block, 0, stream, x, g); break;
+    case 2: hipLaunchKernelGGL((gemv_q4k_m1<2, WAVES, MATS, OutT>), grid, block, 0, stream, x, g); break;
+    case 3: hipLaunchKernelGGL((gemv_q4k_m1<3, WAVES, MATS, OutT>), grid, block, 0, stream, x, g); break;
+    case 4: hipLaunchKernelGGL((gemv_q4k_m1<4, WAVES, MATS, OutT>), grid, block, 0, stream, x, g); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-template <typename OutT>
-static hipError_t launch_m1_group(const GemvArgs* a, int count, hipStream_t stream) {
+template <int WAVES, typename OutT>
+static hipError_t launch_m1_waves(const GemvArgs* a, int count, hipStream_t stream) {
   GemvGroup<OutT> g{};
   for (int i = 0; i < count; ++i) {
     g.w[i] = static_cast<const uint8_t*>(a[i].w);
     g.out[i] = static_cast<OutT*>(a[i].out);
     g.n[i] = a[i].n;
-    g.blocks[i] = (a[i].n + kM1Waves - 1) / kM1Waves;
+    g.blocks[i] = (a[i].n + WAVES - 1) / WAVES;
   }
   const _Float16* x = static_cast<const _Float16*>(a[0].x);
   switch (count) {
-    case 1: return launch_m1<1, OutT>(x, g, a[0].k, stream);
-    case 2: return launch_m1<2, OutT>(x, g, a[0].k, stream);
-    case 3: return launch_m1<3, OutT>(x, g, a[0].k, stream);
+    case 1: return launch_m1<WAVES, 1, OutT>(x, g, a[0].k, stream);
+    case 2: return launch_m1<WAVES, 2, OutT>(x, g, a[0].k, stream);
+    case 3: return launch_m1<WAVES, 3, OutT>(x, g, a[0].k, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Rows per workgroup (measured on MI355X, M = 1): 16 for K = 4096 groups of up to 16384 rows
+// (a single 12288-row gate: 7.4 us at 16, 7.8 us at 8), 8 for longer groups and longer rows
+// (gate + up 24576 rows: 13.0 us at 8, 13.8 us at 16; down 4096 x 12288: 7.6 us at 8, 8.4 us at 16).
+static int m1_waves(const GemvArgs* a, int count) {
+  long rows = 0;
+  for (int i = 0; i < count; ++i) rows += a[i].n;
+  return a[0].k == 4096 && rows <= 16384 ? 16 : 8;
+}
+
+template <typename OutT>
+static hipError_t launch_m1_group(const GemvArgs* a, int count, hipStream_t stream, int waves = 0) {
+  switch (waves > 0 ? waves : m1_waves(a, count)) {
+    case 4: return launch_m1_waves<4, OutT>(a, count, stream);
+    case 8: return launch_m1_waves<8, OutT>(a, count, stream);
+    case 16: return launch_m1_waves<16, OutT>(a, count, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -463,8 +492,8 @@ hipError_t launch_gemv_q4k_fast(const GemvArgs& a, hipStream_t stream, bool* han
 
 bool gemv_q4k_group_supported(int m, int k) { return m == 1 && k % 4096 == 0 && k <= 4 * 4096; }
 
-hipError_t launch_gemv_q4k_group(const GemvArgs* a, int count, hipStream_t stream) {
-  return a[0].out_half ? launch_m1_group<_Float16>(a, count, stream) : launch_m1_group<float>(a, count, stream);
+hipError_t launch_gemv_q4k_group(const GemvArgs* a, int count, hipStream_t stream, int waves) {
+  return a[0].out_half ? launch_m1_group<_Float16>(a, count, stream, waves) : launch_m1_group<float>(a, count, stream, waves);
 }
 
 }  // namespace tensor_gguf

@@ -29,9 +29,6 @@ constexpr int kGemvMaxM = 8;
 
 // Largest number of matrices one grouped decode GEMV launch covers.
 constexpr int kGemvGroupMax = 3;
-// Waves (= rows) per workgroup of the M = 1 Q4_K kernel.
-constexpr int kM1Waves = 16;
-
 // Matrices of one grouped launch: they share x and K; blocks[i] workgroups
 // cover matrix i.
 template <typename OutT>
@@ -48,7 +45,8 @@ hipError_t launch_gemv(const GemvArgs& args, hipStream_t stream);
 hipError_t launch_gemv_q4k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 // Grouped M = 1 Q4_K GEMV: `count` (<= kGemvGroupMax) matrices sharing x and K in one launch.
 bool gemv_q4k_group_supported(int m, int k);
-hipError_t launch_gemv_q4k_group(const GemvArgs* args, int count, hipStream_t stream);
+// waves: rows (one per wave) per workgroup; 0 takes the default, 4 / 8 / 16 fix it (for sweeps)
+hipError_t launch_gemv_q4k_group(const GemvArgs* args, int count, hipStream_t stream, int waves = 0);
 // Q6_K fast path (LDS-staged x, M = 1, K in {4096, 8192, 12288}).
 hipError_t launch_gemv_q6k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 hipError_t launch_dequant(const DequantArgs& args, hipStream_t stream);

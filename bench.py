@@ -1,10 +1,10 @@
 """Benchmark of the GGUF quantized-linear hot path on one MI355X.
 
 Headline ("C2"): Q4_K decode GEMV at Qwen3-8B MLP
-shapes, M = 1.  One *step* is one decode MLP's three linears, each its own
-launch through the C ABI: gate [12288 x 4096], up [12288 x 4096] and down
-[4096 x 12288].  ``value`` is the algorithmic bytes of all K steps (packed
-weights + fp16 x + fp16 out) divided by the timed region.
+shapes, M = 1.  One *step* is one decode MLP's linears through the C ABI: gate
+[12288 x 4096] and up [12288 x 4096] as one grouped launch (they share x), then
+down [4096 x 12288].  ``value`` is the algorithmic bytes of all K steps
+(packed weights + fp16 x + fp16 out) divided by the timed region.
 
 Protocol (after benchmarks/kernels/showcase/benchmark.py:66-94): every launch
 is bound once (allocation-free BoundCall), the K steps are captured into one
@@ -12,11 +12,14 @@ HIP graph, and the graph replay is timed with HIP events recorded on the
 launch stream.  Weights rotate through distinct copies (>= 3 x 256 MiB per
 rotation) so no launch finds its weights in the 256 MiB MALL.
 
-Also reported: ``roofline`` for the dominant kernel (Q4_K GEMV 12288 x 4096),
-``cpu_baseline`` (the C restatement in oracle/, invoked through its
-TensorKernelV1 entry exactly as the reference CPU provider invokes images), and
-``details`` for the other BASELINE configurations (C2 M = 4/8, C3 LM head, C4
-prefill GEMM, C5 decoder-layer chain).
+Also reported: ``roofline`` for the dominant kernel (the grouped gate + up
+GEMV, 2 x 12288 x 4096; its HBM ``traffic`` is the per-launch figure measured
+with rocprofv3 FETCH_SIZE / WRITE_SIZE and recorded in
+profiles/gemv_q4k_m1_qwen3_mlp.md), ``cpu_baseline`` (the C restatement in
+oracle/, invoked through its TensorKernelV1 entry exactly as the reference CPU
+provider invokes images), and ``details`` for the other BASELINE
+configurations (C2 M = 4/8 and the three-launch step, C3 LM head, C4 prefill
+GEMM, C5 decoder-layer chain at M = 1 and M = 256).
 """
 
 from __future__ import annotations
@@ -109,6 +112,22 @@ class GroupLinear:
                 b.release()
         for b in self.outs:
             b.release()
+
+
+PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_q4k_m1_qwen3_mlp.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel, from the committed rocprofv3 summary
+    (FETCH_SIZE and WRITE_SIZE passes scaled by a 256 MiB copy); None if it is absent."""
+    try:
+        with open(PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def copies_for(bytes_per_rotation_unit):
@@ -266,6 +285,8 @@ def main():
                         help="first run 5 device copies of 256 MiB (a known-size copy kernel for PMC scaling)")
     parser.add_argument("--timing", choices=("graph", "eager"), default="graph",
                         help="replay each timed sequence from a captured HIP graph, or enqueue it eagerly")
+    parser.add_argument("--only", metavar="PREFIX",
+                        help="run only the details cases whose name starts with PREFIX (for profiling one kernel)")
     parser.add_argument("--eager-only", action="store_true",
                         help="stop after the eager warmup launches (for per-dispatch counter runs)")
     args = parser.parse_args()
@@ -324,8 +345,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "gemv_q4k_m1<STEPS=1, MATS=2> gate+up 2 x 12288x4096, M=1, fp16 out",
+            "traffic": measured_traffic(),
+            "kernel": "gemv_q4k_m1<STEPS=1, WAVES=8, MATS=2> gate+up 2 x 12288x4096, M=1, fp16 out",
             "avg_us": round(kernel_s * 1e6, 3),
             "algorithmic_bytes": gate_up.bytes,
         }
@@ -333,7 +354,7 @@ def main():
 
         details = {}
         if not args.no_details:
-            details = run_details(device, gate_up.x, log)
+            details = run_details(device, gate_up.x, log, args.only)
         for layer in mlp:
             layer.release()
 
@@ -368,21 +389,8 @@ def main():
     return 0
 
 
-def run_details(device, x4096, log):
-    """Per-config figures for the other BASELINE configurations."""
-    details = {}
-
-    def gemv_case(name, encoding, m, n, k, out_dtype, launches=60):
-        copies = copies_for(weight_bytes(encoding, n, k))
-        layer = Linear(device, "gguf_gemv", encoding, m, n, k, out_dtype, copies, 7 + m)
-        seconds = time_launches(device, [layer.calls[i % copies].launch for i in range(launches)]) / launches
-        gbs = layer.bytes / seconds / 1e9
-        details[name] = {"us": round(seconds * 1e6, 3), "GB/s": round(gbs, 1),
-                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
-        log(name, details[name])
-        layer.release()
-
-    # the headline step as three single-matrix launches (gate, up, down)
+def three_launch_step(device, x4096, log, details):
+    """The headline step as three single-matrix launches (gate, up, down)."""
     copies = copies_for(2 * weight_bytes("q4_k", 12288, 4096) + weight_bytes("q4_k", 4096, 12288))
     mlp = [Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 1, x=x4096),
            Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 3, x=x4096),
@@ -397,12 +405,39 @@ def run_details(device, x4096, log):
     for layer in mlp:
         layer.release()
 
+
+def run_details(device, x4096, log, only=None):
+    """Per-config figures for the other BASELINE configurations (those whose name starts with
+    ``only``, when given)."""
+    details = {}
+
+    def wanted(name):
+        return only is None or name.startswith(only)
+
+    def gemv_case(name, encoding, m, n, k, out_dtype, launches=60):
+        if not wanted(name):
+            return
+        copies = copies_for(weight_bytes(encoding, n, k))
+        layer = Linear(device, "gguf_gemv", encoding, m, n, k, out_dtype, copies, 7 + m)
+        seconds = time_launches(device, [layer.calls[i % copies].launch for i in range(launches)]) / launches
+        gbs = layer.bytes / seconds / 1e9
+        details[name] = {"us": round(seconds * 1e6, 3), "GB/s": round(gbs, 1),
+                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
+        log(name, details[name])
+        layer.release()
+
+    # the headline step as three single-matrix launches (gate, up, down)
+    if wanted("C2_step_m1_three_launches"):
+        three_launch_step(device, x4096, log, details)
+
     for m in (1, 4, 8):
         gemv_case(f"C2_q4k_gemv_m{m}_12288x4096", "q4_k", m, 12288, 4096, "float16")
         gemv_case(f"C2_q4k_gemv_m{m}_4096x12288", "q4_k", m, 4096, 12288, "float16")
     gemv_case("C3_q6k_lm_head_m1_151936x4096_fp32", "q6_k", 1, 151936, 4096, "float32", launches=20)
 
     def gemm_case(name, encoding, m, n, k, launches=10):
+        if not wanted(name):
+            return
         layer = Linear(device, "gguf_gemm", encoding, m, n, k, "float16", 2, 9)
         seconds = time_launches(device, [layer.calls[i % 2].launch for i in range(launches)]) / launches
         tflops = layer.flops / seconds / 1e12
@@ -420,6 +455,8 @@ def run_details(device, x4096, log):
               ("down", "q6_k", 4096, 12288)]
     layer_weights = sum(weight_bytes(e, n, k) for _, e, n, k in shapes)
     for m, kernel in ((1, "gguf_gemv"), (256, "gguf_gemm")):
+        if not wanted(f"C5_layer_m{m}"):
+            continue
         copies = copies_for(layer_weights) if m == 1 else 2
         layers = [Linear(device, kernel, e, m, n, k, "float16", copies, 20 + i) for i, (_, e, n, k) in enumerate(shapes)]
         steps = 20 if m == 1 else 4
@@ -435,6 +472,8 @@ def run_details(device, x4096, log):
         for layer in layers:
             layer.release()
     # C5 at M=1 the way a decode step runs it: q + k + v grouped, o, gate + up grouped, down
+    if not wanted("C5_layer_m1_grouped"):
+        return details
     copies = copies_for(layer_weights)
     x = device.from_numpy(np.zeros((1, 4096), np.float16) + np.float16(0.5))
     layers = [GroupLinear(device, "q4_k", 1, [(4096, 4096), (1024, 4096), (1024, 4096)], "float16", copies, 40, x=x),

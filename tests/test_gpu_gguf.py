@@ -119,6 +119,25 @@ def test_gemv_parity_baseline_shapes(hip_device, c_oracle, encoding, n, k, m, ou
     assert R.relative_l2(got, expected) <= TOLERANCE
 
 
+@pytest.mark.parametrize("n", [65536 + 1007, 70000])
+def test_gemv_q6k_tall_rows_each_within_tolerance(hip_device, c_oracle, n):
+    """Tall K = 4096 Q6_K matrices (the LM head's shape class, ragged row counts): every row
+    is checked, so a skipped, repeated or misplaced row fails even where the relative L2 of
+    the whole output would hide it."""
+    note("gemv-q6k-tall", n)
+    k = 4096
+    raw = cases.weight(n, k, "q6_k", 42)
+    x = cases.activation(1, k, 43)
+    c_oracle.set_threads(16)
+    expected = c_oracle.linear(x, raw, Q.Q6_K, n, k)[0]
+    scale = float(np.sqrt(np.mean(expected.astype(np.float64) ** 2)))
+    for out_dtype in ("float32", "float16"):
+        got = run_linear(hip_device, "gguf_gemv", "q6_k", x, raw, out_dtype)[0].astype(np.float32)
+        assert not np.isnan(got).any()
+        err = np.abs(got - expected)
+        assert err.max() <= 2e-3 * scale + 1e-3 * np.abs(expected).max(), (out_dtype, int(err.argmax()))
+
+
 @pytest.mark.parametrize("m,n,k", [
     (8, 8200, 4096),    # two 16-row tiles per wave, ragged last tile pair
     (5, 4100, 12288),   # three super-blocks per wave, x of 120 KiB in LDS

@@ -166,6 +166,25 @@ int32_t tensor_hip_capture_end(uint64_t stream, uint64_t *graph_exec, TensorErro
 int32_t tensor_hip_graph_launch(uint64_t graph_exec, uint64_t stream, TensorErrorV1 *error);
 int32_t tensor_hip_graph_destroy(uint64_t graph_exec, TensorErrorV1 *error);
 
+/* Hand-built code objects from `hip` artifacts (the reference's cuModuleLoadData /
+ * cuModuleGetFunction / cuModuleUnload / cuLaunchKernel path,
+ * src/tensor/providers/cuda/device.py:211-229, :359-389).  `image` is a gfx950
+ * ELF code object; `*module` and `*function` are opaque handles. */
+int32_t tensor_hip_module_load(const void *image, uint64_t bytes, uint64_t *module,
+                               TensorErrorV1 *error);
+int32_t tensor_hip_module_function(uint64_t module, const char *name, uint64_t *function,
+                                   TensorErrorV1 *error);
+int32_t tensor_hip_module_unload(uint64_t module, TensorErrorV1 *error);
+/* Launches `function` with the call's grid, block, dynamic shared memory and
+ * stream; argument i is passed by value in kernel-parameter order: a buffer as
+ * its device address, a scalar as its dtype-sized payload.  Header and argument
+ * descriptors are checked (ABI version, flags, ROCm stream and buffers on the
+ * stream's device, launch bounds) before any HIP call.  The caller guarantees
+ * the argument list matches the kernel's parameters (the Python loader checks
+ * it against the code object's metadata). */
+int32_t tensor_hip_module_launch_v1(uint64_t function, const TensorCallV1 *call,
+                                    TensorErrorV1 *error);
+
 /* Library build identity: "tensor_hip <abi> <arch>". */
 const char *tensor_hip_version(void);
 

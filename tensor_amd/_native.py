@@ -73,6 +73,9 @@ SERVICES = {
     "tensor_hip_capture_end": [_u64, c.POINTER(_u64)],
     "tensor_hip_graph_launch": [_u64, _u64],
     "tensor_hip_graph_destroy": [_u64],
+    "tensor_hip_module_load": [c.c_void_p, _u64, c.POINTER(_u64)],
+    "tensor_hip_module_function": [_u64, c.c_char_p, c.POINTER(_u64)],
+    "tensor_hip_module_unload": [_u64],
 }
 
 
@@ -115,6 +118,8 @@ def library(path: Path | None = None) -> c.CDLL:
             function = getattr(lib, name)
             function.argtypes = [*argtypes, _err]
             function.restype = c.c_int32
+        lib.tensor_hip_module_launch_v1.argtypes = [_u64, c.POINTER(CallDescriptor), _err]
+        lib.tensor_hip_module_launch_v1.restype = c.c_int32
         lib.tensor_hip_version.argtypes = []
         lib.tensor_hip_version.restype = c.c_char_p
         if path is None:

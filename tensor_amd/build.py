@@ -2,8 +2,10 @@
 
 ``python -m tensor_amd.build`` (or ``__graft_entry__.build()``) compiles every
 ``csrc/*.hip`` translation unit in parallel and links the shared library next
-to this file, where the provider loads it.  There is no JIT path: a missing
-library is an error at load time, never a fallback.
+to this file, where the provider loads it; it also compiles every hand-written
+kernel under ``kernels/`` to an unbundled gfx950 code object and packs it into a
+`hip` executable bundle (``kernels/<name>.tbin``).  There is no JIT path: a
+missing library or bundle is an error at load time, never a fallback.
 """
 
 from __future__ import annotations
@@ -53,6 +55,38 @@ def _compile(source: Path, verbose: bool) -> Path:
     return obj
 
 
+KERNELS = PACKAGE / "kernels"
+
+
+def _compiler_version() -> str:
+    result = subprocess.run([hipcc(), "--version"], capture_output=True, text=True)
+    lines = [line.strip() for line in result.stdout.splitlines() if line.strip()]
+    return "; ".join(lines[:2]) if lines else "unknown"
+
+
+def build_bundles(verbose: bool = False) -> list:
+    """Compile kernels/<name>.hip to a code object and pack kernels/<name>.tbin."""
+    from tensor_amd.artifacts import write_artifact
+    from tensor_amd.kernels import BUNDLES
+
+    built = []
+    version = _compiler_version()
+    for name, spec in BUNDLES.items():
+        source = KERNELS / f"{name}.hip"
+        code_object = KERNELS / f"{name}.hsaco"
+        cmd = [hipcc(), "--genco", "--no-gpu-bundle-output", *DEVICE_FLAGS, str(source), "-o", str(code_object)]
+        result = subprocess.run(cmd, capture_output=True, text=True)
+        if result.returncode:
+            raise RuntimeError(f"hipcc failed for {source.name}:\n{result.stdout}\n{result.stderr}")
+        if verbose and result.stderr.strip():
+            print(result.stderr, file=sys.stderr)
+        bundle = KERNELS / f"{name}.tbin"
+        write_artifact(bundle, code_object.read_bytes(), name=name, target=ARCH,
+                       compiler={"name": "hipcc", "version": version}, source=source.read_bytes(), **spec)
+        built.append(bundle)
+    return built
+
+
 def build(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
@@ -64,6 +98,7 @@ def build(verbose: bool = False) -> Path:
     if result.returncode:
         raise RuntimeError(f"link failed:\n{result.stdout}\n{result.stderr}")
     os.replace(tmp, LIBRARY)
+    build_bundles(verbose)
     return LIBRARY
 
 

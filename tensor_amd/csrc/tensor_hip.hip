@@ -441,6 +441,71 @@ int32_t tensor_hip_graph_destroy(uint64_t graph_exec, TensorErrorV1* error) {
   return ok(error);
 }
 
+// ----------------------------------------------------------- code objects ---
+
+int32_t tensor_hip_module_load(const void* image, uint64_t bytes, uint64_t* module, TensorErrorV1* error) {
+  if (!image || bytes < 64 || !module || std::memcmp(image, "\x7f" "ELF", 4) != 0)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "module image is not an ELF code object");
+  hipModule_t handle = nullptr;
+  HIP_TRY(hipModuleLoadData(&handle, image), "hipModuleLoadData");
+  *module = reinterpret_cast<uint64_t>(handle);
+  return ok(error);
+}
+
+int32_t tensor_hip_module_function(uint64_t module, const char* name, uint64_t* function, TensorErrorV1* error) {
+  if (!module || !name || !function) return fail(error, TENSOR_ERROR_ARGUMENT, "invalid module or function name");
+  hipFunction_t handle = nullptr;
+  HIP_TRY(hipModuleGetFunction(&handle, reinterpret_cast<hipModule_t>(module), name), "hipModuleGetFunction");
+  *function = reinterpret_cast<uint64_t>(handle);
+  return ok(error);
+}
+
+int32_t tensor_hip_module_unload(uint64_t module, TensorErrorV1* error) {
+  if (!module) return fail(error, TENSOR_ERROR_ARGUMENT, "invalid module");
+  HIP_TRY(hipModuleUnload(reinterpret_cast<hipModule_t>(module)), "hipModuleUnload");
+  return ok(error);
+}
+
+int32_t tensor_hip_module_launch_v1(uint64_t function, const TensorCallV1* call, TensorErrorV1* error) {
+  constexpr uint32_t kMaxArguments = 256;
+  if (!call || call->abi_version != TENSOR_ABI_VERSION || call->struct_size < sizeof(TensorCallV1))
+    return fail(error, TENSOR_ERROR_ABI, "unsupported call ABI");
+  if (!function) return fail(error, TENSOR_ERROR_ARGUMENT, "invalid kernel function");
+  if (call->flags || call->argument_count > kMaxArguments || (call->argument_count && !call->arguments))
+    return fail(error, TENSOR_ERROR_ARGUMENT, "invalid argument count or flags");
+  if (call->stream.device_type != TENSOR_DEVICE_ROCM || call->stream.device_ordinal < 0)
+    return fail(error, TENSOR_ERROR_PROVIDER, "ROCm calls need a ROCm stream");
+  uint64_t threads = 1;
+  for (int d = 0; d < 3; ++d) {
+    if (call->grid[d] < 1 || call->grid[d] > 0x7FFFFFFFu || call->block[d] < 1)
+      return fail(error, TENSOR_ERROR_ARGUMENT, "launch dimensions must be positive int32");
+    threads *= call->block[d];
+  }
+  if (threads > 1024) return fail(error, TENSOR_ERROR_ARGUMENT, "launch block exceeds 1024 threads");
+  void* parameters[kMaxArguments];
+  for (uint32_t i = 0; i < call->argument_count; ++i) {
+    const TensorArgumentV1& arg = call->arguments[i];
+    if (arg.kind == TENSOR_ARG_BUFFER) {
+      const TensorBufferV1& b = arg.buffer;
+      if (b.device_type != TENSOR_DEVICE_ROCM || b.device_ordinal != call->stream.device_ordinal || !b.address ||
+          b.dtype != arg.dtype)
+        return fail(error, TENSOR_ERROR_ARGUMENT, "argument %u: buffer is not on the stream's ROCm device", i);
+      parameters[i] = const_cast<uint64_t*>(&b.address);
+    } else if (arg.kind == TENSOR_ARG_SCALAR) {
+      parameters[i] = const_cast<uint64_t*>(&arg.scalar);  // little-endian: the value is in the low bytes
+    } else {
+      return fail(error, TENSOR_ERROR_ARGUMENT, "argument %u: unknown kind %u", i, (unsigned)arg.kind);
+    }
+  }
+  if (int32_t status = check_device(call, error)) return status;
+  HIP_TRY(hipModuleLaunchKernel(reinterpret_cast<hipFunction_t>(function), call->grid[0], call->grid[1],
+                                call->grid[2], call->block[0], call->block[1], call->block[2],
+                                call->shared_memory_bytes, reinterpret_cast<hipStream_t>(call->stream.handle),
+                                call->argument_count ? parameters : nullptr, nullptr),
+          "hipModuleLaunchKernel");
+  return ok(error);
+}
+
 const char* tensor_hip_version(void) { return "tensor_hip 1.3 gfx950"; }
 
 }  // extern "C"

@@ -229,10 +229,19 @@ class Device(Session):
 
     # -------------------------------------------------------- executables --
     def load(self, artifact, **options) -> Executable:
-        """Load a built-in GGUF executable by kernel name or manifest dict."""
+        """Load an executable: a built-in GGUF kernel by name (with its options) or manifest
+        dict, or a `hip` executable bundle from a path (a hand-built code object; see
+        tensor_amd.artifacts), as the reference's ``Device.load(artifact)`` does for its
+        bundles (src/tensor/providers/cuda/device.py:359-386)."""
+        import os
+
         from tensor_amd.gguf.kernels import manifest as gguf_manifest
 
         self._check()
+        if isinstance(artifact, os.PathLike) or (isinstance(artifact, str) and os.path.isfile(artifact)):
+            if options:
+                raise ValueError("options apply only to kernels loaded by name")
+            return self._load_bundle(artifact)
         if isinstance(artifact, str):
             manifest = gguf_manifest(artifact, **options)
         elif isinstance(artifact, dict):
@@ -240,7 +249,7 @@ class Device(Session):
                 raise ValueError("options apply only to kernels loaded by name")
             manifest = artifact
         else:
-            raise TypeError("artifact must be a built-in kernel name or a manifest dict")
+            raise TypeError("artifact must be a built-in kernel name, a manifest dict or a bundle path")
         if manifest.get("provider") != "hip":
             raise ValueError("artifact requires a different runtime provider")
         check_requirement(manifest["runtime_abi"], self.capabilities)
@@ -249,13 +258,38 @@ class Device(Session):
         function = _native.kernel(manifest["entrypoint"])
         return Executable(self, manifest, _native.library(), function, None)
 
+    def _load_bundle(self, path) -> Executable:
+        from tensor_amd.artifacts import read_artifact
+        from tensor_amd.artifacts.hip import IMAGE
+
+        manifest, files = read_artifact(path)  # every member verified before HIP sees a byte
+        check_requirement(manifest["runtime_abi"], self.capabilities)
+        if manifest["target"] != self.info["arch"]:
+            raise ValueError(f"artifact target {manifest['target']} does not match device {self.info['arch']}")
+        image = c.create_string_buffer(files[IMAGE], len(files[IMAGE]))
+        module, function = c.c_uint64(), c.c_uint64()
+        _native.call("tensor_hip_set_device", self.ordinal)
+        _native.call("tensor_hip_module_load", c.cast(image, c.c_void_p), len(files[IMAGE]), c.byref(module))
+        try:
+            _native.call("tensor_hip_module_function", module.value, manifest["entrypoint"].encode(), c.byref(function))
+        except BaseException:
+            _native.call("tensor_hip_module_unload", module.value)
+            raise
+        return Executable(self, manifest, module.value, function.value, image)
+
     def _unload_executable(self, executable) -> None:
-        pass  # entry points live for the life of the process-wide library
+        if executable.manifest.get("kind") == "hsaco":
+            _native.call("tensor_hip_module_unload", executable.module)
+        # built-in entry points live for the life of the process-wide library
 
     def _launch(self, executable, call) -> None:
         self._check()
         error = ErrorDescriptor()
-        status = executable.function(c.byref(call.descriptor), c.byref(error))
+        if executable.manifest.get("kind") == "hsaco":
+            status = _native.library().tensor_hip_module_launch_v1(executable.function, c.byref(call.descriptor),
+                                                                  c.byref(error))
+        else:
+            status = executable.function(c.byref(call.descriptor), c.byref(error))
         if status:
             raise HipError(executable.manifest["entrypoint"], status, error.message.decode(errors="replace"))
 

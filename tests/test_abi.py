@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol():
     assert "tensor_gguf_gemv_v1" in names and "tensor_hip_malloc" in names
     missing = [name for name in names if not hasattr(lib, name)]
     assert not missing, missing
-    assert set(_native.KERNELS) | set(_native.SERVICES) | {"tensor_hip_version"} == set(names)
+    assert set(_native.KERNELS) | set(_native.SERVICES) | {"tensor_hip_version", "tensor_hip_module_launch_v1"} == set(names)
 
 
 class Call:

@@ -21,6 +21,8 @@
 //    product (v_mfma_f32_16x16x4f32) whose A operand is the per-sub-block
 //    activation sums and whose B operand is dmin * m.  The K range is split
 //    across the waves of a workgroup and the partial tiles meet in LDS.
+//    gemv_q4k_sec is the same arithmetic with the weights read as whole
+//    64-byte sectors of 16 rows per load (wide matrices, long rows).
 //
 // Block format and element formula: benchmarks/kernels/showcase/triton_kernels.py:143-162.
 #include <algorithm>
@@ -256,6 +258,168 @@ __global__ __launch_bounds__(SPLIT * 64) void gemv_q4k_mfma(const _Float16* __re
   }
 }
 
+// Sector-aligned variant for 2 <= M <= 8 and K a multiple of 1024 (wide matrices and long
+// rows).  Wave (t, q) of a workgroup owns 16-row tile t and the 576-byte range of four
+// super-blocks 4q .. 4q+3 of every row; a workgroup holds TILES tiles x K/1024 waves.
+// Load c (0..8) of a lane (n, g) reads the 16-byte chunk 4c + g of row n's range, so each
+// load instruction covers whole 64-byte sectors of 16 rows.  With 9 chunks per 144-byte
+// super-block this hands every lane exactly one header (super-block b = g, at load 9b/4)
+// and two quant chunks of each super-block, at fixed loads for some lanes and one of two
+// loads for others (one v_cndmask per dword).  A quant chunk r (1..8) is bytes 16(r-1) ..
+// of the 128 quant bytes: pair j = (r-1)/2, half (r-1)%2, low nibbles sub-block 2j and
+// high nibbles 2j+1.  Headers reach the other lanes of their row with ds_bpermute; codes
+// are widened and scaled as in gemv_q4k_mfma (exact sc*q in fp16), d applied per
+// super-block; the min term uses a per-8-element table of x sums staged with x.
+//
+// Issue order (measured on MI355X): x, then the loads of super-block 0 only; the other six
+// loads follow the barrier that publishes x.  Issued together, the 28 MB weight stream
+// queued the 32-64 KB activation loads behind it (x was staged ~4.5 us after launch);
+// this way x is staged in ~1.5 us while a third of the weights is already in flight.
+constexpr int kSecEarlyLoads = 3;
+constexpr int kSecXPad = 16;               // bytes after each LDS row of x
+constexpr size_t kSecMaxLds = 160 * 1024;  // LDS of one gfx950 workgroup
+
+__device__ __forceinline__ uint4 shfl4(const uint4& v, int src) {
+  return make_uint4(__shfl(v.x, src, 64), __shfl(v.y, src, 64), __shfl(v.z, src, 64), __shfl(v.w, src, 64));
+}
+
+__device__ __forceinline__ uint4 select4(bool c, const uint4& a, const uint4& b) {
+  return make_uint4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+}
+
+// Scale and min codes of sub-blocks 2j (bits 0-7) and 2j+1 (bits 8-15), j varying per lane.
+__device__ __forceinline__ void pair_codes(const uint4& hd, int j, uint32_t& scs, uint32_t& mns) {
+  const int shift = 16 * (j & 1);
+  const uint32_t b0 = hd.y >> shift, b1 = hd.z >> shift, b2 = hd.w >> shift;
+  if (j < 2) {
+    scs = b0 & 0x3F3Fu;
+    mns = b1 & 0x3F3Fu;
+  } else {
+    scs = (b2 & 0x0F0Fu) | ((b0 >> 2) & 0x3030u);
+    mns = ((b2 >> 4) & 0x0F0Fu) | ((b1 >> 2) & 0x3030u);
+  }
+}
+
+template <int M, typename OutT>
+__global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict__ x, const uint8_t* __restrict__ w,
+                                                     OutT* __restrict__ out, int n_rows, int k, int tiles) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int XCH = 8;  // x chunks per thread (the host checks M * K / 8 <= XCH * threads)
+  const int KW = k >> 10;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int t = wv / KW, q = wv - t * KW;
+  const int row_bytes = (k >> 8) * 144;
+  const int xrow = 2 * k + kSecXPad;
+  const int chunks = M * k / 8, cpr = k / 8;
+  uint8_t* xl = lds;                                          // M rows of x, then 16 zero bytes
+  float* s8 = reinterpret_cast<float*>(lds + M * xrow + 16);  // sums of 8 x values, then 2 zeros
+
+  uint4 xr[XCH];
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) {
+    const int c = threadIdx.x + i * (int)blockDim.x;
+    if (c < chunks) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * (size_t)c);
+  }
+  const int tile = blockIdx.x * tiles + t;
+  const uint8_t* base = w + (size_t)min(tile * 16 + n, n_rows - 1) * row_bytes + q * 576 + 16 * g;
+  uint4 v[9];
+#pragma unroll
+  for (int c = 0; c < kSecEarlyLoads; ++c) v[c] = load16(base + 64 * c);
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) {
+    const int c = threadIdx.x + i * (int)blockDim.x;
+    if (c < chunks) {
+      const int m = c / cpr, cc = c - m * cpr;
+      *reinterpret_cast<uint4*>(xl + m * xrow + 16 * cc) = xr[i];
+      const uint32_t one = 0x3C003C00u;
+      s8[c] = dot2(xr[i].w, one, dot2(xr[i].z, one, dot2(xr[i].y, one, dot2(xr[i].x, one, 0.f))));
+    }
+  }
+  if (threadIdx.x == 0) {
+    *reinterpret_cast<uint4*>(xl + M * xrow) = make_uint4(0, 0, 0, 0);
+    s8[chunks] = 0.f;
+    s8[chunks + 1] = 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = kSecEarlyLoads; c < 9; ++c) v[c] = load16(base + 64 * c);
+
+  // as the A operand lane (n, g) holds activation row n; lanes past M read zeros at every offset
+  const bool has_row = n < M;
+  const uint8_t* xn = has_row ? xl + n * xrow + 2048 * q : xl + M * xrow;
+  const int xstep = has_row ? 1 : 0;
+  const float* s8n = has_row ? s8 + n * cpr + 128 * q : s8 + chunks;
+  float4v_t acc = {0.f, 0.f, 0.f, 0.f}, accmin = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    // the lane's two quant chunks of super-block b (register, chunk index r)
+    uint4 F, S;
+    int rF, rS;
+    if (b == 0) {
+      F = v[1]; rF = 4 + g; S = select4(g == 0, v[2], v[0]); rS = g == 0 ? 8 : g;
+    } else if (b == 1) {
+      F = v[3]; rF = 3 + g; S = select4(g < 2, v[4], v[2]); rS = g < 2 ? 7 + g : g - 1;
+    } else if (b == 2) {
+      F = v[5]; rF = 2 + g; S = select4(g < 3, v[6], v[4]); rS = g < 3 ? 6 + g : 1;
+    } else {
+      F = v[7]; rF = 1 + g; S = v[8]; rS = 5 + g;
+    }
+    const uint4 hd = shfl4(v[(9 * b) / 4], n + 16 * b);
+    const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
+    float4v_t cs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint4 C = h == 0 ? F : S;
+      const int r = h == 0 ? rF : rS;
+      const int j = (r - 1) >> 1, half = (r - 1) & 1;
+      uint32_t scs, mns;
+      pair_codes(hd, j, scs, mns);
+      const float sc_lo = (float)(scs & 0xFF), sc_hi = (float)(scs >> 8);
+      // low: (1024 + q) sc - 1024 sc = sc q;  high: (1024 + 16 q) sc / 16 - 64 sc = sc q  (exact)
+      const uint32_t mul_lo = half2_splat(sc_lo), add_lo = half2_splat(-1024.0f * sc_lo);
+      const uint32_t mul_hi = half2_splat(sc_hi * 0.0625f), add_hi = half2_splat(-64.0f * sc_hi);
+      const int e_lo = 256 * b + 64 * j + 16 * half;  // first element of the low-nibble run
+#pragma unroll
+      for (int nib = 0; nib < 2; ++nib) {
+        const int e = e_lo + 32 * nib;
+        const uint32_t mask = nib == 0 ? 0x0F0F0F0Fu : 0xF0F0F0F0u;
+        const uint32_t mul = nib == 0 ? mul_lo : mul_hi, add = nib == 0 ? add_lo : add_hi;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const uint32_t ca = word(C, 2 * p) & mask, cb = word(C, 2 * p + 1) & mask;
+          const uint4 bv = make_uint4(pk_fma(magic01(ca), mul, add), pk_fma(magic23(ca), mul, add),
+                                      pk_fma(magic01(cb), mul, add), pk_fma(magic23(cb), mul, add));
+          const uint4 xa = *reinterpret_cast<const uint4*>(xn + xstep * 2 * (e + 8 * p));
+          cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, xa),
+                                                      __builtin_bit_cast(half8_t, bv), cs, 0, 0, 0);
+        }
+        // sum of x over the run's 16 elements: two entries of the table
+        const float2 s2 = *reinterpret_cast<const float2*>(s8n + xstep * (e >> 3));
+        const float mv = dmin * (float)(nib == 0 ? (mns & 0xFF) : (mns >> 8));
+        accmin = __builtin_amdgcn_mfma_f32_16x16x4f32(s2.x + s2.y, mv, accmin, 0, 0, 0);
+      }
+    }
+    acc += d * cs;
+  }
+  const float4v_t total = acc - accmin;
+  __syncthreads();  // every wave is done with x: the partial tiles go over it
+  float4v_t* partial = reinterpret_cast<float4v_t*>(lds);
+  partial[wv * 64 + lane] = total;
+  __syncthreads();
+  if (q != 0 || tile * 16 >= n_rows) return;
+  // wave (t, 0) sums its tile's K ranges in order and stores it
+  float4v_t sum = partial[t * KW * 64 + lane];
+  for (int p = 1; p < KW; ++p) sum += partial[(t * KW + p) * 64 + lane];
+  const int col = tile * 16 + n;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = 4 * g + i;
+    if (m < M && col < n_rows) store_out<OutT>(out, (size_t)m * n_rows + col, sum[i]);
+  }
+}
+
 // Multi-tile variant for 2 <= M <= 8 when x fits in LDS (M * K <= kMtMaxMK).
 // A workgroup of W waves owns TILES 16-row tiles; wave w takes the S
 // super-blocks [w S, w S + S) of every tile.  The workgroup first loads all of
@@ -468,20 +632,55 @@ static hipError_t launch_mt(const GemvArgs& a, hipStream_t stream, bool* handled
   return wide ? launch_mt_cfg<M, 2, 3, OutT>(a, stream) : launch_mt_cfg<M, 1, 3, OutT>(a, stream);
 }
 
+static size_t sec_lds_bytes(int m, int k) {
+  return (size_t)m * (2 * k + kSecXPad) + 16 + ((size_t)m * k / 8 + 2) * sizeof(float);
+}
+
+// Sector-aligned kernel for matrices of at least 512 tiles (gate / up, 12288 x 4096: 11.0 us
+// at M = 4 against 12.8 us for gemv_q4k_mt) and rows of at least 8192 columns (down,
+// 4096 x 12288: 12.5 against 14.5 us); shorter and narrower shapes keep gemv_q4k_mt
+// (4096 x 4096: 6.1 us both).  Three tiles per workgroup when that still gives 256
+// workgroups, so every CU holds one.
+template <int M, typename OutT>
+static hipError_t launch_sec(const GemvArgs& a, hipStream_t stream, bool* handled) {
+  *handled = false;
+  const int kw = a.k / 1024, tiles = (a.n + 15) / 16;
+  if (a.k % 1024 != 0 || (tiles < 512 && kw < 8) || kw > 16) return hipSuccess;
+  const int per = tiles >= 768 && 3 * kw <= 16 ? 3 : tiles >= 512 && 2 * kw <= 16 ? 2 : 1;
+  const int threads = per * kw * 64;
+  const size_t lds = std::max(sec_lds_bytes(M, a.k), (size_t)per * kw * 64 * sizeof(float4v_t));
+  // x is staged with eight 16-byte chunks per thread at most, and must fit in LDS with its sums
+  if ((long)M * a.k / 8 > 8L * threads || lds > kSecMaxLds) return hipSuccess;
+  *handled = true;
+  hipLaunchKernelGGL((gemv_q4k_sec<M, OutT>), dim3((tiles + per - 1) / per), dim3(threads), lds, stream,
+                     static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out),
+                     a.n, a.k, per);
+  return hipGetLastError();
+}
+
+// 2 <= M <= 8: the sector-aligned kernel, else the LDS multi-tile kernel, else one super-block per step.
+template <int M, typename OutT>
+static hipError_t launch_multirow(const GemvArgs& a, hipStream_t stream) {
+  bool done = false;
+  hipError_t status = launch_sec<M, OutT>(a, stream, &done);
+  if (done) return status;
+  status = launch_mt<M, OutT>(a, stream, &done);
+  if (done) return status;
+  return launch_mfma<M, OutT>(a, stream);
+}
+
 template <typename OutT>
 static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream, bool* handled) {
   *handled = true;
   if (a.m == 1 && a.k % 4096 == 0 && a.k <= 4 * 4096) return launch_m1_group<OutT>(&a, 1, stream);
-  hipError_t status = hipSuccess;
-  bool mt = false;
   switch (a.m) {
-    case 2: status = launch_mt<2, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<2, OutT>(a, stream); return status;
-    case 3: status = launch_mt<3, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<3, OutT>(a, stream); return status;
-    case 4: status = launch_mt<4, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<4, OutT>(a, stream); return status;
-    case 5: status = launch_mt<5, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<5, OutT>(a, stream); return status;
-    case 6: status = launch_mt<6, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<6, OutT>(a, stream); return status;
-    case 7: status = launch_mt<7, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<7, OutT>(a, stream); return status;
-    case 8: status = launch_mt<8, OutT>(a, stream, &mt); if (!mt) status = launch_mfma<8, OutT>(a, stream); return status;
+    case 2: return launch_multirow<2, OutT>(a, stream);
+    case 3: return launch_multirow<3, OutT>(a, stream);
+    case 4: return launch_multirow<4, OutT>(a, stream);
+    case 5: return launch_multirow<5, OutT>(a, stream);
+    case 6: return launch_multirow<6, OutT>(a, stream);
+    case 7: return launch_multirow<7, OutT>(a, stream);
+    case 8: return launch_multirow<8, OutT>(a, stream);
     default: *handled = false; return hipSuccess;
   }
 }

@@ -139,9 +139,14 @@ def test_gemv_q6k_tall_rows_each_within_tolerance(hip_device, c_oracle, n):
 
 
 @pytest.mark.parametrize("m,n,k", [
-    (8, 8200, 4096),    # two 16-row tiles per wave, ragged last tile pair
-    (5, 4100, 12288),   # three super-blocks per wave, x of 120 KiB in LDS
-    (3, 9000, 2560),    # five waves per workgroup (ten super-blocks)
+    (8, 8200, 4096),    # sector-aligned kernel, two tiles per workgroup, ragged last tile
+    (6, 12296, 4096),   # sector-aligned, three tiles per workgroup, last workgroup one tile
+    (3, 8200, 8192),    # sector-aligned, two tiles x eight K ranges (1024 threads)
+    (4, 4101, 12288),   # sector-aligned for a long row, twelve K ranges, ragged rows
+    (2, 100, 16384),    # sector-aligned, sixteen K ranges of one 16-row tile
+    (5, 4100, 12288),   # x too large for the sector kernel: three super-blocks per wave, x in LDS
+    (8, 4100, 4096),    # narrow matrix: the LDS multi-tile kernel
+    (3, 9000, 2560),    # K not a multiple of 1024: two tiles per wave, five waves
     (2, 40, 256),       # one super-block, one wave
     (4, 8200, 512),     # two tiles per wave and a single wave: the wave stores both tiles
     (8, 1024, 12288),   # x too large for LDS: the one-super-block-per-step kernel

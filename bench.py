@@ -114,6 +114,32 @@ class GroupLinear:
             b.release()
 
 
+class SwigluLinear:
+    """An MLP's gate and up matrices launched as one SwiGLU GEMV: out = silu(x Wg^T) * (x Wu^T)."""
+
+    def __init__(self, device, encoding, m, n, k, out_dtype, copies, seed, x=None):
+        from tests import gguf_cases as cases
+
+        self.device, self.encoding, self.m, self.n, self.k = device, encoding, m, n, k
+        self.weights = []
+        for i in range(2):
+            raw = cases.weight(n, k, encoding, seed + 2 * i)
+            first = device.from_numpy(raw)
+            self.weights.append([first] + [device.empty(raw.shape, "uint8").copy_from(first) for _ in range(copies - 1)])
+        self.x = x if x is not None else device.from_numpy(cases.activation(m, k, seed + 1))
+        self.out = device.empty((m, n), out_dtype)
+        self.exe = device.load("gguf_gemv_swiglu", encoding=encoding, out_dtype=out_dtype)
+        self.calls = [self.exe.bind(self.x, self.weights[0][c], self.weights[1][c], self.out) for c in range(copies)]
+        self.bytes = 2 * weight_bytes(encoding, n, k) + 2 * m * k + np.dtype(out_dtype).itemsize * m * n
+        self.flops = 4 * m * n * k
+
+    def release(self):
+        for ws in self.weights:
+            for b in ws:
+                b.release()
+        self.out.release()
+
+
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_q4k_m1_qwen3_mlp.md")
 
 
@@ -429,6 +455,28 @@ def run_details(device, x4096, log, only=None):
     # the headline step as three single-matrix launches (gate, up, down)
     if wanted("C2_step_m1_three_launches"):
         three_launch_step(device, x4096, log, details)
+
+    # the MLP as a decode step runs it: gate + up with the SwiGLU epilogue in one launch, then
+    # down on its output (the headline step leaves the SwiGLU between them out)
+    if wanted("C2_q4k_gemv_swiglu_m1_12288x4096") or wanted("C2_step_m1_swiglu"):
+        copies = copies_for(2 * weight_bytes("q4_k", 12288, 4096) + weight_bytes("q4_k", 4096, 12288))
+        fused = SwigluLinear(device, "q4_k", 1, 12288, 4096, "float16", copies, 60, x=x4096)
+        launches = 60
+        seconds = time_launches(device, [fused.calls[i % copies].launch for i in range(launches)]) / launches
+        gbs = fused.bytes / seconds / 1e9
+        details["C2_q4k_gemv_swiglu_m1_12288x4096"] = {"us": round(seconds * 1e6, 3), "GB/s": round(gbs, 1),
+                                                       "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
+        log("C2_q4k_gemv_swiglu_m1_12288x4096", details["C2_q4k_gemv_swiglu_m1_12288x4096"])
+        down = Linear(device, "gguf_gemv", "q4_k", 1, 4096, 12288, "float16", copies, 64, x=fused.out)
+        steps = 50
+        seconds = time_launches(device, rotated_launches([fused, down], steps)) / steps
+        step_bytes = fused.bytes + down.bytes
+        details["C2_step_m1_swiglu"] = {"us": round(seconds * 1e6, 3), "GB/s": round(step_bytes / seconds / 1e9, 1),
+                                        "hbm_frac": round(step_bytes / seconds / 1e9 / HBM_PEAK_GBS, 4),
+                                        "launches": 2}
+        log("C2_step_m1_swiglu", details["C2_step_m1_swiglu"])
+        down.release()
+        fused.release()
 
     for m in (1, 4, 8):
         gemv_case(f"C2_q4k_gemv_m{m}_12288x4096", "q4_k", m, 12288, 4096, "float16")

@@ -94,6 +94,25 @@ int32_t tensor_gguf_linear_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 int32_t tensor_gguf_gemv_group_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 
 /*
+ * Decode GEMV of an MLP's gate and up projections with the SwiGLU epilogue:
+ * out[m, n] = silu(g) * u, silu(g) = g / (1 + exp(-g)), where g and u are the
+ * fp32 sums x[m, :] . dequant(W_gate)[n, :] and x[m, :] . dequant(W_up)[n, :]
+ * (nothing is rounded before the epilogue).  Replaces the reference's
+ * two-RHS packed-integer matmul with its SwiGLU output
+ * (src/tensor/compiler/webgpu/schedules/packed_integer.py:26-31, epilogue
+ * :204-205); the showcase path would take two gemv_packed launches and an
+ * elementwise kernel.  One launch: the Q4_K M = 1 kernel with gate and up rows
+ * in one workgroup when K is a multiple of 4096 (at most 16384), else the
+ * generic decode kernels with a gate / up row pair per wave.  Arguments:
+ *   0 x      buffer fp16  [M, K], 1 <= M <= TENSOR_GGUF_GEMV_MAX_M
+ *   1 w_gate buffer uint8 [N, K/QK*BLOCK]
+ *   2 w_up   buffer uint8 [N, K/QK*BLOCK]
+ *   3 out    buffer fp16 or fp32 [M, N]
+ *   4 type   scalar uint32 GGML type id of both matrices
+ */
+int32_t tensor_gguf_gemv_swiglu_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/*
  * Dequantize raw GGUF rows: out[n, k] = dequant(W)[n, k], exact in fp32 and
  * round-to-nearest-even in fp16 (block decoding of
  * benchmarks/kernels/showcase/triton_kernels.py:134-181, the decode_ggml

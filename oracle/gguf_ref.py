@@ -112,6 +112,22 @@ def gemm_reference(x: np.ndarray, raw: np.ndarray, ggml_type: int, n: int, k: in
     return xr.reshape(-1, k) @ w.T
 
 
+def silu(g: np.ndarray) -> np.ndarray:
+    """g / (1 + exp(-g)) in fp64, the reference's SwiGLU gate
+    (src/tensor/compiler/webgpu/schedules/packed_integer.py:204-205)."""
+    g = np.asarray(g, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return g / (1.0 + np.exp(-g))
+
+
+def swiglu_reference(x: np.ndarray, raw_gate: np.ndarray, raw_up: np.ndarray, ggml_type: int, n: int,
+                     k: int) -> np.ndarray:
+    """Gate / up pair with the SwiGLU epilogue: silu(x W_gate^T) * (x W_up^T), both
+    products the decode oracle's (fp32 operands, fp64 sums), the epilogue in fp64
+    (packed_integer.py:204-205 applies it to the two fp32 accumulators)."""
+    return silu(gemv_reference(x, raw_gate, ggml_type, n, k)) * gemv_reference(x, raw_up, ggml_type, n, k)
+
+
 def relative_l2(actual: np.ndarray, expected: np.ndarray) -> float:
     """external_baselines.py:49-62: |a - e|_2 / max(|e|_2, 1e-12)."""
     a = np.asarray(actual, dtype=np.float64).reshape(-1)

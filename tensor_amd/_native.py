@@ -21,6 +21,7 @@ KERNELS = (
     "tensor_gguf_gemm_v1",
     "tensor_gguf_linear_v1",
     "tensor_gguf_gemv_group_v1",
+    "tensor_gguf_gemv_swiglu_v1",
     "tensor_gguf_dequant_v1",
 )
 

@@ -126,6 +126,12 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t* scales, int sub, in
   }
 }
 
+// SwiGLU epilogue of a gate / up pair in fp32: silu(g) * u = g / (1 + exp(-g)) * u
+// (src/tensor/compiler/webgpu/schedules/packed_integer.py:204-205).
+__device__ __forceinline__ float swiglu(float g, float u) {
+  return g / (1.0f + expf(-g)) * u;
+}
+
 template <typename T>
 __device__ __forceinline__ void store_out(T* out, size_t index, float v);
 template <>

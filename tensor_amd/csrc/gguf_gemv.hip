@@ -22,25 +22,55 @@
 namespace tensor_gguf {
 
 // x is fp16 [M, K] (row stride K), W raw rows of row_bytes, out [M, N].
+//
+// SWIGLU = true fuses the gate / up pair of an MLP: a wave owns one output row n,
+// its two "rows" are row n of the gate matrix w and of the up matrix w2, and it
+// stores silu(gate) * up from the fp32 dot products (no rounding in between).
+
+// Row r of a wave: rows row0 .. row0 + R - 1 of w, or row row0 of w (r = 0) and w2 (r = 1).
+template <bool PAIR>
+__device__ __forceinline__ const uint8_t* pair_row(const uint8_t* w, const uint8_t* w2, int row0, int r,
+                                                   size_t row_bytes) {
+  return PAIR ? (r == 0 ? w : w2) + (size_t)row0 * row_bytes : w + (size_t)(row0 + r) * row_bytes;
+}
+
+// Reduce each row's lane partials over the wave and store them (lane 0), or the pair's epilogue.
+template <bool PAIR, int M, int R, typename OutT>
+__device__ __forceinline__ void store_rows(float (&acc)[M][R], OutT* out, int n_rows, int row0, int rows, int lane) {
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    if constexpr (PAIR) {
+      const float g = wave_sum(acc[m][0]), u = wave_sum(acc[m][1]);
+      if (lane == 0) store_out<OutT>(out, (size_t)m * n_rows + row0, swiglu(g, u));
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float v = wave_sum(acc[m][r]);
+        if (lane == 0 && r < rows) store_out<OutT>(out, (size_t)m * n_rows + row0 + r, v);
+      }
+    }
+  }
+}
 
 // ------------------------------------------------------------------ Q4_K ---
 // Lane plan: 8 lanes per 144-byte super-block, 8 super-blocks per step.
 // Lane (slot, c): super-block slot = lane/8, 16-byte quant chunk c = lane%8,
 // i.e. pair j = c/2 (sub-blocks 2j, 2j+1) and half h = c%2 of its 32 bytes.
 // Low nibbles are elements 64j+16h+t of the block, high nibbles 64j+32+16h+t.
-template <int M, int R, typename OutT>
+template <int M, int R, typename OutT, bool SWIGLU = false>
 __global__ __launch_bounds__(256) void gemv_q4k(const _Float16* __restrict__ x,
                                                 const uint8_t* __restrict__ w,
-                                                OutT* __restrict__ out, int n_rows, int k) {
+                                                OutT* __restrict__ out, int n_rows, int k,
+                                                const uint8_t* __restrict__ w2 = nullptr) {
   const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (SWIGLU ? 1 : R);
   if (row0 >= n_rows) return;
   const int blocks = k >> 8;
   const size_t row_bytes = (size_t)blocks * 144;
   const int slot = lane >> 3, c = lane & 7, j = c >> 1, h = c & 1;
   const int quant_offset = 16 + 32 * j + 16 * h;
   const int x_offset = 64 * j + 16 * h;
-  const int rows = min(R, n_rows - row0);
+  const int rows = SWIGLU ? R : min(R, n_rows - row0);
   float acc[M][R];
 #pragma unroll
   for (int m = 0; m < M; ++m)
@@ -62,7 +92,7 @@ __global__ __launch_bounds__(256) void gemv_q4k(const _Float16* __restrict__ x,
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (r < rows) {
-        const uint8_t* block = w + (size_t)(row0 + r) * row_bytes + (size_t)b * 144;
+        const uint8_t* block = pair_row<SWIGLU>(w, w2, row0, r, row_bytes) + (size_t)b * 144;
         head[r] = load16(block);
         quant[r] = load16(block + quant_offset);
       }
@@ -109,13 +139,7 @@ __global__ __launch_bounds__(256) void gemv_q4k(const _Float16* __restrict__ x,
       }
     }
   }
-#pragma unroll
-  for (int m = 0; m < M; ++m)
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float v = wave_sum(acc[m][r]);
-      if (lane == 0 && r < rows) store_out<OutT>(out, (size_t)m * n_rows + row0 + r, v);
-    }
+  store_rows<SWIGLU>(acc, out, n_rows, row0, rows, lane);
 }
 
 // ------------------------------------------------------------------ Q6_K ---
@@ -124,17 +148,18 @@ __global__ __launch_bounds__(256) void gemv_q4k(const _Float16* __restrict__ x,
 // Its 16 bytes of ql at 64hh+l0 (quarters 0 and 2), of ql at 64hh+32+l0
 // (quarters 1 and 3) and of qh at 128+32hh+l0 decode the four 16-element
 // runs 128hh + 32c + l0 + t (c = 0..3), each one scale group.
-template <int M, int R, typename OutT>
+template <int M, int R, typename OutT, bool SWIGLU = false>
 __global__ __launch_bounds__(256) void gemv_q6k(const _Float16* __restrict__ x,
                                                 const uint8_t* __restrict__ w,
-                                                OutT* __restrict__ out, int n_rows, int k) {
+                                                OutT* __restrict__ out, int n_rows, int k,
+                                                const uint8_t* __restrict__ w2 = nullptr) {
   const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (SWIGLU ? 1 : R);
   if (row0 >= n_rows) return;
   const int blocks = k >> 8;
   const size_t row_bytes = (size_t)blocks * 210;
   const int slot = lane >> 2, part = lane & 3, hh = part >> 1, l0 = 16 * (part & 1);
-  const int rows = min(R, n_rows - row0);
+  const int rows = SWIGLU ? R : min(R, n_rows - row0);
   float acc[M][R];
 #pragma unroll
   for (int m = 0; m < M; ++m)
@@ -159,7 +184,7 @@ __global__ __launch_bounds__(256) void gemv_q6k(const _Float16* __restrict__ x,
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (r < rows) {
-        const uint8_t* block = w + (size_t)(row0 + r) * row_bytes + (size_t)b * 210;
+        const uint8_t* block = pair_row<SWIGLU>(w, w2, row0, r, row_bytes) + (size_t)b * 210;
         qa[r] = load16(block + 64 * hh + l0);
         qb[r] = load16(block + 64 * hh + 32 + l0);
         qh[r] = load16(block + 128 + 32 * hh + l0);
@@ -217,31 +242,26 @@ __global__ __launch_bounds__(256) void gemv_q6k(const _Float16* __restrict__ x,
       }
     }
   }
-#pragma unroll
-  for (int m = 0; m < M; ++m)
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float v = wave_sum(acc[m][r]);
-      if (lane == 0 && r < rows) store_out<OutT>(out, (size_t)m * n_rows + row0 + r, v);
-    }
+  store_rows<SWIGLU>(acc, out, n_rows, row0, rows, lane);
 }
 
 // ------------------------------------------------------------ Q8_0, Q4_0 ---
 // Lane plan: one 32-element block per lane, 64 blocks per step.
-template <int TYPE, int M, int R, typename OutT>
+template <int TYPE, int M, int R, typename OutT, bool SWIGLU = false>
 __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
                                                 const uint8_t* __restrict__ w,
-                                                OutT* __restrict__ out, int n_rows, int k) {
+                                                OutT* __restrict__ out, int n_rows, int k,
+                                                const uint8_t* __restrict__ w2 = nullptr) {
   constexpr int kBytes = TYPE == kQ8_0 ? 34 : 18;
   // bias removed per block: 1024 from the fp16 widening, plus 128 for the
   // sign flip of Q8_0 codes or 8 for the Q4_0 code offset
   constexpr float kBias = TYPE == kQ8_0 ? 1152.0f : 1032.0f;
   const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (SWIGLU ? 1 : R);
   if (row0 >= n_rows) return;
   const int blocks = k >> 5;
   const size_t row_bytes = (size_t)blocks * kBytes;
-  const int rows = min(R, n_rows - row0);
+  const int rows = SWIGLU ? R : min(R, n_rows - row0);
   float acc[M][R];
 #pragma unroll
   for (int m = 0; m < M; ++m)
@@ -262,7 +282,7 @@ __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (r < rows) {
-        const uint8_t* block = w + (size_t)(row0 + r) * row_bytes + (size_t)b * kBytes;
+        const uint8_t* block = pair_row<SWIGLU>(w, w2, row0, r, row_bytes) + (size_t)b * kBytes;
         head[r] = (uint32_t)block[0] | ((uint32_t)block[1] << 8);
         q0[r] = load16(block + 2);
         if (TYPE == kQ8_0) q1[r] = load16(block + 18);
@@ -312,13 +332,7 @@ __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
       for (int m = 0; m < M; ++m) acc[m][r] = fmaf(d, a[m] - kBias * sx[m], acc[m][r]);
     }
   }
-#pragma unroll
-  for (int m = 0; m < M; ++m)
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float v = wave_sum(acc[m][r]);
-      if (lane == 0 && r < rows) store_out<OutT>(out, (size_t)m * n_rows + row0 + r, v);
-    }
+  store_rows<SWIGLU>(acc, out, n_rows, row0, rows, lane);
 }
 
 // --------------------------------------------------------------- launch ---
@@ -363,6 +377,57 @@ static hipError_t launch_out(const GemvArgs& a, hipStream_t stream) {
     case 8: return launch_m<8, OutT>(a, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+// SwiGLU pairs on the generic kernels: one output row per wave, R = 2 (gate row, up row).
+template <int M, typename OutT>
+static hipError_t launch_swiglu_m(const GemvArgs& a, const uint8_t* w_up, hipStream_t stream) {
+  const _Float16* x = static_cast<const _Float16*>(a.x);
+  const uint8_t* w = static_cast<const uint8_t*>(a.w);
+  OutT* out = static_cast<OutT*>(a.out);
+  const dim3 grid((a.n + 3) / 4), block(256);
+  switch (a.type) {
+    case kQ4_K:
+      hipLaunchKernelGGL((gemv_q4k<M, 2, OutT, true>), grid, block, 0, stream, x, w, out, a.n, a.k, w_up);
+      break;
+    case kQ6_K:
+      hipLaunchKernelGGL((gemv_q6k<M, 2, OutT, true>), grid, block, 0, stream, x, w, out, a.n, a.k, w_up);
+      break;
+    case kQ8_0:
+      hipLaunchKernelGGL((gemv_q32<kQ8_0, M, 2, OutT, true>), grid, block, 0, stream, x, w, out, a.n, a.k, w_up);
+      break;
+    case kQ4_0:
+      hipLaunchKernelGGL((gemv_q32<kQ4_0, M, 2, OutT, true>), grid, block, 0, stream, x, w, out, a.n, a.k, w_up);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <typename OutT>
+static hipError_t launch_swiglu_out(const GemvArgs& a, const uint8_t* w_up, hipStream_t stream) {
+  switch (a.m) {
+    case 1: return launch_swiglu_m<1, OutT>(a, w_up, stream);
+    case 2: return launch_swiglu_m<2, OutT>(a, w_up, stream);
+    case 3: return launch_swiglu_m<3, OutT>(a, w_up, stream);
+    case 4: return launch_swiglu_m<4, OutT>(a, w_up, stream);
+    case 5: return launch_swiglu_m<5, OutT>(a, w_up, stream);
+    case 6: return launch_swiglu_m<6, OutT>(a, w_up, stream);
+    case 7: return launch_swiglu_m<7, OutT>(a, w_up, stream);
+    case 8: return launch_swiglu_m<8, OutT>(a, w_up, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemv_swiglu(const GemvArgs& a, const void* w_up, hipStream_t stream) {
+  if (a.type == kQ4_K) {
+    bool handled = false;
+    const hipError_t status = launch_gemv_q4k_swiglu_fast(a, w_up, stream, &handled);
+    if (handled) return status;
+  }
+  const uint8_t* up = static_cast<const uint8_t*>(w_up);
+  return a.out_half ? launch_swiglu_out<_Float16>(a, up, stream) : launch_swiglu_out<float>(a, up, stream);
 }
 
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t stream) {

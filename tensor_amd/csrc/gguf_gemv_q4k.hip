@@ -83,22 +83,33 @@ constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
 // the weight loads from sinking below the x staging, and the workgroup
 // barrier fences LDS only, so decoding starts as soon as this wave's own
 // bytes have arrived.
-template <int STEPS, int WAVES, int MATS, typename OutT>
+//
+// SWIGLU = true (MATS = 2: gate, up): waves 0 .. WAVES/2-1 take rows r .. of
+// the gate matrix and the other half the same rows of the up matrix; the up
+// waves hand their sums over in LDS and the gate waves store silu(gate) * up
+// to g.out[0], so the pair's products never leave the workgroup.
+template <int STEPS, int WAVES, int MATS, typename OutT, bool SWIGLU = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __restrict__ x, GemvGroup<OutT> g) {
   constexpr int K = STEPS * 4096, ROW_BYTES = STEPS * 16 * 144, T = WAVES * 64;
   constexpr int XC = (K / 8 + T - 1) / T;  // 16-byte x chunks per thread
+  constexpr int PAIRS = WAVES / 2;
+  static_assert(!SWIGLU || MATS == 2, "the SwiGLU pairing takes a gate and an up matrix");
   __shared__ __attribute__((aligned(16))) uint8_t xlds[K * 2 + K / 4];
   __shared__ __attribute__((aligned(16))) float sxl[K / 32];
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   int mat = 0, block = blockIdx.x;
+  if constexpr (SWIGLU) {
+    mat = wv >= PAIRS ? 1 : 0;
+  } else {
 #pragma unroll
-  for (int i = 1; i < MATS; ++i) {
-    if (block < g.blocks[i - 1]) break;
-    block -= g.blocks[i - 1];
-    mat = i;
+    for (int i = 1; i < MATS; ++i) {
+      if (block < g.blocks[i - 1]) break;
+      block -= g.blocks[i - 1];
+      mat = i;
+    }
   }
   const int n_rows = g.n[mat];
-  const int row = block * WAVES + (threadIdx.x >> 6);
+  const int row = SWIGLU ? block * PAIRS + wv - mat * PAIRS : block * WAVES + wv;
   const int slot = lane >> 2, j = lane & 3;
 
   uint4 xr[XC];
@@ -136,7 +147,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __rest
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-  if (row >= n_rows) return;
+  // (a SwiGLU pair past the last row still decodes the clamped row: it meets the barrier below)
+  if (!SWIGLU && row >= n_rows) return;
 
   const PairSelect sel(j);
   float total = 0.f;
@@ -175,7 +187,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __rest
     total = fmaf(-dmin * (float)(mns >> 8), sx.y, total);
   }
   const float v = wave_sum_dpp(total);
-  if (lane == 0) store_out<OutT>(g.out[mat], (size_t)row, v);
+  if constexpr (SWIGLU) {
+    __shared__ float up_sum[PAIRS];
+    const int pair = wv - mat * PAIRS;
+    if (mat == 1 && lane == 0) up_sum[pair] = v;
+    __syncthreads();
+    if (mat == 0 && lane == 0 && row < n_rows) store_out<OutT>(g.out[0], (size_t)row, swiglu(v, up_sum[pair]));
+  } else {
+    if (lane == 0) store_out<OutT>(g.out[mat], (size_t)row, v);
+  }
 }
 
 // ------------------------------------------------------- 2 <= M, MFMA ---
@@ -693,6 +713,44 @@ bool gemv_q4k_group_supported(int m, int k) { return m == 1 && k % 4096 == 0 && 
 
 hipError_t launch_gemv_q4k_group(const GemvArgs* a, int count, hipStream_t stream, int waves) {
   return a[0].out_half ? launch_m1_group<_Float16>(a, count, stream, waves) : launch_m1_group<float>(a, count, stream, waves);
+}
+
+// M = 1 SwiGLU pairs: WAVES / 2 gate rows and the same up rows per workgroup.
+template <int WAVES, typename OutT>
+static hipError_t launch_m1_swiglu(const GemvArgs& a, const void* w_up, hipStream_t stream) {
+  GemvGroup<OutT> g{};
+  g.w[0] = static_cast<const uint8_t*>(a.w);
+  g.w[1] = static_cast<const uint8_t*>(w_up);
+  g.out[0] = g.out[1] = static_cast<OutT*>(a.out);
+  g.n[0] = g.n[1] = a.n;
+  g.blocks[0] = (a.n + WAVES / 2 - 1) / (WAVES / 2);
+  const _Float16* x = static_cast<const _Float16*>(a.x);
+  const dim3 grid(g.blocks[0]), block(WAVES * 64);
+  switch (a.k / 4096) {
+    case 1: hipLaunchKernelGGL((gemv_q4k_m1<1, WAVES, 2, OutT, true>), grid, block, 0, stream, x, g); break;
+    case 2: hipLaunchKernelGGL((gemv_q4k_m1<2, WAVES, 2, OutT, true>), grid, block, 0, stream, x, g); break;
+    case 3: hipLaunchKernelGGL((gemv_q4k_m1<3, WAVES, 2, OutT, true>), grid, block, 0, stream, x, g); break;
+    case 4: hipLaunchKernelGGL((gemv_q4k_m1<4, WAVES, 2, OutT, true>), grid, block, 0, stream, x, g); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <typename OutT>
+static hipError_t launch_m1_swiglu_waves(const GemvArgs& a, const void* w_up, hipStream_t stream, int waves) {
+  switch (waves > 0 ? waves : 8) {
+    case 8: return launch_m1_swiglu<8, OutT>(a, w_up, stream);
+    case 16: return launch_m1_swiglu<16, OutT>(a, w_up, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemv_q4k_swiglu_fast(const GemvArgs& a, const void* w_up, hipStream_t stream, bool* handled,
+                                       int waves) {
+  *handled = gemv_q4k_group_supported(a.m, a.k);
+  if (!*handled) return hipSuccess;
+  return a.out_half ? launch_m1_swiglu_waves<_Float16>(a, w_up, stream, waves)
+                    : launch_m1_swiglu_waves<float>(a, w_up, stream, waves);
 }
 
 }  // namespace tensor_gguf

@@ -47,6 +47,12 @@ hipError_t launch_gemv_q4k_fast(const GemvArgs& args, hipStream_t stream, bool* 
 bool gemv_q4k_group_supported(int m, int k);
 // waves: rows (one per wave) per workgroup; 0 takes the default, 4 / 8 / 16 fix it (for sweeps)
 hipError_t launch_gemv_q4k_group(const GemvArgs* args, int count, hipStream_t stream, int waves = 0);
+// Decode GEMV with the SwiGLU epilogue of an MLP: out = silu(x W_gate^T) * (x W_up^T),
+// args.w the gate matrix, w_up the up matrix of the same shape and encoding.
+hipError_t launch_gemv_swiglu(const GemvArgs& gate, const void* w_up, hipStream_t stream);
+// Its Q4_K M = 1 path (gate and up rows of one workgroup); waves: 8 or 16 per workgroup, 0 the default.
+hipError_t launch_gemv_q4k_swiglu_fast(const GemvArgs& gate, const void* w_up, hipStream_t stream, bool* handled,
+                                       int waves = 0);
 // Q6_K fast path (LDS-staged x, M = 1, K in {4096, 8192, 12288}).
 hipError_t launch_gemv_q6k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 hipError_t launch_dequant(const DequantArgs& args, hipStream_t stream);

@@ -205,9 +205,50 @@ int32_t group_call(const TensorCallV1* call, TensorErrorV1* error) {
   return TENSOR_OK;
 }
 
+// Gate / up pair with the SwiGLU epilogue: arguments [x, w_gate, w_up, out, type].
+int32_t swiglu_call(const TensorCallV1* call, TensorErrorV1* error) {
+  ok(error);
+  if (int32_t s = check_call(call, 5, error)) return s;
+  const int ordinal = call->stream.device_ordinal;
+  const TensorArgumentV1* a = call->arguments;
+  Format format;
+  if (int32_t s = check_type(a[4], &format, error)) return s;
+  if (int32_t s = check_matrix(a[0], "x", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT16, error)) return s;
+  if (int32_t s = check_matrix(a[1], "w_gate", ordinal, TENSOR_UINT8, TENSOR_UINT8, error)) return s;
+  if (int32_t s = check_matrix(a[2], "w_up", ordinal, TENSOR_UINT8, TENSOR_UINT8, error)) return s;
+  if (int32_t s = check_matrix(a[3], "out", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT32, error)) return s;
+  const int64_t m = a[0].buffer.shape[0], k = a[0].buffer.shape[1], n = a[1].buffer.shape[0];
+  if (m > tensor_gguf::kGemvMaxM)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "x: decode GEMV takes at most %d rows", tensor_gguf::kGemvMaxM);
+  if (k % format.qk || a[1].buffer.shape[1] != k / format.qk * format.bytes)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "w_gate: shape, stride or size mismatch");
+  if (a[2].buffer.shape[0] != n || a[2].buffer.shape[1] != a[1].buffer.shape[1])
+    return fail(error, TENSOR_ERROR_ARGUMENT, "w_up: shape differs from w_gate");
+  if (a[3].buffer.shape[0] != m || a[3].buffer.shape[1] != n)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "out: shape, stride or size mismatch");
+  if (int32_t s = check_device(call, error)) return s;
+  tensor_gguf::GemvArgs args;
+  args.x = reinterpret_cast<const void*>(a[0].buffer.address);
+  args.w = reinterpret_cast<const void*>(a[1].buffer.address);
+  args.out = reinterpret_cast<void*>(a[3].buffer.address);
+  args.type = (int)a[4].scalar;
+  args.m = (int)m;
+  args.n = (int)n;
+  args.k = (int)k;
+  args.out_half = a[3].dtype == TENSOR_FLOAT16;
+  hipError_t status = tensor_gguf::launch_gemv_swiglu(args, reinterpret_cast<const void*>(a[2].buffer.address),
+                                                      reinterpret_cast<hipStream_t>(call->stream.handle));
+  if (status != hipSuccess) return hip_fail(error, status, "GGUF SwiGLU GEMV launch");
+  return TENSOR_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int32_t tensor_gguf_gemv_swiglu_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  return swiglu_call(call, error);
+}
 
 int32_t tensor_gguf_gemv_v1(const TensorCallV1* call, TensorErrorV1* error) {
   return linear_call(call, error, Op::kGemv);

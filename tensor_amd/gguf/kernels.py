@@ -24,6 +24,7 @@ ENTRYPOINTS = {
     "gguf_gemm": "tensor_gguf_gemm_v1",
     "gguf_linear": "tensor_gguf_linear_v1",
     "gguf_gemv_group": "tensor_gguf_gemv_group_v1",
+    "gguf_gemv_swiglu": "tensor_gguf_gemv_swiglu_v1",
     "gguf_dequant": "tensor_gguf_dequant_v1",
 }
 GEMV_GROUP_MAX = 3  # TENSOR_GGUF_GEMV_GROUP_MAX
@@ -49,6 +50,8 @@ def manifest(kernel: str, encoding, out_dtype: str = "float16", count: int | Non
     ``gguf_gemv_group`` takes ``count`` (1..3) weight matrices that share the
     activations: arguments ``[x, w0, out0, w1, out1, ..., type]`` with row
     counts ``N0, N1, ...``; every other kernel takes no ``count``.
+    ``gguf_gemv_swiglu`` takes ``[x, w_gate, w_up, out, type]`` and stores
+    silu(x W_gate^T) * (x W_up^T).
     """
     if kernel not in ENTRYPOINTS:
         raise ValueError(f"unknown HIP kernel {kernel!r}; choose {', '.join(ENTRYPOINTS)}")
@@ -70,6 +73,14 @@ def manifest(kernel: str, encoding, out_dtype: str = "float16", count: int | Non
             arguments.append({"name": f"w{i}", "dtype": "uint8", "shape": [{"var": f"N{i}"}, _row_bytes(code)], "alignment": 16})
             arguments.append({"name": f"out{i}", "dtype": out_dtype, "shape": [{"var": "M"}, {"var": f"N{i}"}], "alignment": 16})
         arguments.append(type_argument)
+    elif kernel == "gguf_gemv_swiglu":
+        arguments = [
+            {"name": "x", "dtype": "float16", "shape": [{"var": "M"}, {"var": "K"}], "alignment": 16},
+            dict(weight, name="w_gate"),
+            dict(weight, name="w_up"),
+            {"name": "out", "dtype": out_dtype, "shape": [{"var": "M"}, {"var": "N"}], "alignment": 16},
+            type_argument,
+        ]
     elif kernel == "gguf_dequant":
         arguments = [
             weight,
@@ -104,6 +115,6 @@ def manifest(kernel: str, encoding, out_dtype: str = "float16", count: int | Non
         "launch": {"grid": [1, 1, 1], "block": [256, 1, 1], "shared_memory_bytes": 0},
         "ggml_type": code,
     }
-    if kernel in ("gguf_gemv", "gguf_gemv_group"):
+    if kernel in ("gguf_gemv", "gguf_gemv_group", "gguf_gemv_swiglu"):
         result["shape_domain"] = {"M": [1, GEMV_MAX_M]}
     return result

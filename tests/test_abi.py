@@ -228,6 +228,71 @@ def test_group_manifest_binds_each_matrix():
         kernels.manifest("gguf_gemv", "q4_k", count=2)
 
 
+class SwigluCall:
+    """A well-formed SwiGLU GEMV call [x, w_gate, w_up, out, type] with fake addresses."""
+
+    def __init__(self, m=1, n=64, k=512, type_=12, block=144, qk=256, up_rows=None):
+        shapes = [(m, k), (n, k // qk * block), (up_rows or n, k // qk * block), (m, n)]
+        dtypes, items = [10, 3, 3, 10], [2, 1, 1, 2]
+        self.keep = []
+        self.args = (abi.Argument * 5)()
+        for i, (shape, dtype, item) in enumerate(zip(shapes, dtypes, items)):
+            shp = (c.c_int64 * 2)(*shape)
+            strides = (c.c_int64 * 2)(shape[1] * item, item)
+            self.keep += [shp, strides]
+            self.args[i].kind = 1
+            self.args[i].dtype = dtype
+            self.args[i].buffer = abi.BufferDescriptor(0x10000 * (i + 1), shape[0] * shape[1] * item, shp, strides,
+                                                       2, dtype, 10, 0)
+        self.args[4].kind = 2
+        self.args[4].dtype = 7
+        self.args[4].scalar = type_
+        self.call = abi.CallDescriptor(1, 72, self.args, 5, 0, (c.c_uint32 * 3)(1, 1, 1),
+                                       (c.c_uint32 * 3)(256, 1, 1), 0, abi.StreamDescriptor(10, 0, 0))
+
+    def run(self):
+        error = abi.ErrorDescriptor()
+        status = _native.kernel("tensor_gguf_gemv_swiglu_v1")(c.byref(self.call), c.byref(error))
+        return status, error.message.decode()
+
+
+def test_swiglu_call_argument_checks():
+    call = SwigluCall()
+    call.call.argument_count = 4
+    assert call.run() == (ERR_ARG, "invalid argument count or flags")
+    assert SwigluCall(up_rows=63).run() == (ERR_ARG, "w_up: shape differs from w_gate")
+    call = SwigluCall()
+    call.args[2].dtype = call.args[2].buffer.dtype = 10  # fp16 in place of raw bytes
+    assert call.run() == (ERR_ARG, "w_up: wrong argument kind or dtype")
+    status, message = SwigluCall(m=9).run()
+    assert status == ERR_ARG and "at most 8" in message
+    call = SwigluCall()
+    call.keep[6][1] = 63  # out columns != N (a consistent [1, 63] descriptor)
+    call.keep[7][0] = 63 * 2
+    call.args[3].buffer.byte_size = 63 * 2
+    assert call.run() == (ERR_ARG, "out: shape, stride or size mismatch")
+    status, message = SwigluCall(type_=5).run()
+    assert status == ERR_ARG and "unsupported GGML type" in message
+    # a Q8_0 pair whose rows are not whole blocks
+    status, message = SwigluCall(k=40, type_=8, block=34, qk=32).run()
+    assert status == ERR_ARG and "w_gate" in message
+
+
+def test_swiglu_manifest_binds_gate_and_up():
+    manifest = kernels.manifest("gguf_gemv_swiglu", "q4_k", "float16")
+    assert manifest["entrypoint"] == "tensor_gguf_gemv_swiglu_v1" and manifest["outputs"] == ["out"]
+    assert [a["name"] for a in manifest["arguments"]] == ["x", "w_gate", "w_up", "out", "type"]
+    k, n = 4096, 12288
+    buffers = {"x": fake((1, k), "float16"), "w_gate": fake((n, k // 256 * 144), "uint8"),
+               "w_up": fake((n, k // 256 * 144), "uint8"), "out": fake((1, n), "float16")}
+    symbols, _ = bind_shapes(manifest, buffers)
+    assert symbols == {"M": 1, "N": n, "K": k}
+    with pytest.raises(ValueError):
+        bind_shapes(manifest, dict(buffers, w_up=fake((n - 16, k // 256 * 144), "uint8")))
+    with pytest.raises(ValueError, match="outside"):
+        bind_shapes(manifest, dict(buffers, x=fake((9, k), "float16"), out=fake((9, n), "float16")))
+
+
 # --------------------------------------------------------- manifest binding --
 
 def fake(shape, dtype):

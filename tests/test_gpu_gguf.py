@@ -219,6 +219,47 @@ def test_gemv_group_matches_single_launches(hip_device):
         b.release()
 
 
+def run_swiglu(device, encoding, x, gate, up, out_dtype):
+    exe = device.load("gguf_gemv_swiglu", encoding=encoding, out_dtype=out_dtype)
+    xb, gb, ub = device.from_numpy(x), device.from_numpy(gate), device.from_numpy(up)
+    out = device.empty((x.shape[0], gate.shape[0]), out_dtype)
+    device.fill_bytes(out, 0xFF)  # NaN in both fp16 and fp32
+    exe.launch(xb, gb, ub, out)
+    result = out.to_numpy()
+    for b in (xb, gb, ub, out):
+        b.release()
+    return result
+
+
+@pytest.mark.parametrize("encoding,m,n,k", [
+    ("q4_k", 1, 12288, 4096),   # C2 gate / up: the fused M = 1 kernel
+    ("q4_k", 1, 1003, 8192),    # fused kernel, two column steps, ragged last workgroup
+    ("q4_k", 1, 301, 2560),     # K not a multiple of 4096: generic gate / up pairs
+    ("q4_k", 4, 301, 4096),     # M > 1: generic pairs
+    ("q6_k", 1, 300, 4096),
+    ("q6_k", 3, 77, 512),
+    ("q8_0", 2, 100, 2560),
+    ("q4_0", 8, 65, 1024),
+])
+def test_gemv_swiglu_parity(hip_device, encoding, m, n, k):
+    """silu(x W_gate^T) * (x W_up^T) in one launch against the oracle's composition."""
+    code = Q.ggml_type(encoding)
+    note("gemv-swiglu", encoding, m, n, k)
+    gate = cases.weight(n, k, encoding, 110 + m)
+    up = cases.weight(n, k, encoding, 120 + m)
+    x = cases.activation(m, k, 130 + m)
+    expected = R.swiglu_reference(x, gate, up, code, n, k)
+    for out_dtype in ("float16", "float32"):
+        got = run_swiglu(hip_device, encoding, x, gate, up, out_dtype)
+        assert not np.isnan(got).any(), out_dtype
+        err = R.relative_l2(got, expected)
+        assert err <= TOLERANCE, (encoding, m, out_dtype, err)
+        if out_dtype == "float32":
+            assert err <= 2e-4, (encoding, m, err)
+    zero = run_swiglu(hip_device, encoding, np.zeros_like(x), gate, up, "float32")
+    assert np.array_equal(zero, np.zeros_like(zero))
+
+
 @pytest.mark.parametrize("encoding", ["q4_k", "q6_k"])
 def test_gemv_input_families_and_graph_replay(hip_device, encoding):
     """One captured graph, replayed after x changes: random, x*-1.5, zeros."""

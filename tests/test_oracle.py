@@ -211,6 +211,35 @@ def test_prefill_reference_differs_from_decode_reference():
     assert 1e-6 < R.relative_l2(b, a) < 2e-3
 
 
+def test_silu_closed_forms():
+    """silu(g) = g * sigmoid(g): scipy's logistic, the odd-part identity silu(g) - silu(-g) = g,
+    its limits and zero (no NaN where exp(-g) overflows)."""
+    from scipy.special import expit
+
+    g = np.linspace(-30.0, 30.0, 601)
+    np.testing.assert_allclose(R.silu(g), g * expit(g), rtol=1e-13, atol=1e-300)
+    np.testing.assert_allclose(R.silu(g) - R.silu(-g), g, rtol=0, atol=1e-12)
+    assert R.silu(0.0) == 0.0
+    assert R.silu(-1000.0) == 0.0 and R.silu(1000.0) == 1000.0
+
+
+def test_swiglu_reference_composition(c_oracle):
+    """silu of the gate product times the up product, against the C decoder and scipy: a swap of
+    gate and up, or the gate taken from the wrong matrix, changes the result."""
+    from scipy.special import expit
+
+    n, k = 48, 512
+    gate = Q.sample_weight(n, k, Q.Q4_K, seed=11)
+    up = Q.sample_weight(n, k, Q.Q4_K, seed=12)
+    x = Q.sample_activation(3, k, seed=13).astype(np.float32).astype(np.float64)
+    g = x @ c_oracle.dequantize(gate, Q.Q4_K, n, k).astype(np.float64).T
+    u = x @ c_oracle.dequantize(up, Q.Q4_K, n, k).astype(np.float64).T
+    got = R.swiglu_reference(x, gate, up, Q.Q4_K, n, k)
+    np.testing.assert_allclose(got, g * expit(g) * u, rtol=1e-12, atol=1e-15)
+    swapped = R.swiglu_reference(x, up, gate, Q.Q4_K, n, k)
+    assert R.relative_l2(swapped, got) > 0.1
+
+
 def test_relative_l2_definition():
     e = np.array([3.0, 4.0])
     assert R.relative_l2(e + np.array([0.3, 0.4]), e) == pytest.approx(0.1)

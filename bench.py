@@ -10,7 +10,12 @@ Protocol (after benchmarks/kernels/showcase/benchmark.py:66-94): every launch
 is bound once (allocation-free BoundCall), the K steps are captured into one
 HIP graph, and the graph replay is timed with HIP events recorded on the
 launch stream.  Weights rotate through distinct copies (>= 3 x 256 MiB per
-rotation) so no launch finds its weights in the 256 MiB MALL.
+rotation) so no launch finds its weights in the 256 MiB MALL.  Before the timed
+replays every sequence is replayed, untimed, for WARM_SECONDS: an MI355X that
+has idled through the host-side set-up of a case starts in deep sleep and needs
+~30 ms of sustained load to reach its steady clocks (measured on the LM head:
+123 us per launch over the first 100 launches, 93 us from the fourth hundred
+on), so shorter warm-ups time the clock ramp instead of the kernel.
 
 Also reported: ``roofline`` for the dominant kernel (the grouped gate + up
 GEMV, 2 x 12288 x 4096; its HBM ``traffic`` is the per-launch figure measured
@@ -172,10 +177,21 @@ def time_launches(device, launches, replays=3):
     return time_graph(device, launches, replays)
 
 
+WARM_SECONDS = 0.1  # untimed replay before each timed sequence (steady clocks; module docstring)
+
+
+def warm(device, run):
+    """Call ``run`` (which enqueues GPU work) back to back until WARM_SECONDS have passed."""
+    start = time.perf_counter()
+    while True:
+        run()
+        device.synchronize()
+        if time.perf_counter() - start >= WARM_SECONDS:
+            return
+
+
 def time_eager(device, launches, replays=3):
-    for launch in launches:
-        launch()
-    device.synchronize()
+    warm(device, lambda: [launch() for launch in launches])
     samples = []
     for _ in range(replays):
         start = device.record_event(timing=True)
@@ -193,8 +209,7 @@ def time_graph(device, launches, replays=3):
     """Capture ``launches`` (callables) into one graph; return the median seconds of one replay."""
     graph = device.graph(lambda: [launch() for launch in launches])
     try:
-        graph.replay()
-        device.synchronize()
+        warm(device, graph.replay)
         samples = []
         for _ in range(replays):
             start = device.record_event(timing=True)

@@ -330,6 +330,8 @@ def main():
                         help="run only the details cases whose name starts with PREFIX (for profiling one kernel)")
     parser.add_argument("--eager-only", action="store_true",
                         help="stop after the eager warmup launches (for per-dispatch counter runs)")
+    parser.add_argument("--warm-seconds", type=float, default=WARM_SECONDS,
+                        help="untimed replay before each timed sequence (0: one replay, e.g. for counter runs)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -337,8 +339,9 @@ def main():
         return 2
     if args.steps < 1 or args.warmup < 0:
         parser.error("steps must be >= 1 and warmup >= 0")
-    global TIMING
+    global TIMING, WARM_SECONDS
     TIMING = args.timing
+    WARM_SECONDS = max(0.0, args.warm_seconds)
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import tensor_amd as tx

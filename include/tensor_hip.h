@@ -149,6 +149,12 @@ int32_t tensor_hip_device_synchronize(TensorErrorV1 *error);
 
 int32_t tensor_hip_malloc(uint64_t bytes, uint64_t *address, TensorErrorV1 *error);
 int32_t tensor_hip_free(uint64_t address, TensorErrorV1 *error);
+/* Which device an address belongs to, for DLPack imports (the reference checks an
+ * imported pointer with cuPointerGetAttribute, src/tensor/providers/cuda/device.py:296-309):
+ * *ordinal = the owning device, *device_memory = 1 for device (or managed) memory,
+ * 0 for host memory.  An address this runtime does not know is TENSOR_ERROR_PROVIDER. */
+int32_t tensor_hip_pointer_device(uint64_t address, int32_t *ordinal, int32_t *device_memory,
+                                  TensorErrorV1 *error);
 /* Host <-> device copies are synchronous with respect to the host. */
 int32_t tensor_hip_copy_htod(uint64_t dst, const void *src, uint64_t bytes,
                              uint64_t stream, TensorErrorV1 *error);

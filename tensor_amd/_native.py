@@ -55,6 +55,7 @@ SERVICES = {
     "tensor_hip_device_synchronize": [],
     "tensor_hip_malloc": [_u64, c.POINTER(_u64)],
     "tensor_hip_free": [_u64],
+    "tensor_hip_pointer_device": [_u64, c.POINTER(_i32), c.POINTER(_i32)],
     "tensor_hip_copy_htod": [_u64, c.c_void_p, _u64, _u64],
     "tensor_hip_copy_dtoh": [c.c_void_p, _u64, _u64, _u64],
     "tensor_hip_copy_dtod": [_u64, _u64, _u64, _u64],

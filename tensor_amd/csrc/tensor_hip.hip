@@ -347,6 +347,17 @@ int32_t tensor_hip_free(uint64_t address, TensorErrorV1* error) {
   return ok(error);
 }
 
+int32_t tensor_hip_pointer_device(uint64_t address, int32_t* ordinal, int32_t* device_memory,
+                                  TensorErrorV1* error) {
+  if (!ordinal || !device_memory) return fail(error, TENSOR_ERROR_ARGUMENT, "null result pointer");
+  hipPointerAttribute_t attributes;
+  std::memset(&attributes, 0, sizeof(attributes));
+  HIP_TRY(hipPointerGetAttributes(&attributes, reinterpret_cast<const void*>(address)), "hipPointerGetAttributes");
+  *ordinal = attributes.device;
+  *device_memory = attributes.type == hipMemoryTypeDevice || attributes.type == hipMemoryTypeManaged ? 1 : 0;
+  return ok(error);
+}
+
 int32_t tensor_hip_copy_htod(uint64_t dst, const void* src, uint64_t bytes, uint64_t stream,
                              TensorErrorV1* error) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);

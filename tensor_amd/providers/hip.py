@@ -160,6 +160,55 @@ class Device(Session):
             buffer.release()
             raise
 
+    def from_dlpack(self, source, *, stream: int | None = None) -> Buffer:
+        """Import a DLPack producer (reference: src/tensor/providers/cuda/device.py:278-314 for
+        CUDA).  CPU tensors are copied in; ROCm tensors on this device (kDLROCM, 10) are
+        borrowed without a copy and keep the producer's memory alive until released.  The
+        producer orders its pending writes before ``stream`` (default: this session's)."""
+        from tensor_amd.runtime import dlpack
+
+        self._check()
+        if not hasattr(source, "__dlpack_device__") or not hasattr(source, "__dlpack__"):
+            raise TypeError("DLPack source must implement __dlpack__ and __dlpack_device__")
+        kind, ordinal = source.__dlpack_device__()
+        if kind == dlpack.KDL_CPU:
+            return self.from_numpy(np.from_dlpack(source))
+        if kind != dlpack.KDL_ROCM or ordinal != self.ordinal:
+            raise BufferError(f"DLPack source must be on the CPU or ROCm device {self.ordinal}")
+        owner, address, shape, dtype = dlpack.borrow(source, stream=self.stream if stream is None else int(stream),
+                                                     device_type=dlpack.KDL_ROCM, ordinal=self.ordinal)
+        try:
+            owning, device_memory = c.c_int32(), c.c_int32()
+            try:
+                _native.call("tensor_hip_pointer_device", address, c.byref(owning), c.byref(device_memory))
+            except HipError as exc:
+                raise BufferError(f"DLPack pointer is unknown to this HIP runtime ({exc}); a second HIP "
+                                  "runtime in the process would explain it") from None
+            if not device_memory.value or owning.value != self.ordinal:
+                raise BufferError(f"DLPack pointer is not device memory of ROCm device {self.ordinal}")
+            buffer = Buffer(self, address, shape, dtype, owner=owner)
+            self._buffers.add(buffer)
+            return buffer
+        except BaseException:
+            owner.release()
+            raise
+
+    def _export_dlpack(self, buffer: Buffer, *, stream=None, max_version=None, dl_device=None, copy=None):
+        """Buffer.__dlpack__: a kDLROCM capsule of the buffer, after this session's queued work
+        has been ordered before the consumer's ``stream`` (None: the null stream, -1: no ordering)."""
+        from tensor_amd.runtime import dlpack
+
+        buffer._check()
+        if copy:
+            raise BufferError("DLPack export shares the buffer; copy=True is not supported")
+        if dl_device is not None and tuple(dl_device) != (DEVICE_ROCM, self.ordinal):
+            raise BufferError("DLPack export is only to this ROCm device")
+        consumer = 0 if stream is None else int(stream)
+        if consumer != -1:
+            self.handoff(consumer)
+        versioned = max_version is not None and int(max_version[0]) >= 1
+        return dlpack.export(buffer, device_type=DEVICE_ROCM, versioned=versioned)
+
     def upload(self, buffer: Buffer, array) -> Buffer:
         """Overwrite a buffer's contents from host memory (synchronous)."""
         buffer._check()

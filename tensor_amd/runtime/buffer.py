@@ -125,7 +125,10 @@ class Buffer:
         return self.device.device_type, self.device.ordinal
 
     def __dlpack__(self, *, stream=None, max_version=None, dl_device=None, copy=None):
-        raise BufferError("DLPack export is not provided by this provider")
+        export = getattr(self.device, "_export_dlpack", None)
+        if export is None:
+            raise BufferError("DLPack export is not provided by this provider")
+        return export(self, stream=stream, max_version=max_version, dl_device=dl_device, copy=copy)
 
 
 class BufferView(Buffer):

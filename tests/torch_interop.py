@@ -1,0 +1,220 @@
+"""PyTorch-ROCm interop checks, run as its own process by test_gpu_torch.py.
+
+torch is imported before anything loads libtensor_hip.so, so the library binds
+to the HIP runtime that torch's wheel carries and the two share streams and
+pointers.  Each check prints its name before it touches the GPU.
+"""
+
+from __future__ import annotations
+
+import gc
+import sys
+import time
+from pathlib import Path
+
+import torch  # first: the process's HIP runtime is torch's
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+import numpy as np  # noqa: E402
+
+import tensor_amd.torch as tt  # noqa: E402
+from oracle import gguf_ref as R  # noqa: E402
+from tensor_amd.gguf import quant as Q  # noqa: E402
+from tensor_amd.runtime.errors import TensorRuntimeError  # noqa: E402
+from tensor_amd.torch import session as S  # noqa: E402
+from tests import gguf_cases as cases  # noqa: E402
+
+TOLERANCE = 2e-3  # relative L2 against the oracle
+
+
+def step(name):
+    print("[torch-interop]", name, flush=True)
+
+
+def check_linear(oracle, encoding, m, n, k, out_dtype, seed=60):
+    step(f"linear {encoding} M={m} N={n} K={k} {out_dtype}")
+    code = Q.ggml_type(encoding)
+    raw, x = cases.weight(n, k, encoding, seed), cases.activation(m, k, seed + 1)
+    kernel = tt.load("gguf_linear", encoding=encoding, out_dtype=out_dtype)
+    xt, wt = torch.from_numpy(x).cuda(), torch.from_numpy(raw).cuda()
+    out = kernel(xt, wt)
+    assert out.shape == (m, n) and out.dtype == getattr(torch, out_dtype) and out.device == xt.device
+    expect(oracle, out, x, raw, code, n, k)
+    # same shapes, new storage: the cached descriptors are rebound to the new pointers
+    x2 = (x * np.float16(-1.5)).astype(np.float16)
+    out2 = kernel(torch.from_numpy(x2).cuda(), wt.clone())
+    expect(oracle, out2, x2, raw, code, n, k)
+    assert len(kernel._prepared) == 1
+    return kernel, xt, wt, out
+
+
+def expect(oracle, got, x, raw, code, n, k):
+    expected = oracle.linear(x, raw, code, n, k, prefill=x.shape[0] > 8)
+    error = R.relative_l2(got.float().cpu().numpy(), expected)
+    assert error <= TOLERANCE, error
+
+
+def check_stream_order(kernel, xt, wt, reference):
+    """Inputs written on a side stream just before the call: the launch must follow them there."""
+    step("launch on a non-default torch stream")
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        x = torch.empty_like(xt)
+        x.copy_(xt)
+        w = wt.clone()
+        out = kernel(x, w)
+        got = out.cpu()  # ordered after the kernel on the same stream
+    assert torch.equal(got, reference.cpu())
+    torch.cuda.synchronize()
+
+
+def check_raw_into_prepare(kernel, xt, wt, reference):
+    step("raw, into and prepare")
+    assert torch.equal(kernel.raw(xt, wt).cpu(), reference.cpu())
+    out = torch.full_like(reference, float("nan"))
+    kernel.into(xt, wt, outputs=[out])
+    assert torch.equal(out.cpu(), reference.cpu())
+    x = xt.clone()
+    prepared = kernel.prepare(x, wt)
+    prepared()
+    assert torch.equal(prepared.outputs[0].cpu(), reference.cpu())
+    x.mul_(-1)  # in-place data changes are seen by the next submission
+    prepared()
+    negated = kernel.raw(x, wt)
+    got = prepared.outputs[0]
+    step(f"  negated input: max |prepared + reference| = {(got.float() + reference.float()).abs().max().item():.3g}")
+    assert torch.equal(got.cpu(), negated.cpu())
+    assert torch.linalg.norm(got.float() + reference.float()) <= TOLERANCE * torch.linalg.norm(reference.float())
+    kernel(xt.clone(), wt)  # a launch through the cache leaves the prepared call's pointers alone
+    prepared()
+    assert torch.equal(prepared.outputs[0].cpu(), negated.cpu())
+    x.set_(x.clone())
+    try:
+        prepared()
+    except ValueError:
+        pass
+    else:
+        raise AssertionError("a prepared call ran on changed storage")
+    for bad in (xt.cpu(), xt[:, ::2]):
+        try:
+            kernel(bad, wt)
+        except (TypeError, ValueError):
+            pass
+        else:
+            raise AssertionError("a CPU or strided input was accepted")
+    try:
+        kernel.into(xt, wt, outputs=[torch.empty(reference.shape, dtype=torch.float32, device=xt.device)])
+    except (ValueError, RuntimeError):
+        pass
+    else:
+        raise AssertionError("an output of the wrong dtype was accepted")
+
+
+def check_compile(oracle):
+    step("torch.compile (aot_eager, dynamic shapes) over the registered operator")
+    n, k = 512, 2048
+    raw = cases.weight(n, k, "q4_k", 70)
+    kernel = tt.load("gguf_linear", encoding="q4_k", out_dtype="float32")
+    wt = torch.from_numpy(raw).cuda()
+
+    def layer(x, w):
+        return kernel(x, w) * 2.0 + 1.0
+
+    compiled = torch.compile(layer, backend="aot_eager", dynamic=True, fullgraph=True)
+    for m in (3, 5, 40):
+        x = cases.activation(m, k, 71 + m)
+        got = compiled(torch.from_numpy(x).cuda(), wt)
+        expected = oracle.linear(x, raw, Q.Q4_K, n, k, prefill=m > 8) * 2.0 + 1.0
+        error = R.relative_l2(got.cpu().numpy(), expected)
+        assert error <= TOLERANCE, (m, error)
+
+
+def check_bundle():
+    step("hip bundle (derived scalar arguments) through torch")
+    kernel = tt.load(str(ROOT / "tensor_amd" / "kernels" / "swiglu.tbin"))
+    gate = torch.randn(7, 3001, dtype=torch.float16, device="cuda")
+    up = torch.randn(7, 3001, dtype=torch.float16, device="cuda")
+    out = kernel(gate, up)
+    want = torch.nn.functional.silu(gate.float()) * up.float()
+    assert torch.allclose(out.float(), want, rtol=2e-3, atol=2e-3)
+
+
+def check_overhead(kernel, xt, wt):
+    step("host cost per call (not asserted)")
+    prepared = kernel.prepare(xt, wt)
+    for name, run in (("operator", lambda: kernel(xt, wt)), ("raw", lambda: kernel.raw(xt, wt)),
+                      ("prepared", prepared)):
+        for _ in range(20):
+            run()
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(500):
+            run()
+        torch.cuda.synchronize()
+        step(f"  {name}: {(time.perf_counter() - start) / 500 * 1e6:.1f} us per call")
+
+
+def check_import(session):
+    step("Device.from_dlpack on a torch tensor: zero copy, producer held until release")
+    source = torch.arange(1, 4097, dtype=torch.float32, device="cuda").reshape(64, 64)
+    buffer = session.from_dlpack(source)
+    assert buffer.pointer == source.data_ptr() and buffer.shape == (64, 64)
+    source.mul_(3)
+    assert np.array_equal(buffer.to_numpy(), source.cpu().numpy())
+    buffer.release()
+    step("Device.from_dlpack on a CPU tensor copies")
+    host = torch.arange(10, dtype=torch.int32)
+    copied = session.from_dlpack(host)
+    assert np.array_equal(copied.to_numpy(), host.numpy())
+    copied.release()
+
+
+def check_export(session):
+    step("torch.from_dlpack on a tensor_amd buffer: shared memory, release waits for torch")
+    host = (np.arange(4096) % 1024).astype(np.float16).reshape(16, 256)  # x + 1 stays exact in fp16
+    buffer = session.from_numpy(host)
+    view = torch.from_dlpack(buffer)
+    assert view.data_ptr() == buffer.pointer and view.shape == (16, 256) and view.dtype == torch.float16
+    assert view.device.type == "cuda"
+    view.add_(1)
+    torch.cuda.synchronize()
+    assert np.array_equal(buffer.to_numpy(), host + np.float16(1))
+    try:
+        buffer.release()
+    except TensorRuntimeError:
+        pass
+    else:
+        raise AssertionError("a buffer torch still views was released")
+    del view
+    gc.collect()
+    buffer.release()
+
+
+def main():
+    assert torch.cuda.is_available()
+    step(f"torch {torch.__version__} hip {torch.version.hip}")
+    oracle = R.c_oracle()
+    oracle.set_threads(16)
+    kernel, xt, wt, out = check_linear(oracle, "q4_k", 1, 4096, 4096, "float16")
+    assert len(tt.hip_runtimes()) == 1, tt.hip_runtimes()
+    check_stream_order(kernel, xt, wt, out)
+    check_raw_into_prepare(kernel, xt, wt, out)
+    check_linear(oracle, "q4_k", 64, 1024, 4096, "float16")
+    check_linear(oracle, "q6_k", 3, 1000, 2560, "float32")
+    check_compile(oracle)
+    check_bundle()
+    session = S.session(torch.cuda.current_device())
+    check_import(session)
+    check_export(session)
+    check_overhead(kernel, xt, wt)
+    step("close, then launch again in a new session")
+    tt.close()
+    assert torch.equal(kernel(xt, wt).cpu(), out.cpu())
+    tt.close()
+    step("ok")
+
+
+if __name__ == "__main__":
+    main()

@@ -87,6 +87,51 @@ def build_bundles(verbose: bool = False) -> list:
     return built
 
 
+EXECUTOR = PACKAGE / "torch" / "executor.cpp"
+
+
+def executor_module() -> str:
+    """Module name of the native executor for the installed torch (its major/minor)."""
+    import torch
+
+    major, minor = torch.__version__.split("+")[0].split(".")[:2]
+    return f"_executor_{major}_{minor}"
+
+
+def build_executor(verbose: bool = False) -> Path | None:
+    """Compile tensor_amd.torch's native executor against the installed PyTorch-ROCm
+    (host C++ only, g++; it calls the provider's C ABI).  Skipped without torch."""
+    try:
+        import torch
+        from torch.utils import cpp_extension
+    except ImportError:
+        return None
+    if torch.version.hip is None:
+        return None
+    import sysconfig
+
+    name = executor_module()
+    target = EXECUTOR.parent / f"{name}.so"
+    tmp = target.with_suffix(".so.tmp")
+    torch_lib = Path(torch.__file__).parent / "lib"
+    cmd = [
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden",
+        f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+        f"-DTENSOR_EXECUTOR_MODULE={name}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        *(f"-I{path}" for path in cpp_extension.include_paths()),
+        f"-I{sysconfig.get_paths()['include']}", f"-I{ROOT / 'include'}", "-I/opt/rocm/include",
+        str(EXECUTOR), f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_python",
+        f"-Wl,-rpath,{torch_lib}", "-o", str(tmp),
+    ]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode:
+        raise RuntimeError(f"executor build failed:\n{result.stdout}\n{result.stderr}")
+    if verbose and result.stderr.strip():
+        print(result.stderr, file=sys.stderr)
+    os.replace(tmp, target)
+    return target
+
+
 def build(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))

@@ -28,7 +28,7 @@ from pathlib import Path
 import torch
 
 from tensor_amd.runtime.signature import buffer_argument
-from tensor_amd.torch.launch import Prepared, _slots, launch
+from tensor_amd.torch.launch import Prepared, _slots, launch, native_plan
 from tensor_amd.torch.signatures import metadata
 
 _operator_ids = count()
@@ -77,6 +77,9 @@ class Kernel:
         self._slots = _slots(self.manifest)
         self._executables: dict = {}
         self._prepared: OrderedDict = OrderedDict()
+        # Rebinding native plans by input metadata, for kernels whose inputs are all tensors
+        # (scalar values are not part of a plan's key).
+        self._plans: dict | None = {} if all(buffer_argument(d) for d in self.inputs) else None
         self._lock = threading.RLock()
         self._op = None
         self._into_op = None
@@ -89,6 +92,8 @@ class Kernel:
         if executable is None or not executable.device._open or executable.device is not device:
             executable = self._executables[ordinal] = device.load(self._loadable)
             self._prepared.clear()
+            if self._plans is not None:
+                self._plans.clear()
         return executable
 
     def metadata(self, args, *, symbolic=False):
@@ -101,11 +106,32 @@ class Kernel:
     def _launch(self, args, outputs, **options):
         return launch(self, args, outputs, **options)
 
-    def raw(self, *args):
-        """Allocate the outputs and launch, bypassing the registered operator."""
+    def _run(self, args):
+        """Allocate the outputs and launch; a list of outputs.  Inputs whose metadata a
+        native plan recorded go straight to it; others take the validated path, which
+        records a plan for the next call."""
+        plans = self._plans
+        if plans is not None and args:
+            key = tuple((t.shape, t.dtype, t.device) if isinstance(t, torch.Tensor) else None for t in args)
+            entry = plans.get(key)
+            if entry is not None and entry[1].device._open:
+                result = entry[0](*args)
+                if result is not None:
+                    return [result] if len(self.outputs) == 1 else list(result)
         contract = self.metadata(args)
         outputs = [torch.empty(shape, dtype=dtype, device=contract[1]) for shape, dtype in contract[0]]
-        self._launch(args, outputs, contract=contract, trusted_outputs=True)
+        executable, call, _, _ = self._launch(args, outputs, contract=contract, trusted_outputs=True)
+        if plans is not None:
+            plan = native_plan(self, executable, call, args, outputs, fixed=False)
+            if plan is not None:
+                if len(plans) >= 64:
+                    plans.pop(next(iter(plans)))
+                plans[key] = (plan, executable)
+        return outputs
+
+    def raw(self, *args):
+        """Allocate the outputs and launch, bypassing the registered operator."""
+        outputs = self._run(args)
         return outputs[0] if len(outputs) == 1 else tuple(outputs)
 
     def prepare(self, *args, outputs=None):
@@ -115,7 +141,7 @@ class Kernel:
             contract = self.metadata(args)
             outputs = [torch.empty(shape, dtype=dtype, device=contract[1]) for shape, dtype in contract[0]]
         state = self._launch(args, list(outputs), enqueue=False)
-        return Prepared(state, args, tuple(outputs))
+        return Prepared(self, state, args, tuple(outputs))
 
     def register(self):
         return register(self)
@@ -150,11 +176,7 @@ def register(kernel):
     @torch.library.custom_op("tensor_amd::" + name, mutates_args=(),
                              schema="(Tensor[] tensors, Scalar[] scalars) -> Tensor[]")
     def op(tensors, scalars):
-        args = unpack(tensors, scalars)
-        contract = kernel.metadata(args)
-        outputs = [torch.empty(shape, dtype=dtype, device=contract[1]) for shape, dtype in contract[0]]
-        kernel._launch(args, outputs, contract=contract, trusted_outputs=True)
-        return outputs
+        return kernel._run(unpack(tensors, scalars))
 
     @op.register_fake
     def _(tensors, scalars):

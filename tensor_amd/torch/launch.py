@@ -16,6 +16,8 @@ native call, which is what the reference's submission shim
 from __future__ import annotations
 
 import ctypes as c
+import importlib
+import os
 import threading
 from contextlib import nullcontext
 
@@ -26,6 +28,22 @@ from tensor_amd.runtime.signature import SCALAR_TYPES, buffer_argument, scalar_v
 from tensor_amd.torch.session import current_stream, session
 
 PREPARED_CACHE = 64
+
+# The C++ executor (executor.cpp) is built against torch's non-stable ABI: only a module
+# built for this torch's major/minor version is imported.  TENSOR_AMD_TORCH_NATIVE=0
+# keeps every launch on the Python path.
+_executor = None
+if os.environ.get("TENSOR_AMD_TORCH_NATIVE", "1") != "0":
+    _major, _minor = torch.__version__.split("+")[0].split(".")[:2]
+    try:
+        _executor = importlib.import_module(f"tensor_amd.torch._executor_{_major}_{_minor}")
+    except ImportError:
+        pass
+
+
+def native_executor():
+    """The native executor module in use, or None."""
+    return _executor
 
 
 class _Call:
@@ -51,6 +69,27 @@ def _slots(manifest):
     alignments = {d["name"]: d.get("alignment", 256) for d in manifest["arguments"] if buffer_argument(d)}
     return [(index, d, alignments.get(d["name"], 1))
             for index, d in enumerate(manifest.get("abi", manifest["arguments"]))]
+
+
+def native_plan(kernel, executable, call, args, outputs, *, fixed):
+    """A native executor Plan over ``call``'s descriptors, or None without the executor.
+    ``args`` are the kernel's inputs in order; tensors are bound by position."""
+    if _executor is None:
+        return None
+    from tensor_amd import _native
+
+    tensors = [v for d, v in zip(kernel.inputs, args) if buffer_argument(d)]
+    positions = {d["name"]: i for i, d in enumerate(d for d in kernel.inputs if buffer_argument(d))}
+    positions.update((d["name"], len(tensors) + i) for i, d in enumerate(kernel.outputs))
+    bindings = [(index, positions[d["name"]], alignment) for index, d, alignment in kernel._slots
+                if buffer_argument(d)]
+    if executable.manifest.get("kind") == "hsaco":
+        entry = c.cast(_native.library().tensor_hip_module_launch_v1, c.c_void_p).value
+        function = executable.function
+    else:
+        entry, function = c.cast(executable.function, c.c_void_p).value, 0
+    return _executor.Plan(executable.manifest["entrypoint"], entry, function, c.addressof(call.descriptor),
+                          tuple(tensors), tuple(outputs), bindings, fixed)
 
 
 def _bind(device, executable, manifest, values, stream):
@@ -148,7 +187,7 @@ class Prepared:
     shape, strides, dtype or device is refused.
     """
 
-    def __init__(self, state, args, outputs):
+    def __init__(self, kernel, state, args, outputs):
         self.executable, call, self.tensors, stream = state
         self.call = call.copy()  # later launches of the kernel rewrite the cached descriptors
         self.args, self.outputs = args, outputs
@@ -157,10 +196,14 @@ class Prepared:
         self.metadata = [(tuple(t.shape), tuple(t.stride()), t.dtype, t.device, t.data_ptr()) for t in self.tensors]
         self.streams = {stream.cuda_stream: stream}
         self.lock = threading.RLock()
+        self._native = native_plan(kernel, self.executable, self.call, args, outputs, fixed=True)
 
     def __call__(self):
         if not self.device._open or self.executable._released:
             raise RuntimeError("prepared call belongs to a closed session")
+        if self._native is not None:
+            self._native()
+            return
         for tensor, (shape, stride, dtype, device, pointer) in zip(self.tensors, self.metadata):
             if (tensor.data_ptr() != pointer or tuple(tensor.shape) != shape or tuple(tensor.stride()) != stride
                     or tensor.dtype != dtype or tensor.device != device):

@@ -8,6 +8,7 @@ pointers.  Each check prints its name before it touches the GPU.
 from __future__ import annotations
 
 import gc
+import os
 import sys
 import time
 from pathlib import Path
@@ -23,6 +24,7 @@ import tensor_amd.torch as tt  # noqa: E402
 from oracle import gguf_ref as R  # noqa: E402
 from tensor_amd.gguf import quant as Q  # noqa: E402
 from tensor_amd.runtime.errors import TensorRuntimeError  # noqa: E402
+from tensor_amd.torch import launch as L  # noqa: E402
 from tensor_amd.torch import session as S  # noqa: E402
 from tests import gguf_cases as cases  # noqa: E402
 
@@ -47,6 +49,7 @@ def check_linear(oracle, encoding, m, n, k, out_dtype, seed=60):
     out2 = kernel(torch.from_numpy(x2).cuda(), wt.clone())
     expect(oracle, out2, x2, raw, code, n, k)
     assert len(kernel._prepared) == 1
+    assert len(kernel._plans) == (1 if L.native_executor() else 0)  # the second call ran the plan
     return kernel, xt, wt, out
 
 
@@ -195,6 +198,9 @@ def check_export(session):
 def main():
     assert torch.cuda.is_available()
     step(f"torch {torch.__version__} hip {torch.version.hip}")
+    executor = L.native_executor()
+    step(f"native executor: {executor.__name__ if executor else None}")
+    assert (executor is not None) == (os.environ.get("TENSOR_AMD_TORCH_NATIVE", "1") != "0")
     oracle = R.c_oracle()
     oracle.set_threads(16)
     kernel, xt, wt, out = check_linear(oracle, "q4_k", 1, 4096, 4096, "float16")

@@ -385,3 +385,23 @@ def test_gemm_zero_input_gives_exact_zero(hip_device):
     x = np.zeros((64, 512), np.float16)
     got = run_linear(hip_device, "gguf_gemm", "q4_k", x, raw, "float32")
     assert np.array_equal(got, np.zeros_like(got))
+
+
+@pytest.mark.parametrize("encoding", ENCODINGS)
+def test_linear_on_weights_read_from_a_gguf_file(hip_device, c_oracle, encoding, tmp_path):
+    """Raw rows ingested from a GGUF file (a read-only memory map) feed the kernels as is."""
+    from tensor_amd.gguf import file as G
+
+    code = Q.ggml_type(encoding)
+    n, k = 300, 2048
+    note("gguf-file", encoding, n, k)
+    raw = cases.weight(n, k, encoding, 95)
+    path = G.write(tmp_path / "model.gguf", {"blk.0.ffn_up.weight": (code, (k, n), raw)},
+                   {"general.architecture": "qwen3"})
+    x = cases.activation(3, k, 96)
+    expected = c_oracle.linear(x, raw, code, n, k)
+    with G.read(path) as gguf:
+        rows = gguf.raw("blk.0.ffn_up.weight")
+        got = run_linear(hip_device, "gguf_linear", encoding, x, rows, "float32")
+        del rows
+    assert R.relative_l2(got, expected) <= TOLERANCE

@@ -34,10 +34,19 @@
 extern "C" {
 #endif
 
-/* GGML block type ids accepted by the GGUF entry points. */
+/* GGML block type ids accepted by the GGUF entry points.  Q4_0, Q8_0, Q4_K and Q6_K are
+ * the showcase's encodings (benchmarks/kernels/showcase/benchmark.py:122-126 and
+ * research/plans/v1-benchmarks.md:297-301); Q4_1, Q5_0, Q5_1, Q2_K, Q3_K and Q5_K are the
+ * plan's other basic and K formats (v1-benchmarks.md:297-300), public GGML layouts. */
 #define TENSOR_GGML_Q4_0 2u
+#define TENSOR_GGML_Q4_1 3u
+#define TENSOR_GGML_Q5_0 6u
+#define TENSOR_GGML_Q5_1 7u
 #define TENSOR_GGML_Q8_0 8u
+#define TENSOR_GGML_Q2_K 10u
+#define TENSOR_GGML_Q3_K 11u
 #define TENSOR_GGML_Q4_K 12u
+#define TENSOR_GGML_Q5_K 13u
 #define TENSOR_GGML_Q6_K 14u
 
 /* Largest activation row count of the decode GEMV entry. */

@@ -6,7 +6,8 @@
  * Scalar C restatement of the reference's GGUF block decoding and of the
  * quantized-linear numerics it is checked against.
  *
- *   Block formats (GGML types 2, 8, 12, 14):
+ *   Block formats (GGML types 2, 8, 12, 14; types 3, 6, 7, 10, 11 and 13 below
+ *   decode_q4_1 follow the public GGML block definitions, with no reference code):
  *     Q4_0  benchmarks/kernels/showcase/triton_kernels.py:135-142
  *     Q4_K  benchmarks/kernels/showcase/triton_kernels.py:143-162
  *     Q6_K  benchmarks/kernels/showcase/triton_kernels.py:163-180
@@ -45,8 +46,14 @@
 #include "tensor/abi.h"
 
 #define GGML_Q4_0 2
+#define GGML_Q4_1 3
+#define GGML_Q5_0 6
+#define GGML_Q5_1 7
 #define GGML_Q8_0 8
+#define GGML_Q2_K 10
+#define GGML_Q3_K 11
 #define GGML_Q4_K 12
+#define GGML_Q5_K 13
 #define GGML_Q6_K 14
 
 /* ---------------------------------------------------------------- fp16 --- */
@@ -115,8 +122,14 @@ static float load_half(const uint8_t *p) {
 int oracle_block_geometry(int type, int *elements, int *bytes) {
   switch (type) {
     case GGML_Q4_0: *elements = 32; *bytes = 18; return 0;
+    case GGML_Q4_1: *elements = 32; *bytes = 20; return 0;
+    case GGML_Q5_0: *elements = 32; *bytes = 22; return 0;
+    case GGML_Q5_1: *elements = 32; *bytes = 24; return 0;
     case GGML_Q8_0: *elements = 32; *bytes = 34; return 0;
+    case GGML_Q2_K: *elements = 256; *bytes = 84; return 0;
+    case GGML_Q3_K: *elements = 256; *bytes = 110; return 0;
     case GGML_Q4_K: *elements = 256; *bytes = 144; return 0;
+    case GGML_Q5_K: *elements = 256; *bytes = 176; return 0;
     case GGML_Q6_K: *elements = 256; *bytes = 210; return 0;
     default: return -1;
   }
@@ -193,11 +206,119 @@ static void decode_q6_k(const uint8_t *block, float *out) {
   }
 }
 
+/* ---- the other GGML encodings (public GGML block definitions; no reference code) ----
+ *   Q4_1  fp16 d | fp16 m | 16 B nibbles                    y = q*d + m
+ *   Q5_0  fp16 d | u32 qh | 16 B nibbles                    y = (q - 16)*d, q = nibble | qh bit << 4
+ *   Q5_1  fp16 d | fp16 m | u32 qh | 16 B nibbles           y = q*d + m
+ *   Q2_K  16 B scales (lo: scale, hi: min) | 64 B 2-bit codes | fp16 d | fp16 dmin
+ *                                                           y = d*sc*q - dmin*m
+ *   Q3_K  32 B high-bit mask | 64 B 2-bit codes | 12 B 6-bit scales | fp16 d
+ *                                                           y = d*(sc - 32)*(q - (hbit ? 0 : 4))
+ *   Q5_K  fp16 d | fp16 dmin | 12 B 6-bit scales/mins (as Q4_K) | 32 B high bits | 128 B nibbles
+ *                                                           y = d*sc*q - dmin*m
+ * Every product is exact in fp32; Q4_1, Q5_1, Q2_K and Q5_K round once, in the final
+ * addition or subtraction. */
+
+static uint32_t load_u32(const uint8_t *p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+static void decode_q4_1(const uint8_t *block, float *out) {
+  float d = load_half(block), m = load_half(block + 2);
+  const uint8_t *qs = block + 4;
+  for (int j = 0; j < 16; ++j) {
+    out[j] = (float)(qs[j] & 15u) * d + m;
+    out[j + 16] = (float)(qs[j] >> 4) * d + m;
+  }
+}
+
+static void decode_q5(const uint8_t *block, float *out, int with_min) {
+  float d = load_half(block);
+  float m = with_min ? load_half(block + 2) : 0.0f;
+  const uint8_t *tail = block + (with_min ? 4 : 2);
+  uint32_t qh = load_u32(tail);
+  const uint8_t *qs = tail + 4;
+  for (int j = 0; j < 16; ++j) {
+    int lo = (int)((qs[j] & 15u) | (((qh >> j) & 1u) << 4));
+    int hi = (int)((qs[j] >> 4) | (((qh >> (j + 16)) & 1u) << 4));
+    if (with_min) {
+      out[j] = (float)lo * d + m;
+      out[j + 16] = (float)hi * d + m;
+    } else {
+      out[j] = (float)(lo - 16) * d;
+      out[j + 16] = (float)(hi - 16) * d;
+    }
+  }
+}
+
+static void decode_q2_k(const uint8_t *block, float *out) {
+  const uint8_t *scales = block, *qs = block + 16;
+  float d = load_half(block + 80), dmin = load_half(block + 82);
+  for (int half = 0; half < 2; ++half) {        /* 128 elements per 32 code bytes */
+    for (int shift = 0; shift < 4; ++shift) {   /* 2-bit planes, 32 elements each */
+      for (int part = 0; part < 2; ++part) {    /* 16 elements per scale byte */
+        int index = 128 * half + 32 * shift + 16 * part;
+        uint8_t sc = scales[index / 16];
+        float dl = d * (float)(sc & 15), ml = dmin * (float)(sc >> 4);
+        for (int l = 0; l < 16; ++l) {
+          int q = (qs[32 * half + 16 * part + l] >> (2 * shift)) & 3;
+          out[index + l] = dl * (float)q - ml;
+        }
+      }
+    }
+  }
+}
+
+/* Q3_K's 16 six-bit scales: low nibbles in bytes 0-7 (scales 0-7 low, 8-15 high nibble),
+ * the top two bits in bytes 8-11 (scale s in byte 8 + s%4, bits 2*(s/4)). */
+static int q3k_scale(const uint8_t *s, int index) {
+  int low = index < 8 ? (s[index] & 15) : (s[index - 8] >> 4);
+  int high = (s[8 + (index & 3)] >> (2 * (index >> 2))) & 3;
+  return (low | (high << 4)) - 32;
+}
+
+static void decode_q3_k(const uint8_t *block, float *out) {
+  const uint8_t *hmask = block, *qs = block + 32, *scales = block + 96;
+  float d = load_half(block + 108);
+  for (int half = 0; half < 2; ++half) {
+    for (int shift = 0; shift < 4; ++shift) {
+      int bit = 4 * half + shift;               /* high-bit plane of these 32 elements */
+      for (int l = 0; l < 32; ++l) {
+        int index = 128 * half + 32 * shift + l;
+        int q = ((qs[32 * half + l] >> (2 * shift)) & 3) - (((hmask[l] >> bit) & 1) ? 0 : 4);
+        out[index] = d * (float)q3k_scale(scales, index / 16) * (float)q;
+      }
+    }
+  }
+}
+
+static void decode_q5_k(const uint8_t *block, float *out) {
+  float d = load_half(block), dmin = load_half(block + 2);
+  const uint8_t *scales = block + 4, *qh = block + 16, *qs = block + 48;
+  for (int group = 0; group < 4; ++group) {
+    for (int half = 0; half < 2; ++half) {
+      int sub = 2 * group + half, scale, min;
+      q4k_scale_min(scales, sub, &scale, &min);
+      float ds = d * (float)scale, dm = dmin * (float)min;
+      for (int l = 0; l < 32; ++l) {
+        int q = ((qs[32 * group + l] >> (4 * half)) & 15) | (((qh[l] >> sub) & 1) << 4);
+        out[64 * group + 32 * half + l] = ds * (float)q - dm;
+      }
+    }
+  }
+}
+
 int oracle_decode_block(int type, const uint8_t *block, float *out) {
   switch (type) {
     case GGML_Q4_0: decode_q4_0(block, out); return 0;
+    case GGML_Q4_1: decode_q4_1(block, out); return 0;
+    case GGML_Q5_0: decode_q5(block, out, 0); return 0;
+    case GGML_Q5_1: decode_q5(block, out, 1); return 0;
     case GGML_Q8_0: decode_q8_0(block, out); return 0;
+    case GGML_Q2_K: decode_q2_k(block, out); return 0;
+    case GGML_Q3_K: decode_q3_k(block, out); return 0;
     case GGML_Q4_K: decode_q4_k(block, out); return 0;
+    case GGML_Q5_K: decode_q5_k(block, out); return 0;
     case GGML_Q6_K: decode_q6_k(block, out); return 0;
     default: return -1;
   }

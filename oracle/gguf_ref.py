@@ -17,7 +17,9 @@ encoders, exhaustive scale/min packing and closed forms.
 
 Q8_0 does not appear in the reference's code (``research/plans/v1-benchmarks.md:301``
 names it); it follows the public GGML definition: fp16 ``d`` then 32 int8,
-``y = d * q``.
+``y = d * q``.  Q4_1, Q5_0, Q5_1, Q2_K, Q3_K and Q5_K (the plan's "other K-quants
+and basic formats", ``research/plans/v1-benchmarks.md:297-300``) likewise follow the
+public GGML block definitions; the C decoders list their layouts.
 
 Product conventions: ``out[m, n] = sum_k x[m, k] * W[n, k]``
 (``triton_kernels.py:199-211``).  Decode numerics use fp32 operands
@@ -38,8 +40,12 @@ HERE = Path(__file__).resolve().parent
 LIBRARY = HERE / "liboracle.so"
 
 Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+# The other GGML encodings: public GGML block definitions, no reference code.
+Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K = 3, 6, 7, 10, 11, 13
 # GGML type id -> (elements per block, bytes per block)
-GEOMETRY = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+GEOMETRY = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210),
+            Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q2_K: (256, 84), Q3_K: (256, 110),
+            Q5_K: (256, 176)}
 
 
 def _half(raw: np.ndarray, offset: np.ndarray) -> np.ndarray:
@@ -96,6 +102,53 @@ def dequantize(raw: np.ndarray, ggml_type: int, n: int, k: int) -> np.ndarray:
         sc = raw[base + 192 + local // 16].view(np.int8).astype(np.float32)
         d = _half(raw, base + 208)
         return (((val - 32).astype(np.float32) * sc) * d).astype(np.float32)
+    if ggml_type in (Q4_1, Q5_0, Q5_1):  # 32-element blocks: nibble j and j + 16 share byte j
+        d = _half(raw, base)
+        lane = channels % 32
+        tail = base + (2 if ggml_type == Q5_0 else 4)
+        if ggml_type == Q4_1:
+            byte = raw[tail + lane % 16].astype(np.int32)
+            val = (byte >> (lane // 16 * 4)) & 15
+            return (val.astype(np.float32) * d + _half(raw, base + 2)).astype(np.float32)
+        byte = raw[tail + 4 + lane % 16].astype(np.int32)
+        high = (raw[tail + lane // 8].astype(np.int32) >> (lane % 8)) & 1  # bit `lane` of qh
+        val = ((byte >> (lane // 16 * 4)) & 15) | (high << 4)
+        if ggml_type == Q5_0:
+            return ((val - 16).astype(np.float32) * d).astype(np.float32)
+        return (val.astype(np.float32) * d + _half(raw, base + 2)).astype(np.float32)
+    if ggml_type == Q2_K:
+        local = channels % 256
+        sc = raw[base + local // 16].astype(np.int32)
+        code = (raw[base + 16 + local // 128 * 32 + local % 32].astype(np.int32) >> (local % 128 // 32 * 2)) & 3
+        d, dmin = _half(raw, base + 80), _half(raw, base + 82)
+        main = (d * (sc & 15).astype(np.float32)) * code.astype(np.float32)
+        return (main - dmin * (sc >> 4).astype(np.float32)).astype(np.float32)
+    if ggml_type == Q3_K:
+        local = channels % 256
+        index = local // 16
+        low = np.where(index < 8, raw[base + 96 + index % 8] & 15, raw[base + 96 + index % 8] >> 4).astype(np.int32)
+        high = (raw[base + 104 + index % 4].astype(np.int32) >> (index // 4 * 2)) & 3
+        scale = (low | (high << 4)) - 32
+        code = (raw[base + 32 + local // 128 * 32 + local % 32].astype(np.int32) >> (local % 128 // 32 * 2)) & 3
+        plane = local // 128 * 4 + local % 128 // 32
+        keep = (raw[base + local % 32].astype(np.int32) >> plane) & 1
+        val = code - np.where(keep == 1, 0, 4)
+        d = _half(raw, base + 108)
+        return ((d * scale.astype(np.float32)) * val.astype(np.float32)).astype(np.float32)
+    if ggml_type == Q5_K:
+        local = channels % 256
+        group = local // 32
+        d, dm = _half(raw, base), _half(raw, base + 2)
+        sc0 = raw[base + 4 + group % 4].astype(np.int32)
+        sc1 = raw[base + 8 + group % 4].astype(np.int32)
+        sc2 = raw[base + 12 + group % 4].astype(np.int32)
+        sc = np.where(group < 4, sc0 & 63, (sc2 & 15) | ((sc0 >> 6) << 4))
+        mn = np.where(group < 4, sc1 & 63, (sc2 >> 4) | ((sc1 >> 6) << 4))
+        byte = raw[base + 48 + local // 64 * 32 + local % 32].astype(np.int32)
+        high = (raw[base + 16 + local % 32].astype(np.int32) >> group) & 1
+        val = ((byte >> (local % 64 // 32 * 4)) & 15) | (high << 4)
+        main = (d * sc.astype(np.float32)) * val.astype(np.float32)
+        return (main - dm * mn.astype(np.float32)).astype(np.float32)
     raise ValueError(f"unsupported GGML type {ggml_type}")
 
 

@@ -10,6 +10,18 @@
 // (reference: benchmarks/kernels/showcase/triton_kernels.py:134-181; Q8_0 from
 // the public GGML block definition).  Rows are stored one after another, each
 // row K/QK consecutive blocks.
+//
+// The other GGML encodings the generic kernels decode (public GGML block
+// definitions; the reference has no code for them):
+//   Q4_1 (3):  32,  20  fp16 d | fp16 m | 16 B nibbles    y = q*d + m
+//   Q5_0 (6):  32,  22  fp16 d | u32 qh | 16 B nibbles    y = (q - 16)*d, q = nibble | qh bit << 4
+//   Q5_1 (7):  32,  24  fp16 d | fp16 m | u32 qh | 16 B   y = q*d + m
+//   Q2_K (10): 256, 84  16 B scale|min<<4 | 64 B 2-bit codes | fp16 d | fp16 dmin
+//                                                      y = d*sc*q - dmin*m
+//   Q3_K (11): 256, 110 32 B high-bit mask | 64 B 2-bit codes | 12 B 6-bit scales | fp16 d
+//                                                      y = d*(sc - 32)*(q - (hbit ? 0 : 4))
+//   Q5_K (13): 256, 176 fp16 d | fp16 dmin | 12 B scales/mins (Q4_K's) | 32 B high bits | 128 B nibbles
+//                                                      y = d*sc*q - dmin*m
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -18,13 +30,40 @@
 namespace tensor_gguf {
 
 constexpr int kQ4_0 = 2;
+constexpr int kQ4_1 = 3;
+constexpr int kQ5_0 = 6;
+constexpr int kQ5_1 = 7;
 constexpr int kQ8_0 = 8;
+constexpr int kQ2_K = 10;
+constexpr int kQ3_K = 11;
 constexpr int kQ4_K = 12;
+constexpr int kQ5_K = 13;
 constexpr int kQ6_K = 14;
+
+// Elements (QK) and bytes per block of each encoding.
+template <int TYPE>
+struct Block {
+  static constexpr int QK = (TYPE == kQ2_K || TYPE == kQ3_K || TYPE == kQ4_K || TYPE == kQ5_K || TYPE == kQ6_K)
+                                ? 256 : 32;
+  static constexpr int BYTES = TYPE == kQ4_0 ? 18 : TYPE == kQ4_1 ? 20 : TYPE == kQ5_0 ? 22 : TYPE == kQ5_1 ? 24
+                             : TYPE == kQ8_0 ? 34 : TYPE == kQ2_K ? 84 : TYPE == kQ3_K ? 110
+                             : TYPE == kQ4_K ? 144 : TYPE == kQ5_K ? 176 : 210;
+};
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 values to an fp16 pair, each rounded to nearest even from its fp32 value
+// (one v_cvt_pk_f16_f32).  Dequantization rounds to fp32 and the cast to fp16 rounds
+// again (the reference's order); the register barrier keeps the compiler from fusing a
+// producing fma with the conversion into an fp16-result v_fma_mix, which rounds the
+// exact value once and differs where the fp32 result is an fp16 rounding tie.
+__device__ __forceinline__ uint32_t half2_from_fp32(float a, float b) {
+  asm volatile("" : "+v"(a), "+v"(b));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){a, b}, half2_t));
+}
 
 // fp16 1024.0 in both halves of a dword: OR-ing a byte b into the low mantissa
 // byte of 0x6400 gives the fp16 value 1024 + b exactly (b < 1024).

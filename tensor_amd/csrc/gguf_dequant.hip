@@ -14,8 +14,8 @@ namespace tensor_gguf {
 template <int TYPE, typename OutT>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ w,
                                                       OutT* __restrict__ out, int n, int k) {
-  constexpr int QK = (TYPE == kQ4_K || TYPE == kQ6_K) ? 256 : 32;
-  constexpr int BYTES = TYPE == kQ4_K ? 144 : TYPE == kQ6_K ? 210 : TYPE == kQ8_0 ? 34 : 18;
+  constexpr int QK = Block<TYPE>::QK;
+  constexpr int BYTES = Block<TYPE>::BYTES;
   const size_t groups = (size_t)n * (k / 8);
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups; g += stride) {
@@ -25,9 +25,22 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
     float v[8];
     decode8<TYPE>(block, col % QK, v);
     OutT* dst = out + row * (size_t)k + col;
+    if constexpr (sizeof(OutT) == 2) {
+      // the cast of each fp32 value (never a fused single rounding of the exact value)
+      *reinterpret_cast<uint4*>(dst) = make_uint4(half2_from_fp32(v[0], v[1]), half2_from_fp32(v[2], v[3]),
+                                                  half2_from_fp32(v[4], v[5]), half2_from_fp32(v[6], v[7]));
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dst[i] = (OutT)v[i];
+      for (int i = 0; i < 8; ++i) dst[i] = (OutT)v[i];
+    }
   }
+}
+
+template <int TYPE, typename OutT>
+static hipError_t launch_type(const uint8_t* w, OutT* out, const DequantArgs& a, unsigned blocks,
+                              hipStream_t stream) {
+  hipLaunchKernelGGL((dequant_kernel<TYPE, OutT>), dim3(blocks), dim3(256), 0, stream, w, out, a.n, a.k);
+  return hipGetLastError();
 }
 
 template <typename OutT>
@@ -37,22 +50,18 @@ static hipError_t launch_typed(const DequantArgs& a, hipStream_t stream) {
   const size_t groups = (size_t)a.n * (a.k / 8);
   const unsigned blocks = (unsigned)((groups + 255) / 256 < 65536 ? (groups + 255) / 256 : 65536);
   switch (a.type) {
-    case kQ4_K:
-      hipLaunchKernelGGL((dequant_kernel<kQ4_K, OutT>), dim3(blocks), dim3(256), 0, stream, w, out, a.n, a.k);
-      break;
-    case kQ6_K:
-      hipLaunchKernelGGL((dequant_kernel<kQ6_K, OutT>), dim3(blocks), dim3(256), 0, stream, w, out, a.n, a.k);
-      break;
-    case kQ8_0:
-      hipLaunchKernelGGL((dequant_kernel<kQ8_0, OutT>), dim3(blocks), dim3(256), 0, stream, w, out, a.n, a.k);
-      break;
-    case kQ4_0:
-      hipLaunchKernelGGL((dequant_kernel<kQ4_0, OutT>), dim3(blocks), dim3(256), 0, stream, w, out, a.n, a.k);
-      break;
-    default:
-      return hipErrorInvalidValue;
+    case kQ4_K: return launch_type<kQ4_K>(w, out, a, blocks, stream);
+    case kQ6_K: return launch_type<kQ6_K>(w, out, a, blocks, stream);
+    case kQ8_0: return launch_type<kQ8_0>(w, out, a, blocks, stream);
+    case kQ4_0: return launch_type<kQ4_0>(w, out, a, blocks, stream);
+    case kQ4_1: return launch_type<kQ4_1>(w, out, a, blocks, stream);
+    case kQ5_0: return launch_type<kQ5_0>(w, out, a, blocks, stream);
+    case kQ5_1: return launch_type<kQ5_1>(w, out, a, blocks, stream);
+    case kQ2_K: return launch_type<kQ2_K>(w, out, a, blocks, stream);
+    case kQ3_K: return launch_type<kQ3_K>(w, out, a, blocks, stream);
+    case kQ5_K: return launch_type<kQ5_K>(w, out, a, blocks, stream);
+    default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 hipError_t launch_dequant(const DequantArgs& a, hipStream_t stream) {

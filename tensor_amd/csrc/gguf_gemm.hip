@@ -32,8 +32,7 @@ constexpr int LDS_ROW = BK + PAD;
 }  // namespace gemm
 
 __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
-  const _Float16 ha = (_Float16)a, hb = (_Float16)b;
-  return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+  return half2_from_fp32(a, b);
 }
 
 // Exact Q4_K dequantization of four codes held in the bytes of one dword
@@ -56,8 +55,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_v2(const _Float16* __restri
   constexpr int NT = BN / WN / 16;             // 16-column MFMA tiles per wave
   static_assert(BM / WM == 64, "each wave covers 64 rows of M");
   static_assert(NT * 16 * WN == BN, "BN must split into 16-column tiles per wave");
-  constexpr int QK = (TYPE == kQ4_K || TYPE == kQ6_K) ? 256 : 32;
-  constexpr int BYTES = TYPE == kQ4_K ? 144 : TYPE == kQ6_K ? 210 : TYPE == kQ8_0 ? 34 : 18;
+  constexpr int QK = Block<TYPE>::QK;
+  constexpr int BYTES = Block<TYPE>::BYTES;
   // activation tile: BM rows x BK halves = BM * 8 chunks of 16 bytes
   constexpr int X_LOADS = BM * 8 / THREADS;
   static_assert(X_LOADS * THREADS == BM * 8, "activation tile must split evenly");
@@ -218,6 +217,12 @@ static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream) {
     case kQ6_K: return launch_type<kQ6_K, OutT>(a, stream);
     case kQ8_0: return launch_type<kQ8_0, OutT>(a, stream);
     case kQ4_0: return launch_type<kQ4_0, OutT>(a, stream);
+    case kQ4_1: return launch_type<kQ4_1, OutT>(a, stream);
+    case kQ5_0: return launch_type<kQ5_0, OutT>(a, stream);
+    case kQ5_1: return launch_type<kQ5_1, OutT>(a, stream);
+    case kQ2_K: return launch_type<kQ2_K, OutT>(a, stream);
+    case kQ3_K: return launch_type<kQ3_K, OutT>(a, stream);
+    case kQ5_K: return launch_type<kQ5_K, OutT>(a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -41,17 +41,13 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 // fp16(scale * q + bias) for four codes q < 1024 given as fp16 subnormal pairs
 // p02 = (q0, q2) * 2^-24 and p13 = (q1, q3) * 2^-24 (a code masked into the low
 // bits of a half is that subnormal exactly). With scale24 = scale * 2^24 each
-// product is exactly scale * q, the fma rounds once to fp32 as fmaf(scale, q,
-// bias) does, and the result rounds to fp16: one v_fma_mix per element, the
-// pairs packed by the lo/hi forms of the instruction.
+// product is exactly scale * q and the fma rounds once to fp32 as fmaf(scale, q,
+// bias) does (one fp32-result v_fma_mix per element); each pair is then rounded to
+// fp16 by one packed conversion, so the fp16 weight is the cast of the fp32 value.
 __device__ __forceinline__ uint2 affine4(uint32_t p02, uint32_t p13, float scale24, float bias) {
   const half2_t a = as_half2(p02), b = as_half2(p13);
-  half2_t e01, e23;
-  e01[0] = (_Float16)fmaf((float)a[0], scale24, bias);
-  e01[1] = (_Float16)fmaf((float)b[0], scale24, bias);
-  e23[0] = (_Float16)fmaf((float)a[1], scale24, bias);
-  e23[1] = (_Float16)fmaf((float)b[1], scale24, bias);
-  return make_uint2(__builtin_bit_cast(uint32_t, e01), __builtin_bit_cast(uint32_t, e23));
+  return make_uint2(half2_from_fp32(fmaf((float)a[0], scale24, bias), fmaf((float)b[0], scale24, bias)),
+                    half2_from_fp32(fmaf((float)a[1], scale24, bias), fmaf((float)b[1], scale24, bias)));
 }
 
 template <int TYPE, int TPR>

@@ -17,6 +17,7 @@
 //    a lane is loaded once per step and reused for all R rows.
 //  * Each row's partials are reduced across the wave with shuffles.
 #include "gguf_common.h"
+#include "gguf_decode.h"
 #include "gguf_launch.h"
 
 namespace tensor_gguf {
@@ -335,6 +336,80 @@ __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
   store_rows<SWIGLU>(acc, out, n_rows, row0, rows, lane);
 }
 
+// ------------------------------------------------------ other encodings ---
+// Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K: each lane decodes 8-element groups with the
+// dequantizer's arithmetic (decode8) and accumulates their products with the
+// activations in fp32.  Consecutive lanes take consecutive groups, so one wave
+// pass covers 512 consecutive elements of its rows; the activation group is
+// loaded once and reused for all R rows.
+template <int TYPE, int M, int R, typename OutT, bool SWIGLU = false>
+__global__ __launch_bounds__(256) void gemv_blocks(const _Float16* __restrict__ x,
+                                                   const uint8_t* __restrict__ w,
+                                                   OutT* __restrict__ out, int n_rows, int k,
+                                                   const uint8_t* __restrict__ w2 = nullptr) {
+  constexpr int QK = Block<TYPE>::QK, BYTES = Block<TYPE>::BYTES;
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (SWIGLU ? 1 : R);
+  if (row0 >= n_rows) return;
+  const size_t row_bytes = (size_t)(k / QK) * BYTES;
+  const int rows = SWIGLU ? R : min(R, n_rows - row0);
+  float acc[M][R];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+  for (int g = lane; g < (k >> 3); g += 64) {
+    const int e = 8 * g;
+    float xv[M][8];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const uint4 raw = load16(reinterpret_cast<const uint8_t*>(x + (size_t)m * k + e));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const half2_t pair = as_half2(word(raw, i));
+        xv[m][2 * i] = (float)pair.x;
+        xv[m][2 * i + 1] = (float)pair.y;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r >= rows) break;
+      const uint8_t* block = pair_row<SWIGLU>(w, w2, row0, r, row_bytes) + (size_t)(e / QK) * BYTES;
+      float v[8];
+      decode8<TYPE>(block, e % QK, v);
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[m][r] = fmaf(v[i], xv[m][i], acc[m][r]);
+    }
+  }
+  store_rows<SWIGLU>(acc, out, n_rows, row0, rows, lane);
+}
+
+// Every encoding without a dedicated kernel goes to gemv_blocks.
+template <int M, int R, typename OutT, bool SWIGLU>
+static bool launch_blocks(const GemvArgs& a, const uint8_t* w2, dim3 grid, hipStream_t stream) {
+  const _Float16* x = static_cast<const _Float16*>(a.x);
+  const uint8_t* w = static_cast<const uint8_t*>(a.w);
+  OutT* out = static_cast<OutT*>(a.out);
+  switch (a.type) {
+#define TENSOR_GGUF_BLOCKS(T)                                                                                  \
+  case T:                                                                                                      \
+    hipLaunchKernelGGL((gemv_blocks<T, M, R, OutT, SWIGLU>), grid, dim3(256), 0, stream, x, w, out, a.n, a.k, w2); \
+    return true;
+    TENSOR_GGUF_BLOCKS(kQ4_1)
+    TENSOR_GGUF_BLOCKS(kQ5_0)
+    TENSOR_GGUF_BLOCKS(kQ5_1)
+    TENSOR_GGUF_BLOCKS(kQ2_K)
+    TENSOR_GGUF_BLOCKS(kQ3_K)
+    TENSOR_GGUF_BLOCKS(kQ5_K)
+#undef TENSOR_GGUF_BLOCKS
+    default:
+      return false;
+  }
+}
+
 // --------------------------------------------------------------- launch ---
 
 template <int M, typename OutT>
@@ -359,7 +434,7 @@ static hipError_t launch_m(const GemvArgs& a, hipStream_t stream) {
       hipLaunchKernelGGL((gemv_q32<kQ4_0, M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
       break;
     default:
-      return hipErrorInvalidValue;
+      if (!launch_blocks<M, R, OutT, false>(a, nullptr, grid, stream)) return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -400,7 +475,7 @@ static hipError_t launch_swiglu_m(const GemvArgs& a, const uint8_t* w_up, hipStr
       hipLaunchKernelGGL((gemv_q32<kQ4_0, M, 2, OutT, true>), grid, block, 0, stream, x, w, out, a.n, a.k, w_up);
       break;
     default:
-      return hipErrorInvalidValue;
+      if (!launch_blocks<M, 2, OutT, true>(a, w_up, grid, stream)) return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }

@@ -50,8 +50,14 @@ struct Format {
 bool ggml_format(uint64_t type, Format* format) {
   switch (type) {
     case TENSOR_GGML_Q4_0: *format = {32, 18}; return true;
+    case TENSOR_GGML_Q4_1: *format = {32, 20}; return true;
+    case TENSOR_GGML_Q5_0: *format = {32, 22}; return true;
+    case TENSOR_GGML_Q5_1: *format = {32, 24}; return true;
     case TENSOR_GGML_Q8_0: *format = {32, 34}; return true;
+    case TENSOR_GGML_Q2_K: *format = {256, 84}; return true;
+    case TENSOR_GGML_Q3_K: *format = {256, 110}; return true;
     case TENSOR_GGML_Q4_K: *format = {256, 144}; return true;
+    case TENSOR_GGML_Q5_K: *format = {256, 176}; return true;
     case TENSOR_GGML_Q6_K: *format = {256, 210}; return true;
     default: return false;
   }

@@ -5,7 +5,8 @@ The reference takes raw GGML bytes from AKAS ``weight_storage`` /
 are not vendored.  This module is this package's own producer of the same
 bytes: it quantizes fp32 weights into GGML blocks (types 2, 8, 12, 14) whose
 layouts are fixed by ``benchmarks/kernels/showcase/triton_kernels.py:134-181``
-and the public GGML block definitions.  Quantization happens once, offline, on
+and the public GGML block definitions, and likewise into types 3, 6, 7, 10, 11
+and 13 (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K: public GGML layouts only).  Quantization happens once, offline, on
 the host; it is not on the GPU hot path.
 
 The packers (``pack_*``) place already-chosen integer codes into bytes.  They
@@ -18,8 +19,13 @@ from __future__ import annotations
 import numpy as np
 
 Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
-GEOMETRY = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
-NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+# The other GGML encodings the kernels decode (public GGML block definitions).
+Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K = 3, 6, 7, 10, 11, 13
+GEOMETRY = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210),
+            Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q2_K: (256, 84), Q3_K: (256, 110),
+            Q5_K: (256, 176)}
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k", Q4_1: "q4_1", Q5_0: "q5_0",
+         Q5_1: "q5_1", Q2_K: "q2_k", Q3_K: "q3_k", Q5_K: "q5_k"}
 TYPES = {name: code for code, name in NAMES.items()}
 
 
@@ -134,6 +140,102 @@ def pack_q6_k(d, scales, q) -> np.ndarray:
     return out
 
 
+def pack_q4_1(d, m, q) -> np.ndarray:
+    """d, m: [B]; q: 4-bit codes [B, 32] (value = q * d + m) -> [B, 20]; nibbles as Q4_0."""
+    q = np.asarray(q, dtype=np.uint8)
+    out = np.empty(np.shape(d) + (20,), dtype=np.uint8)
+    out[..., 0:2] = _fp16_bytes(np.asarray(d))
+    out[..., 2:4] = _fp16_bytes(np.asarray(m))
+    out[..., 4:20] = (q[..., :16] & 15) | ((q[..., 16:] & 15) << 4)
+    return out
+
+
+def _pack_q5(head: list, q) -> np.ndarray:
+    """fp16 header fields, then qh (bit j = bit 4 of code j, little-endian u32), then the
+    low nibbles as Q4_0 (element j < 16 low nibble of byte j, j + 16 its high nibble)."""
+    q = np.asarray(q, dtype=np.uint32)
+    count = len(head)
+    out = np.empty(q.shape[:-1] + (2 * count + 20,), dtype=np.uint8)
+    for i, field in enumerate(head):
+        out[..., 2 * i: 2 * i + 2] = _fp16_bytes(np.asarray(field))
+    qh = ((q >> 4) & 1) << np.arange(32, dtype=np.uint32)
+    out[..., 2 * count: 2 * count + 4] = qh.sum(axis=-1, dtype=np.uint32)[..., None].view(np.uint8)
+    low = (q & 15).astype(np.uint8)
+    out[..., 2 * count + 4:] = low[..., :16] | (low[..., 16:] << 4)
+    return out
+
+
+def pack_q5_0(d, q) -> np.ndarray:
+    """d: [B]; q: 5-bit codes [B, 32] (value = (q - 16) * d) -> [B, 22]."""
+    return _pack_q5([d], q)
+
+
+def pack_q5_1(d, m, q) -> np.ndarray:
+    """d, m: [B]; q: 5-bit codes [B, 32] (value = q * d + m) -> [B, 24]."""
+    return _pack_q5([d, m], q)
+
+
+def pack_q2_k(d, dmin, scales, mins, q) -> np.ndarray:
+    """Pack a Q2_K super-block.
+
+    d, dmin: [B]; scales, mins: 4-bit codes [B, 16] (one per 16 elements); q: 2-bit
+    codes [B, 256].  Value of element e: d*scales[e//16]*q[e] - dmin*mins[e//16].
+    Byte s of the 16 scale bytes is scales[s] | mins[s] << 4.  Each 128-element half
+    owns 32 code bytes: element h*128 + 32*p + l sits in bits 2p..2p+1 of byte h*32 + l.
+    Then fp16 d and fp16 dmin.
+    """
+    q = np.asarray(q, dtype=np.uint8)
+    out = np.zeros(np.shape(d) + (84,), dtype=np.uint8)
+    out[..., 0:16] = (np.asarray(scales, dtype=np.uint8) & 15) | ((np.asarray(mins, dtype=np.uint8) & 15) << 4)
+    for h in range(2):
+        for p in range(4):
+            out[..., 16 + 32 * h: 48 + 32 * h] |= (q[..., 128 * h + 32 * p: 128 * h + 32 * p + 32] & 3) << (2 * p)
+    out[..., 80:82] = _fp16_bytes(np.asarray(d))
+    out[..., 82:84] = _fp16_bytes(np.asarray(dmin))
+    return out
+
+
+def pack_q3_k(d, scales, q) -> np.ndarray:
+    """Pack a Q3_K super-block.
+
+    d: [B]; scales: signed 6-bit [B, 16] in -32..31 (one per 16 elements); q: signed
+    3-bit codes [B, 256] in -4..3.  Value of element e: d * scales[e//16] * q[e].
+    Code c = q + 4: its low 2 bits sit like Q2_K's codes (32 bytes after the 32-byte
+    mask), its bit 2 in mask byte e % 32 at bit (e // 128) * 4 + (e % 128) // 32.
+    Scale s is stored as u = scales[s] + 32: the low nibble in byte s (s < 8) or the
+    high nibble of byte s - 8 (s >= 8) of the 12 scale bytes, the top 2 bits in byte
+    8 + s % 4 at bit 2 * (s // 4).  Then fp16 d.
+    """
+    code = (np.asarray(q, dtype=np.int16) + 4).astype(np.uint8)
+    u = (np.asarray(scales, dtype=np.int16) + 32).astype(np.uint8)
+    out = np.zeros(np.shape(d) + (110,), dtype=np.uint8)
+    for e0 in range(0, 256, 32):
+        h, p = e0 // 128, e0 % 128 // 32
+        part = code[..., e0: e0 + 32]
+        out[..., 0:32] |= ((part >> 2) & 1) << (4 * h + p)
+        out[..., 32 + 32 * h: 64 + 32 * h] |= (part & 3) << (2 * p)
+    for index in range(16):
+        low, high = u[..., index] & 15, (u[..., index] >> 4) & 3
+        out[..., 96 + index % 8] |= low << (4 * (index // 8))
+        out[..., 104 + index % 4] |= high << (2 * (index // 4))
+    out[..., 108:110] = _fp16_bytes(np.asarray(d))
+    return out
+
+
+def pack_q5_k(d, dmin, scales, mins, q) -> np.ndarray:
+    """Pack a Q5_K super-block: Q4_K's header and nibble layout for the low 4 bits of
+    the 5-bit codes q [B, 256], with bit 4 of element e in byte e % 32 of the 32-byte
+    qh run at bit e // 32.  Value: d*scales[e//32]*q[e] - dmin*mins[e//32]."""
+    q = np.asarray(q, dtype=np.uint8)
+    q4k = pack_q4_k(d, dmin, scales, mins, q & 15)
+    out = np.zeros(np.shape(d) + (176,), dtype=np.uint8)
+    out[..., 0:16] = q4k[..., 0:16]
+    for sub in range(8):
+        out[..., 16:48] |= ((q[..., 32 * sub: 32 * sub + 32] >> 4) & 1) << sub
+    out[..., 48:176] = q4k[..., 16:144]
+    return out
+
+
 # ---------------------------------------------------------------- quantizers --
 
 def quantize_q8_0(w: np.ndarray) -> np.ndarray:
@@ -203,7 +305,85 @@ def quantize_q6_k(w: np.ndarray) -> np.ndarray:
     return pack_q6_k(d, scales, q.astype(np.uint8).reshape(-1, 256))
 
 
-QUANTIZERS = {Q4_0: quantize_q4_0, Q8_0: quantize_q8_0, Q4_K: quantize_q4_k, Q6_K: quantize_q6_k}
+def _affine_codes(blocks, levels):
+    """Per-block affine fit [lo, hi] -> (step, lo, codes 0..levels) with round-half-away."""
+    lo, hi = blocks.min(axis=-1), blocks.max(axis=-1)
+    step = ((hi - lo) / levels).astype(np.float16).astype(np.float32)
+    base = lo.astype(np.float16).astype(np.float32)
+    safe = np.where(step > 0, step, 1.0)
+    codes = np.where(step[..., None] > 0, _round_half_away((blocks - base[..., None]) / safe[..., None]), 0)
+    return step, base, np.clip(codes, 0, levels).astype(np.uint8)
+
+
+def quantize_q4_1(w: np.ndarray) -> np.ndarray:
+    """Q4_1: per 32 values d = (max - min)/15 and m = min, q = round((x - m)/d)."""
+    step, base, q = _affine_codes(np.asarray(w, dtype=np.float32).reshape(-1, 32), 15)
+    return pack_q4_1(step, base, q)
+
+
+def quantize_q5_1(w: np.ndarray) -> np.ndarray:
+    """Q5_1: per 32 values d = (max - min)/31 and m = min."""
+    step, base, q = _affine_codes(np.asarray(w, dtype=np.float32).reshape(-1, 32), 31)
+    return pack_q5_1(step, base, q)
+
+
+def quantize_q5_0(w: np.ndarray) -> np.ndarray:
+    """Q5_0: the signed extreme maps to code 0 (d = extreme / -16), as Q4_0 does with -8."""
+    blocks = np.asarray(w, dtype=np.float32).reshape(-1, 32)
+    extreme = blocks[np.arange(blocks.shape[0]), np.abs(blocks).argmax(axis=1)]
+    d = (extreme / -16.0).astype(np.float16).astype(np.float32)
+    inv = np.where(d != 0, 1.0 / np.where(d != 0, d, 1.0), 0.0).astype(np.float32)
+    q = np.clip(np.floor(blocks * inv[:, None] + 16.5), 0, 31).astype(np.uint8)
+    return pack_q5_0(d, q)
+
+
+def _k_affine(blocks, levels, scale_levels):
+    """K-quant affine fit: per sub-block step (hi - lo)/levels and offset -lo (lo <= 0),
+    both quantized against the super-block's d and dmin (largest / scale_levels)."""
+    lo = np.minimum(blocks.min(axis=2), 0.0)
+    step = (blocks.max(axis=2) - lo) / levels
+    offset = -lo
+    d = (step.max(axis=1) / scale_levels).astype(np.float16)
+    dmin = (offset.max(axis=1) / scale_levels).astype(np.float16)
+    d32, dmin32 = d.astype(np.float32), dmin.astype(np.float32)
+    scales = np.clip(_round_half_away(step / np.where(d32 > 0, d32, 1.0)[:, None]), 0, scale_levels)
+    mins = np.clip(_round_half_away(offset / np.where(dmin32 > 0, dmin32, 1.0)[:, None]), 0, scale_levels)
+    unit = d32[:, None] * scales.astype(np.float32)
+    base = dmin32[:, None] * mins.astype(np.float32)
+    q = _round_half_away((blocks + base[:, :, None]) / np.where(unit > 0, unit, 1.0)[:, :, None])
+    q = np.where(unit[:, :, None] > 0, np.clip(q, 0, levels), 0).astype(np.uint8)
+    return d, dmin, scales.astype(np.uint8), mins.astype(np.uint8), q.reshape(blocks.shape[0], -1)
+
+
+def quantize_q2_k(w: np.ndarray) -> np.ndarray:
+    """Q2_K: 2-bit codes with a 4-bit (step, offset) pair per 16 elements."""
+    return pack_q2_k(*_k_affine(np.asarray(w, dtype=np.float32).reshape(-1, 16, 16), 3, 15))
+
+
+def quantize_q5_k(w: np.ndarray) -> np.ndarray:
+    """Q5_K: 5-bit codes with 6-bit (step, offset) pairs per 32 elements."""
+    return pack_q5_k(*_k_affine(np.asarray(w, dtype=np.float32).reshape(-1, 8, 32), 31, 63))
+
+
+def quantize_q3_k(w: np.ndarray) -> np.ndarray:
+    """Q3_K: per 16 elements the signed extreme maps to code -4; the sixteen signed
+    6-bit scales are quantized against d = largest / -32."""
+    blocks = np.asarray(w, dtype=np.float32).reshape(-1, 16, 16)
+    extreme = np.take_along_axis(blocks, np.abs(blocks).argmax(axis=2)[:, :, None], axis=2)[:, :, 0]
+    sub = extreme / -4.0
+    big = np.take_along_axis(sub, np.abs(sub).argmax(axis=1)[:, None], axis=1)[:, 0]
+    d = (big / -32.0).astype(np.float16).astype(np.float32)
+    inv = np.where(d != 0, 1.0 / np.where(d != 0, d, 1.0), 0.0).astype(np.float32)
+    scales = np.clip(_round_half_away(sub * inv[:, None]), -32, 31)
+    unit = d[:, None] * scales.astype(np.float32)
+    q = _round_half_away(blocks / np.where(unit != 0, unit, 1.0)[:, :, None])
+    q = np.where(unit[:, :, None] != 0, np.clip(q, -4, 3), 0)
+    return pack_q3_k(d, scales.astype(np.int8), q.astype(np.int8).reshape(-1, 256))
+
+
+QUANTIZERS = {Q4_0: quantize_q4_0, Q8_0: quantize_q8_0, Q4_K: quantize_q4_k, Q6_K: quantize_q6_k,
+              Q4_1: quantize_q4_1, Q5_0: quantize_q5_0, Q5_1: quantize_q5_1, Q2_K: quantize_q2_k,
+              Q3_K: quantize_q3_k, Q5_K: quantize_q5_k}
 
 
 def quantize(w: np.ndarray, encoding) -> np.ndarray:

@@ -33,11 +33,12 @@ def random_blocks(encoding, n: int, k: int, seed: int, scale: float = 0.05) -> n
     rng = np.random.default_rng(seed)
     blocks = n * k // qk
     raw = rng.integers(0, 256, size=(blocks, size), dtype=np.uint8)
-    halves = (rng.standard_normal((blocks, 2)) * scale).astype(np.float16).view(np.uint8).reshape(blocks, 4)
-    if code in (Q.Q4_0, Q.Q8_0):
-        raw[:, 0:2] = halves[:, 0:2]
-    elif code == Q.Q4_K:
-        raw[:, 0:4] = halves
-    else:
-        raw[:, 208:210] = halves[:, 0:2]
+    for offset in HALF_FIELDS[code]:
+        half = (rng.standard_normal(blocks) * scale).astype(np.float16).view(np.uint8).reshape(blocks, 2)
+        raw[:, offset:offset + 2] = half
     return raw.reshape(n, -1)
+
+
+# Byte offsets of each encoding's fp16 fields (d, and m / dmin where present).
+HALF_FIELDS = {Q.Q4_0: (0,), Q.Q8_0: (0,), Q.Q4_K: (0, 2), Q.Q6_K: (208,), Q.Q4_1: (0, 2), Q.Q5_0: (0,),
+               Q.Q5_1: (0, 2), Q.Q2_K: (80, 82), Q.Q3_K: (108,), Q.Q5_K: (0, 2)}

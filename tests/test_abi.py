@@ -344,7 +344,9 @@ def test_unknown_kernel_and_encoding():
     with pytest.raises(ValueError):
         kernels.manifest("gguf_conv", "q4_k")
     with pytest.raises(ValueError):
-        kernels.manifest("gguf_linear", "q5_k")
+        kernels.manifest("gguf_linear", "iq4_xs")
+    with pytest.raises(ValueError):
+        kernels.manifest("gguf_linear", 15)  # Q8_K: an intermediate format, not a weight encoding
     with pytest.raises(ValueError):
         kernels.manifest("gguf_linear", "q4_k", out_dtype="bfloat16")
 

@@ -21,7 +21,9 @@ from tests import gguf_cases as cases
 pytestmark = pytest.mark.gpu
 
 TOLERANCE = 2e-3  # relative L2
-ENCODINGS = ("q4_k", "q6_k", "q8_0", "q4_0")
+# The showcase's encodings, then the other GGML formats (public layouts; generic kernels).
+MORE = ("q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q5_k")
+ENCODINGS = ("q4_k", "q6_k", "q8_0", "q4_0") + MORE
 
 
 def note(*parts):
@@ -172,6 +174,7 @@ def test_gemv_q4k_multirow_configurations(hip_device, m, n, k):
     ("q4_k", 4, 4096),    # M > 1: one launch per matrix
     ("q6_k", 1, 4096),    # no grouped kernel: one launch per matrix
     ("q8_0", 2, 2560),
+    ("q5_k", 1, 2048),
 ])
 @pytest.mark.parametrize("count", [1, 2, 3])
 def test_gemv_group_parity(hip_device, encoding, m, k, count):
@@ -240,6 +243,12 @@ def run_swiglu(device, encoding, x, gate, up, out_dtype):
     ("q6_k", 3, 77, 512),
     ("q8_0", 2, 100, 2560),
     ("q4_0", 8, 65, 1024),
+    ("q5_k", 1, 300, 2048),
+    ("q3_k", 3, 77, 512),
+    ("q2_k", 1, 64, 4096),
+    ("q4_1", 2, 100, 1024),
+    ("q5_0", 4, 33, 512),
+    ("q5_1", 8, 65, 1024),
 ])
 def test_gemv_swiglu_parity(hip_device, encoding, m, n, k):
     """silu(x W_gate^T) * (x W_up^T) in one launch against the oracle's composition."""
@@ -405,3 +414,58 @@ def test_linear_on_weights_read_from_a_gguf_file(hip_device, c_oracle, encoding,
         got = run_linear(hip_device, "gguf_linear", encoding, x, rows, "float32")
         del rows
     assert R.relative_l2(got, expected) <= TOLERANCE
+
+
+# A Q4_K / Q5_K element whose fp32 value is an fp16 rounding tie although the exact value
+# is not: d = fp16 bits 11277, dmin = fp16 bits 4647, scale 9, min 23, code 15 gives the
+# exact 8.5273432..., fp32 8.52734375 (the midpoint of fp16 8.5234375 and 8.53125), so the
+# reference's order (fp32 dequantization, then a cast) stores 8.53125 and a single
+# rounding of the exact value would store 8.5234375.
+TIE_D, TIE_DMIN, TIE_SC, TIE_MN, TIE_Q, TIE_HALF = 11277, 4647, 9, 23, 15, 8.53125
+
+
+def tie_blocks(encoding, n, k):
+    blocks = n * k // 256
+    d = np.full(blocks, TIE_D, np.uint16).view(np.float16)
+    dmin = np.full(blocks, TIE_DMIN, np.uint16).view(np.float16)
+    scales, mins = np.full((blocks, 8), TIE_SC), np.full((blocks, 8), TIE_MN)
+    q = np.full((blocks, 256), TIE_Q, np.uint8)
+    pack = Q.pack_q4_k if encoding == "q4_k" else Q.pack_q5_k
+    return pack(d, dmin, scales, mins, q).reshape(n, -1)
+
+
+@pytest.mark.parametrize("encoding", ["q4_k", "q5_k"])
+def test_fp16_weights_are_the_cast_of_the_fp32_dequantization(hip_device, c_oracle, encoding):
+    """Dequantizer fp16 output and the weights the GEMMs stage in fp16 (the pipelined Q4_K
+    kernel, the generic kernel for Q5_K) round the fp32 value, not the exact value."""
+    code = Q.ggml_type(encoding)
+    n, k = 256, 512
+    note("fp16-tie", encoding)
+    raw = tie_blocks(encoding, n, k)
+    assert np.all(c_oracle.dequantize(raw, code, n, k).astype(np.float16) == TIE_HALF)
+    exe = hip_device.load("gguf_dequant", encoding=encoding, out_dtype="float16")
+    wb = hip_device.from_numpy(raw)
+    out = exe(wb, K=k)
+    assert np.all(out.to_numpy() == TIE_HALF)
+    out.release()
+    wb.release()
+    x = np.zeros((64, k), np.float16)
+    x[np.arange(64), np.arange(64) * 7] = 1.0  # one-hot rows: out = fp16 weights
+    got = run_linear(hip_device, "gguf_gemm", encoding, x, raw, "float32")
+    assert np.all(got == TIE_HALF), np.unique(got)
+
+
+@pytest.mark.parametrize("encoding", MORE)
+def test_generic_gemm_one_hot_rows_give_dequantized_weights(hip_device, c_oracle, encoding):
+    """The generic GEMM stages every weight of the other encodings as fp16(dequant): one-hot
+    rows read them back bit for bit."""
+    code = Q.ggml_type(encoding)
+    k, n = 512, 384
+    note("gemm-one-hot-generic", encoding)
+    raw = cases.random_blocks(encoding, n, k, 98)
+    deq = c_oracle.dequantize(raw, code, n, k).astype(np.float16).astype(np.float32)
+    perm = np.random.default_rng(99).permutation(k)
+    x = np.zeros((k, k), np.float16)
+    x[np.arange(k), perm] = 1.0
+    got = run_linear(hip_device, "gguf_gemm", encoding, x, raw, "float32")
+    assert np.array_equal(got, deq[:, perm].T), encoding

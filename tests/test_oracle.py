@@ -18,6 +18,8 @@ from oracle import gguf_ref as R
 from tensor_amd.gguf import quant as Q
 
 TYPES = (Q.Q4_0, Q.Q8_0, Q.Q4_K, Q.Q6_K)
+# Encodings restated from the public GGML block definitions only.
+MORE = (Q.Q4_1, Q.Q5_0, Q.Q5_1, Q.Q2_K, Q.Q3_K, Q.Q5_K)
 
 
 def both(raw, t, n, k, c_oracle):
@@ -27,21 +29,22 @@ def both(raw, t, n, k, c_oracle):
     return a
 
 
+# Byte offsets of each encoding's fp16 fields.
+HALF_FIELDS = {Q.Q4_0: (0,), Q.Q8_0: (0,), Q.Q4_K: (0, 2), Q.Q6_K: (208,), Q.Q4_1: (0, 2), Q.Q5_0: (0,),
+               Q.Q5_1: (0, 2), Q.Q2_K: (80, 82), Q.Q3_K: (108,), Q.Q5_K: (0, 2)}
+
+
 def random_blocks(t, blocks, rng):
     """Random bytes with every fp16 scale field replaced by a finite value."""
     qk, size = Q.GEOMETRY[t]
     raw = rng.integers(0, 256, size=(blocks, size), dtype=np.uint8)
-    halves = (rng.standard_normal((blocks, 2)) * 0.05).astype(np.float16).view(np.uint8).reshape(blocks, 4)
-    if t in (Q.Q4_0, Q.Q8_0):
-        raw[:, 0:2] = halves[:, 0:2]
-    elif t == Q.Q4_K:
-        raw[:, 0:4] = halves
-    else:
-        raw[:, 208:210] = halves[:, 0:2]
+    for offset in HALF_FIELDS[t]:
+        half = (rng.standard_normal(blocks) * 0.05).astype(np.float16).view(np.uint8).reshape(blocks, 2)
+        raw[:, offset:offset + 2] = half
     return raw
 
 
-@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("t", TYPES + MORE)
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_numpy_and_c_decoders_agree_bitwise(t, seed, c_oracle):
     rng = np.random.default_rng(seed)
@@ -139,8 +142,110 @@ def test_q4_0_layout(c_oracle):
     assert np.array_equal(got, (d.astype(np.float64)[:, None] * (q.astype(np.float64) - 8)).astype(np.float32))
 
 
+def fp16(rng, shape):
+    return rng.standard_normal(shape).astype(np.float16)
+
+
+def test_q4_1_layout(c_oracle):
+    rng = np.random.default_rng(11)
+    blocks = 256
+    d, m = fp16(rng, blocks), fp16(rng, blocks)
+    q = rng.integers(0, 16, size=(blocks, 32), dtype=np.uint8)
+    got = both(Q.pack_q4_1(d, m, q), Q.Q4_1, blocks, 32, c_oracle)
+    # q*d is exact; the addition rounds once
+    expected = (d.astype(np.float64)[:, None] * q + m.astype(np.float64)[:, None]).astype(np.float32)
+    assert np.array_equal(got, expected)
+
+
+@pytest.mark.parametrize("t", [Q.Q5_0, Q.Q5_1])
+def test_q5_high_bit_and_nibble_layout(t, c_oracle):
+    rng = np.random.default_rng(12)
+    blocks = 256
+    d, m = fp16(rng, blocks), fp16(rng, blocks)
+    q = rng.integers(0, 32, size=(blocks, 32), dtype=np.uint8)
+    q[0] = np.arange(32)  # every code, every position of the high-bit word
+    q[1] = 31 - np.arange(32)
+    if t == Q.Q5_0:
+        got = both(Q.pack_q5_0(d, q), t, blocks, 32, c_oracle)
+        expected = d.astype(np.float64)[:, None] * (q.astype(np.float64) - 16)
+    else:
+        got = both(Q.pack_q5_1(d, m, q), t, blocks, 32, c_oracle)
+        expected = d.astype(np.float64)[:, None] * q + m.astype(np.float64)[:, None]
+    assert np.array_equal(got, expected.astype(np.float32))
+    # the unit-scale block decodes to the codes themselves
+    unit = both(Q.pack_q5_1(np.ones(1), np.zeros(1), q[:1]), Q.Q5_1, 1, 32, c_oracle)
+    assert np.array_equal(unit[0], np.arange(32, dtype=np.float32))
+
+
+def test_q2_k_fields(c_oracle):
+    rng = np.random.default_rng(13)
+    blocks = 256
+    d, dmin = fp16(rng, blocks), fp16(rng, blocks)
+    scales = rng.integers(0, 16, size=(blocks, 16))
+    mins = rng.integers(0, 16, size=(blocks, 16))
+    q = rng.integers(0, 4, size=(blocks, 256), dtype=np.uint8)
+    got = both(Q.pack_q2_k(d, dmin, scales, mins, q), Q.Q2_K, blocks, 256, c_oracle)
+    ds = d.astype(np.float64)[:, None] * np.repeat(scales, 16, axis=1)
+    dm = dmin.astype(np.float64)[:, None] * np.repeat(mins, 16, axis=1)
+    assert np.array_equal(got, (ds * q - dm).astype(np.float32))
+    # unit scales: the codes themselves, in element order
+    unit = both(Q.pack_q2_k(np.ones(blocks), np.zeros(blocks), np.ones((blocks, 16)), np.zeros((blocks, 16)), q),
+                Q.Q2_K, blocks, 256, c_oracle)
+    assert np.array_equal(unit, q.astype(np.float32))
+
+
+def test_q3_k_scale_packing_exhaustive(c_oracle):
+    """Every signed 6-bit scale in each of the 16 positions, codes -4..3 in every plane."""
+    rng = np.random.default_rng(14)
+    for index in range(16):
+        blocks = 64
+        scales = rng.integers(-32, 32, size=(blocks, 16))
+        scales[:, index] = np.arange(-32, 32)
+        q = np.ones((blocks, 256), dtype=np.int8)
+        got = both(Q.pack_q3_k(np.ones(blocks), scales, q), Q.Q3_K, blocks, 256, c_oracle)
+        assert np.array_equal(got, np.repeat(scales.astype(np.float32), 16, axis=1)), f"scale {index}"
+    q = rng.integers(-4, 4, size=(64, 256)).astype(np.int8)
+    q[0] = np.tile(np.arange(-4, 4), 32)
+    unit = both(Q.pack_q3_k(np.ones(64), np.ones((64, 16)), q), Q.Q3_K, 64, 256, c_oracle)
+    assert np.array_equal(unit, q.astype(np.float32))
+    d = fp16(rng, 64)
+    scales = rng.integers(-32, 32, size=(64, 16))
+    got = both(Q.pack_q3_k(d, scales, q), Q.Q3_K, 64, 256, c_oracle)
+    expected = d.astype(np.float64)[:, None] * np.repeat(scales, 16, axis=1) * q
+    assert np.array_equal(got, expected.astype(np.float32))
+
+
+def test_q5_k_fields(c_oracle):
+    rng = np.random.default_rng(15)
+    blocks = 256
+    d, dmin = fp16(rng, blocks), fp16(rng, blocks)
+    scales = rng.integers(0, 64, size=(blocks, 8))
+    mins = rng.integers(0, 64, size=(blocks, 8))
+    q = rng.integers(0, 32, size=(blocks, 256), dtype=np.uint8)
+    got = both(Q.pack_q5_k(d, dmin, scales, mins, q), Q.Q5_K, blocks, 256, c_oracle)
+    ds = d.astype(np.float64)[:, None] * np.repeat(scales, 32, axis=1)
+    dm = dmin.astype(np.float64)[:, None] * np.repeat(mins, 32, axis=1)
+    assert np.array_equal(got, (ds * q - dm).astype(np.float32))
+    # the high bit alone: q = 16 * bit places bit 4 of element e in qh byte e % 32, bit e // 32
+    bits = rng.integers(0, 2, size=(blocks, 256), dtype=np.uint8)
+    unit = both(Q.pack_q5_k(np.ones(blocks), np.zeros(blocks), np.ones((blocks, 8)), np.zeros((blocks, 8)), 16 * bits),
+                Q.Q5_K, blocks, 256, c_oracle)
+    assert np.array_equal(unit, 16.0 * bits)
+
+
+@pytest.mark.parametrize("t", MORE + TYPES)
+def test_quantizers_reconstruct_their_input(t, c_oracle):
+    """The seeded quantizers (encoder direction) and the decoders agree on what a block
+    means: decoding a quantized matrix reproduces it within the format's resolution."""
+    w = np.random.default_rng(16).standard_normal((16, 512)).astype(np.float32) * 0.02
+    raw = Q.quantize(w, t)
+    error = np.linalg.norm(both(raw, t, 16, 512, c_oracle) - w) / np.linalg.norm(w)
+    bound = {Q.Q2_K: 0.4, Q.Q3_K: 0.2, Q.Q4_0: 0.12, Q.Q4_1: 0.12, Q.Q4_K: 0.12}.get(t, 0.06)
+    assert error < bound, (Q.NAMES[t], error)
+
+
 def test_all_zero_blocks_decode_to_zero(c_oracle):
-    for t in TYPES:
+    for t in TYPES + MORE:
         qk, size = Q.GEOMETRY[t]
         raw = np.zeros((4, size), dtype=np.uint8)
         assert not both(raw, t, 4, qk, c_oracle).any()
@@ -149,7 +254,7 @@ def test_all_zero_blocks_decode_to_zero(c_oracle):
 def test_row_major_block_order(c_oracle):
     """Block (n, b) sits at byte (n*K/QK + b)*BLOCK: permuting rows permutes output rows."""
     rng = np.random.default_rng(10)
-    for t in TYPES:
+    for t in TYPES + MORE:
         qk, size = Q.GEOMETRY[t]
         n, k = 6, 2 * 256
         raw = random_blocks(t, n * k // qk, rng).reshape(n, -1)
@@ -244,3 +349,19 @@ def test_relative_l2_definition():
     e = np.array([3.0, 4.0])
     assert R.relative_l2(e + np.array([0.3, 0.4]), e) == pytest.approx(0.1)
     assert R.relative_l2(np.ones(2), np.zeros(2)) == pytest.approx(np.sqrt(2) / 1e-12)
+
+
+def test_oracle_fp16_weights_round_twice(c_oracle):
+    """The prefill oracle casts the fp32 dequantized weight to fp16 (the reference's order,
+    triton_kernels.py:199-211): for a weight whose fp32 value is an fp16 tie although the
+    exact value is not, that differs from rounding the exact value once."""
+    d, dmin = np.array([11277], np.uint16).view(np.float16), np.array([4647], np.uint16).view(np.float16)
+    raw = Q.pack_q4_k(d, dmin, np.full((1, 8), 9), np.full((1, 8), 23), np.full((1, 256), 15, np.uint8))
+    fp32 = both(raw, Q.Q4_K, 1, 256, c_oracle)
+    exact = float(d[0]) * 9 * 15 - float(dmin[0]) * 23
+    assert float(fp32[0, 0]) != exact and np.float16(exact) == np.float16(8.5234375)
+    assert np.all(fp32.astype(np.float16) == np.float16(8.53125))
+    x = np.zeros((1, 256), np.float16)
+    x[0, 5] = 1.0
+    assert c_oracle.linear(x, raw, Q.Q4_K, 1, 256, prefill=True)[0, 0] == np.float32(8.53125)
+

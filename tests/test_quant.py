@@ -55,8 +55,10 @@ def test_sample_weight_deterministic_and_seeded():
 
 
 def test_type_names_and_errors():
-    assert Q.ggml_type("Q4_K") == 12 and Q.ggml_type(14) == 14
+    assert Q.ggml_type("Q4_K") == 12 and Q.ggml_type(14) == 14 and Q.ggml_type("q5_k") == 13
     with pytest.raises(ValueError):
-        Q.ggml_type("q5_k")
+        Q.ggml_type("iq4_xs")
+    with pytest.raises(ValueError):
+        Q.ggml_type(15)
     with pytest.raises(ValueError):
         Q.row_bytes(Q.Q4_K, 300)

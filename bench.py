@@ -315,6 +315,7 @@ def cpu_baseline(budget_s=10.0):
 # ------------------------------------------------------------------- main --
 
 def main():
+    global TIMING, WARM_SECONDS
     parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=300)
@@ -339,7 +340,6 @@ def main():
         return 2
     if args.steps < 1 or args.warmup < 0:
         parser.error("steps must be >= 1 and warmup >= 0")
-    global TIMING, WARM_SECONDS
     TIMING = args.timing
     WARM_SECONDS = max(0.0, args.warm_seconds)
 

@@ -152,6 +152,10 @@ def test_gemv_q6k_tall_rows_each_within_tolerance(hip_device, c_oracle, n):
     (2, 40, 256),       # one super-block, one wave
     (4, 8200, 512),     # two tiles per wave and a single wave: the wave stores both tiles
     (8, 1024, 12288),   # x too large for LDS: the one-super-block-per-step kernel
+    (8, 4100, 12288),   # C2 down at M = 8 (one super-block per step), ragged rows
+    (6, 300, 16384),    # the longest rows, x too large for LDS
+    (8, 64, 16384),     # x of 256 KB
+    (8, 300, 8448),     # K not a multiple of 1024 and x too large for LDS
 ])
 def test_gemv_q4k_multirow_configurations(hip_device, m, n, k):
     code = Q.ggml_type("q4_k")

@@ -44,7 +44,8 @@ FP16_PEAK_TFLOPS = 2516.6   # MI355X dense fp16 MFMA
 MALL_BYTES = 256 << 20
 ROTATION_BYTES = 3 * MALL_BYTES
 METRIC = "Q4_K/Q6_K decode GEMV GB/s (% HBM peak); prefill dequant-GEMM TFLOP/s"
-GEOMETRY = {"q4_0": (32, 18), "q8_0": (32, 34), "q4_k": (256, 144), "q6_k": (256, 210)}
+GEOMETRY = {"q4_0": (32, 18), "q8_0": (32, 34), "q4_k": (256, 144), "q6_k": (256, 210), "q4_1": (32, 20),
+            "q5_0": (32, 22), "q5_1": (32, 24), "q2_k": (256, 84), "q3_k": (256, 110), "q5_k": (256, 176)}
 
 
 def log(*parts):
@@ -500,6 +501,10 @@ def run_details(device, x4096, log, only=None):
         gemv_case(f"C2_q4k_gemv_m{m}_12288x4096", "q4_k", m, 12288, 4096, "float16")
         gemv_case(f"C2_q4k_gemv_m{m}_4096x12288", "q4_k", m, 4096, 12288, "float16")
     gemv_case("C3_q6k_lm_head_m1_151936x4096_fp32", "q6_k", 1, 151936, 4096, "float32", launches=20)
+    # every other encoding at the C2 gate shape, M = 1 (Q6_K, Q8_0 and Q4_0 on their own kernels,
+    # the rest on the generic per-element decoder)
+    for encoding in ("q6_k", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q5_k"):
+        gemv_case(f"enc_{encoding}_gemv_m1_12288x4096", encoding, 1, 12288, 4096, "float16")
 
     def gemm_case(name, encoding, m, n, k, launches=10):
         if not wanted(name):

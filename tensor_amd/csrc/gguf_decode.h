@@ -62,11 +62,12 @@ __device__ __forceinline__ void decode8(const uint8_t* __restrict__ block, int e
     }
   } else if (TYPE == kQ4_1 || TYPE == kQ5_0 || TYPE == kQ5_1) {
     // element j < 16: low nibble of byte j; j + 16: its high nibble; Q5 bit 4 = bit j of qh
-    const float d = half_bits_to_float(block[0] | (block[1] << 8));
-    const float m = TYPE == kQ5_0 ? 0.0f : half_bits_to_float(block[2] | (block[3] << 8));
-    const int head = TYPE == kQ4_1 ? 4 : TYPE == kQ5_0 ? 6 : 8;
-    const uint32_t qh = TYPE == kQ4_1 ? 0u : load4(block + head - 4) >> e0;
-    const uint2 q = load8(block + head + (e0 & 15));
+    const uint32_t head = load4(block);  // d, then m (Q4_1, Q5_1) or the first half of qh (Q5_0)
+    const float d = half_bits_to_float(head);
+    const float m = TYPE == kQ5_0 ? 0.0f : half_bits_to_float(head >> 16);
+    const int qs = TYPE == kQ4_1 ? 4 : TYPE == kQ5_0 ? 6 : 8;
+    const uint32_t qh = TYPE == kQ4_1 ? 0u : load4(block + qs - 4) >> e0;
+    const uint2 q = load8(block + qs + (e0 & 15));
     const int shift = 4 * (e0 >> 4);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -77,9 +78,8 @@ __device__ __forceinline__ void decode8(const uint8_t* __restrict__ block, int e
     }
   } else if (TYPE == kQ2_K) {
     const uint32_t sc = block[e0 >> 4];
-    const float d = half_bits_to_float(block[80] | (block[81] << 8));
-    const float dmin = half_bits_to_float(block[82] | (block[83] << 8));
-    const float dl = d * (float)(sc & 15u), ml = dmin * (float)(sc >> 4);
+    const uint32_t dd = load4(block + 80);  // fp16 d, fp16 dmin
+    const float dl = half_bits_to_float(dd) * (float)(sc & 15u), ml = half_bits_to_float(dd >> 16) * (float)(sc >> 4);
     const int shift = 2 * ((e0 & 127) >> 5);
     const uint2 q = load8(block + 16 + 32 * (e0 >> 7) + (e0 & 31));
 #pragma unroll
@@ -88,11 +88,15 @@ __device__ __forceinline__ void decode8(const uint8_t* __restrict__ block, int e
       v[i] = dl * (float)((byte >> shift) & 3u) - ml;
     }
   } else if (TYPE == kQ3_K) {
+    // scale bytes 0-7 (low nibbles) and bytes 6-11 with d (top bits), in two loads inside the block
     const int s = e0 >> 4;
-    const uint8_t* scales = block + 96;
-    const int low = s < 8 ? (scales[s] & 15) : (scales[s - 8] >> 4);
-    const int high = (scales[8 + (s & 3)] >> (2 * (s >> 2))) & 3;
-    const float dl = half_bits_to_float(block[108] | (block[109] << 8)) * (float)((low | (high << 4)) - 32);
+    const uint2 lo8 = load8(block + 96), hi8 = load8(block + 102);
+    const uint32_t low_byte = ((s & 7) < 4 ? lo8.x : lo8.y) >> (8 * (s & 3));
+    const int low = (int)((s < 8 ? low_byte : low_byte >> 4) & 15u);
+    // byte 8 + s % 4 of the scales is byte 2 + s % 4 of hi8 (bytes 102-109)
+    const uint32_t high_byte = ((s & 3) < 2 ? hi8.x >> (16 + 8 * (s & 3)) : hi8.y >> (8 * ((s & 3) - 2))) & 0xFFu;
+    const int high = (int)((high_byte >> (2 * (s >> 2))) & 3u);
+    const float dl = half_bits_to_float(hi8.y >> 16) * (float)((low | (high << 4)) - 32);
     const int plane = (e0 & 127) >> 5, bit = 4 * (e0 >> 7) + plane;
     const uint2 q = load8(block + 32 + 32 * (e0 >> 7) + (e0 & 31));
     const uint2 hm = load8(block + (e0 & 31));
@@ -104,11 +108,12 @@ __device__ __forceinline__ void decode8(const uint8_t* __restrict__ block, int e
       v[i] = dl * (float)code;
     }
   } else {  // Q5_K
-    const float d = half_bits_to_float(block[0] | (block[1] << 8));
-    const float dmin = half_bits_to_float(block[2] | (block[3] << 8));
+    const uint4 hd = load16(block);  // fp16 d, fp16 dmin, 12 scale bytes
+    const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
     const int sub = e0 >> 5;
-    int sc, mn;
-    q4k_scale_min(block + 4, sub, sc, mn);
+    int sc_lo, mn_lo, sc_hi, mn_hi;
+    q4k_scale_pair(hd.y, hd.z, hd.w, sub >> 1, sc_lo, mn_lo, sc_hi, mn_hi);
+    const int sc = (sub & 1) ? sc_hi : sc_lo, mn = (sub & 1) ? mn_hi : mn_lo;
     const float ds = d * (float)sc, dm = dmin * (float)mn;
     const int shift = 4 * (sub & 1);
     const uint2 q = load8(block + 48 + (e0 >> 6) * 32 + (e0 & 31));

@@ -359,6 +359,7 @@ __global__ __launch_bounds__(256) void gemv_blocks(const _Float16* __restrict__ 
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
 
+#pragma unroll 4
   for (int g = lane; g < (k >> 3); g += 64) {
     const int e = 8 * g;
     float xv[M][8];
@@ -387,12 +388,15 @@ __global__ __launch_bounds__(256) void gemv_blocks(const _Float16* __restrict__ 
   store_rows<SWIGLU>(acc, out, n_rows, row0, rows, lane);
 }
 
-// Every encoding without a dedicated kernel goes to gemv_blocks.
-template <int M, int R, typename OutT, bool SWIGLU>
-static bool launch_blocks(const GemvArgs& a, const uint8_t* w2, dim3 grid, hipStream_t stream) {
+// Every encoding without a dedicated kernel goes to gemv_blocks: one row per wave (the gate /
+// up pair for SWIGLU), so that many waves hide the latency of the per-group decoder's loads.
+template <int M, typename OutT, bool SWIGLU>
+static bool launch_blocks(const GemvArgs& a, const uint8_t* w2, hipStream_t stream) {
+  constexpr int R = SWIGLU ? 2 : 1;
   const _Float16* x = static_cast<const _Float16*>(a.x);
   const uint8_t* w = static_cast<const uint8_t*>(a.w);
   OutT* out = static_cast<OutT*>(a.out);
+  const dim3 grid((a.n + 3) / 4);
   switch (a.type) {
 #define TENSOR_GGUF_BLOCKS(T)                                                                                  \
   case T:                                                                                                      \
@@ -434,7 +438,7 @@ static hipError_t launch_m(const GemvArgs& a, hipStream_t stream) {
       hipLaunchKernelGGL((gemv_q32<kQ4_0, M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
       break;
     default:
-      if (!launch_blocks<M, R, OutT, false>(a, nullptr, grid, stream)) return hipErrorInvalidValue;
+      if (!launch_blocks<M, OutT, false>(a, nullptr, stream)) return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -475,7 +479,7 @@ static hipError_t launch_swiglu_m(const GemvArgs& a, const uint8_t* w_up, hipStr
       hipLaunchKernelGGL((gemv_q32<kQ4_0, M, 2, OutT, true>), grid, block, 0, stream, x, w, out, a.n, a.k, w_up);
       break;
     default:
-      if (!launch_blocks<M, 2, OutT, true>(a, w_up, grid, stream)) return hipErrorInvalidValue;
+      if (!launch_blocks<M, OutT, true>(a, w_up, stream)) return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }

@@ -510,10 +510,11 @@ hipError_t launch_gemv_swiglu(const GemvArgs& a, const void* w_up, hipStream_t s
 }
 
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t stream) {
-  if (a.type == kQ4_K || a.type == kQ6_K) {
+  if (a.type == kQ4_K || a.type == kQ5_K || a.type == kQ6_K) {
     bool handled = false;
-    const hipError_t status = a.type == kQ4_K ? launch_gemv_q4k_fast(a, stream, &handled)
-                                              : launch_gemv_q6k_fast(a, stream, &handled);
+    const hipError_t status = a.type == kQ4_K   ? launch_gemv_q4k_fast(a, stream, &handled)
+                              : a.type == kQ5_K ? launch_gemv_q5k_fast(a, stream, &handled)
+                                                : launch_gemv_q6k_fast(a, stream, &handled);
     if (handled) return status;
   }
   return a.out_half ? launch_out<_Float16>(a, stream) : launch_out<float>(a, stream);

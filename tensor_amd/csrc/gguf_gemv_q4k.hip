@@ -88,9 +88,17 @@ constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
 // the gate matrix and the other half the same rows of the up matrix; the up
 // waves hand their sums over in LDS and the gate waves store silu(gate) * up
 // to g.out[0], so the pair's products never leave the workgroup.
-template <int STEPS, int WAVES, int MATS, typename OutT, bool SWIGLU = false>
+//
+// TYPE = kQ5_K runs Q5_K rows through the same kernel: its super-block is Q4_K's header and
+// nibbles (at byte 48) plus 32 bytes of fifth bits, bit sub of byte l for element 32 sub + l.
+// Byte l of a lane's quant chunks pairs with byte l of the qh run, so the fifth bit of each
+// code is OR-ed into its fp16 subnormal (bit 4 for the low nibble, bit 8 for the high nibble's
+// 16 q): every code stays below 1024 and exact.
+template <int STEPS, int WAVES, int MATS, typename OutT, bool SWIGLU = false, int TYPE = kQ4_K>
 __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __restrict__ x, GemvGroup<OutT> g) {
-  constexpr int K = STEPS * 4096, ROW_BYTES = STEPS * 16 * 144, T = WAVES * 64;
+  constexpr bool Q5 = TYPE == kQ5_K;
+  constexpr int BLOCK = Q5 ? 176 : 144, QOFF = Q5 ? 48 : 16, SB = 16 * BLOCK;  // SB: one 4096-column step
+  constexpr int K = STEPS * 4096, ROW_BYTES = STEPS * SB, T = WAVES * 64;
   constexpr int XC = (K / 8 + T - 1) / T;  // 16-byte x chunks per thread
   constexpr int PAIRS = WAVES / 2;
   static_assert(!SWIGLU || MATS == 2, "the SwiGLU pairing takes a gate and an up matrix");
@@ -118,14 +126,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __rest
     const int c = threadIdx.x + i * T;
     if (c < K / 8) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * c);
   }
-  const uint8_t* wl = g.w[mat] + (size_t)min(row, n_rows - 1) * ROW_BYTES + slot * 144;
+  const uint8_t* wl = g.w[mat] + (size_t)min(row, n_rows - 1) * ROW_BYTES + slot * BLOCK;
   const uint8_t* wq = wl + 32 * j;
   uint4 hd[STEPS], q0[STEPS], q1[STEPS];
+  uint4 h0[Q5 ? STEPS : 1], h1[Q5 ? STEPS : 1];  // Q5_K: the 32 fifth-bit bytes of the super-block
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
-    hd[s] = load16(wl + s * 2304);
-    q0[s] = load16(wq + s * 2304 + 16);
-    q1[s] = load16(wq + s * 2304 + 32);
+    hd[s] = load16(wl + s * SB);
+    q0[s] = load16(wq + s * SB + QOFF);
+    q1[s] = load16(wq + s * SB + QOFF + 16);
+    if constexpr (Q5) {
+      h0[s] = load16(wl + s * SB + 16);
+      h1[s] = load16(wl + s * SB + 32);
+    }
   }
   asm volatile("" ::: "memory");
 #pragma unroll
@@ -171,8 +184,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __rest
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const uint32_t q = word(u < 4 ? q0[s] : q1[s], u & 3), t = q >> 8;
-        a = dot2(q & mask, word(xs[u >> 1], 2 * (u & 1)), a);
-        a = dot2(t & mask, word(xs[u >> 1], 2 * (u & 1) + 1), a);
+        uint32_t cq = q & mask, ct = t & mask;
+        if constexpr (Q5) {
+          // fifth bit of sub-block 2j + h: bit 4 (low nibble) or bit 8 (16 x high nibble) of the half
+          const uint32_t hq = word(u < 4 ? h0[s] : h1[s], u & 3) >> (2 * j + h);
+          cq |= (hq & 0x00010001u) << (4 + 4 * h);
+          ct |= ((hq >> 8) & 0x00010001u) << (4 + 4 * h);
+        }
+        a = dot2(cq, word(xs[u >> 1], 2 * (u & 1)), a);
+        a = dot2(ct, word(xs[u >> 1], 2 * (u & 1) + 1), a);
       }
       acc2[h] = a;
       __builtin_amdgcn_sched_barrier(0);
@@ -564,14 +584,14 @@ __global__ __launch_bounds__(1024) void gemv_q4k_mt(const _Float16* __restrict__
 
 // ---------------------------------------------------------------- launch ---
 
-template <int WAVES, int MATS, typename OutT>
+template <int WAVES, int MATS, typename OutT, int TYPE = kQ4_K>
 static hipError_t launch_m1(const _Float16* x, const GemvGroup<OutT>& g, int k, hipStream_t stream) {
   const dim3 grid(g.blocks[0] + (MATS > 1 ? g.blocks[1] : 0) + (MATS > 2 ? g.blocks[2] : 0)), block(WAVES * 64);
   switch (k / 4096) {
-    case 1: hipLaunchKernelGGL((gemv_q4k_m1<1, WAVES, MATS, OutT>), grid, block, 0, stream, x, g); break;
-    case 2: hipLaunchKernelGGL((gemv_q4k_m1<2, WAVES, MATS, OutT>), grid, block, 0, stream, x, g); break;
-    case 3: hipLaunchKernelGGL((gemv_q4k_m1<3, WAVES, MATS, OutT>), grid, block, 0, stream, x, g); break;
-    case 4: hipLaunchKernelGGL((gemv_q4k_m1<4, WAVES, MATS, OutT>), grid, block, 0, stream, x, g); break;
+    case 1: hipLaunchKernelGGL((gemv_q4k_m1<1, WAVES, MATS, OutT, false, TYPE>), grid, block, 0, stream, x, g); break;
+    case 2: hipLaunchKernelGGL((gemv_q4k_m1<2, WAVES, MATS, OutT, false, TYPE>), grid, block, 0, stream, x, g); break;
+    case 3: hipLaunchKernelGGL((gemv_q4k_m1<3, WAVES, MATS, OutT, false, TYPE>), grid, block, 0, stream, x, g); break;
+    case 4: hipLaunchKernelGGL((gemv_q4k_m1<4, WAVES, MATS, OutT, false, TYPE>), grid, block, 0, stream, x, g); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -703,6 +723,28 @@ static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream, bool* hand
     case 8: return launch_multirow<8, OutT>(a, stream);
     default: *handled = false; return hipSuccess;
   }
+}
+
+// Q5_K at M = 1 (K a multiple of 4096, at most 16384): the M = 1 kernel with the fifth bits.
+template <typename OutT>
+static hipError_t launch_q5k_m1(const GemvArgs& a, hipStream_t stream) {
+  GemvGroup<OutT> g{};
+  g.w[0] = static_cast<const uint8_t*>(a.w);
+  g.out[0] = static_cast<OutT*>(a.out);
+  g.n[0] = a.n;
+  const _Float16* x = static_cast<const _Float16*>(a.x);
+  if (m1_waves(&a, 1) == 16) {
+    g.blocks[0] = (a.n + 15) / 16;
+    return launch_m1<16, 1, OutT, kQ5_K>(x, g, a.k, stream);
+  }
+  g.blocks[0] = (a.n + 7) / 8;
+  return launch_m1<8, 1, OutT, kQ5_K>(x, g, a.k, stream);
+}
+
+hipError_t launch_gemv_q5k_fast(const GemvArgs& a, hipStream_t stream, bool* handled) {
+  *handled = gemv_q4k_group_supported(a.m, a.k);
+  if (!*handled) return hipSuccess;
+  return a.out_half ? launch_q5k_m1<_Float16>(a, stream) : launch_q5k_m1<float>(a, stream);
 }
 
 hipError_t launch_gemv_q4k_fast(const GemvArgs& a, hipStream_t stream, bool* handled) {

@@ -53,6 +53,8 @@ hipError_t launch_gemv_swiglu(const GemvArgs& gate, const void* w_up, hipStream_
 // Its Q4_K M = 1 path (gate and up rows of one workgroup); waves: 8 or 16 per workgroup, 0 the default.
 hipError_t launch_gemv_q4k_swiglu_fast(const GemvArgs& gate, const void* w_up, hipStream_t stream, bool* handled,
                                        int waves = 0);
+// Q5_K fast path (the M = 1 Q4_K kernel with the fifth bits; K a multiple of 4096, at most 16384).
+hipError_t launch_gemv_q5k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 // Q6_K fast path (LDS-staged x, M = 1, K in {4096, 8192, 12288}).
 hipError_t launch_gemv_q6k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 hipError_t launch_dequant(const DequantArgs& args, hipStream_t stream);

@@ -109,6 +109,9 @@ def test_gemv_parity_small(hip_device, encoding, m, k):
     ("q6_k", 151936, 4096, 1, "float32"),  # C3 LM head, fp32 logits
     ("q6_k", 4096, 12288, 1, "float16"),   # C5 down (Q6_K)
     ("q8_0", 4096, 4096, 1, "float16"),    # C1 shape
+    ("q5_k", 12288, 4096, 1, "float16"),   # Q5_K through the M = 1 kernel (16 rows per workgroup)
+    ("q5_k", 4096, 12288, 1, "float32"),   # three 4096-column steps, 8 rows per workgroup
+    ("q5_k", 1003, 16384, 1, "float16"),   # four steps, ragged last workgroup
 ])
 def test_gemv_parity_baseline_shapes(hip_device, c_oracle, encoding, n, k, m, out_dtype):
     code = Q.ggml_type(encoding)

@@ -500,7 +500,7 @@ static hipError_t launch_swiglu_out(const GemvArgs& a, const uint8_t* w_up, hipS
 }
 
 hipError_t launch_gemv_swiglu(const GemvArgs& a, const void* w_up, hipStream_t stream) {
-  if (a.type == kQ4_K) {
+  if (a.type == kQ4_K || a.type == kQ5_K) {
     bool handled = false;
     const hipError_t status = launch_gemv_q4k_swiglu_fast(a, w_up, stream, &handled);
     if (handled) return status;

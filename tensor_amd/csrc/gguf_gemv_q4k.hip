@@ -597,7 +597,7 @@ static hipError_t launch_m1(const _Float16* x, const GemvGroup<OutT>& g, int k, 
   return hipGetLastError();
 }
 
-template <int WAVES, typename OutT>
+template <int WAVES, typename OutT, int TYPE = kQ4_K>
 static hipError_t launch_m1_waves(const GemvArgs* a, int count, hipStream_t stream) {
   GemvGroup<OutT> g{};
   for (int i = 0; i < count; ++i) {
@@ -608,9 +608,9 @@ static hipError_t launch_m1_waves(const GemvArgs* a, int count, hipStream_t stre
   }
   const _Float16* x = static_cast<const _Float16*>(a[0].x);
   switch (count) {
-    case 1: return launch_m1<WAVES, 1, OutT>(x, g, a[0].k, stream);
-    case 2: return launch_m1<WAVES, 2, OutT>(x, g, a[0].k, stream);
-    case 3: return launch_m1<WAVES, 3, OutT>(x, g, a[0].k, stream);
+    case 1: return launch_m1<WAVES, 1, OutT, TYPE>(x, g, a[0].k, stream);
+    case 2: return launch_m1<WAVES, 2, OutT, TYPE>(x, g, a[0].k, stream);
+    case 3: return launch_m1<WAVES, 3, OutT, TYPE>(x, g, a[0].k, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -624,12 +624,12 @@ static int m1_waves(const GemvArgs* a, int count) {
   return a[0].k == 4096 && rows <= 16384 ? 16 : 8;
 }
 
-template <typename OutT>
+template <typename OutT, int TYPE = kQ4_K>
 static hipError_t launch_m1_group(const GemvArgs* a, int count, hipStream_t stream, int waves = 0) {
   switch (waves > 0 ? waves : m1_waves(a, count)) {
-    case 4: return launch_m1_waves<4, OutT>(a, count, stream);
-    case 8: return launch_m1_waves<8, OutT>(a, count, stream);
-    case 16: return launch_m1_waves<16, OutT>(a, count, stream);
+    case 4: return launch_m1_waves<4, OutT, TYPE>(a, count, stream);
+    case 8: return launch_m1_waves<8, OutT, TYPE>(a, count, stream);
+    case 16: return launch_m1_waves<16, OutT, TYPE>(a, count, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -726,25 +726,10 @@ static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream, bool* hand
 }
 
 // Q5_K at M = 1 (K a multiple of 4096, at most 16384): the M = 1 kernel with the fifth bits.
-template <typename OutT>
-static hipError_t launch_q5k_m1(const GemvArgs& a, hipStream_t stream) {
-  GemvGroup<OutT> g{};
-  g.w[0] = static_cast<const uint8_t*>(a.w);
-  g.out[0] = static_cast<OutT*>(a.out);
-  g.n[0] = a.n;
-  const _Float16* x = static_cast<const _Float16*>(a.x);
-  if (m1_waves(&a, 1) == 16) {
-    g.blocks[0] = (a.n + 15) / 16;
-    return launch_m1<16, 1, OutT, kQ5_K>(x, g, a.k, stream);
-  }
-  g.blocks[0] = (a.n + 7) / 8;
-  return launch_m1<8, 1, OutT, kQ5_K>(x, g, a.k, stream);
-}
-
 hipError_t launch_gemv_q5k_fast(const GemvArgs& a, hipStream_t stream, bool* handled) {
   *handled = gemv_q4k_group_supported(a.m, a.k);
   if (!*handled) return hipSuccess;
-  return a.out_half ? launch_q5k_m1<_Float16>(a, stream) : launch_q5k_m1<float>(a, stream);
+  return a.out_half ? launch_m1_group<_Float16, kQ5_K>(&a, 1, stream) : launch_m1_group<float, kQ5_K>(&a, 1, stream);
 }
 
 hipError_t launch_gemv_q4k_fast(const GemvArgs& a, hipStream_t stream, bool* handled) {
@@ -754,11 +739,14 @@ hipError_t launch_gemv_q4k_fast(const GemvArgs& a, hipStream_t stream, bool* han
 bool gemv_q4k_group_supported(int m, int k) { return m == 1 && k % 4096 == 0 && k <= 4 * 4096; }
 
 hipError_t launch_gemv_q4k_group(const GemvArgs* a, int count, hipStream_t stream, int waves) {
+  if (a[0].type == kQ5_K)
+    return a[0].out_half ? launch_m1_group<_Float16, kQ5_K>(a, count, stream, waves)
+                         : launch_m1_group<float, kQ5_K>(a, count, stream, waves);
   return a[0].out_half ? launch_m1_group<_Float16>(a, count, stream, waves) : launch_m1_group<float>(a, count, stream, waves);
 }
 
 // M = 1 SwiGLU pairs: WAVES / 2 gate rows and the same up rows per workgroup.
-template <int WAVES, typename OutT>
+template <int WAVES, typename OutT, int TYPE>
 static hipError_t launch_m1_swiglu(const GemvArgs& a, const void* w_up, hipStream_t stream) {
   GemvGroup<OutT> g{};
   g.w[0] = static_cast<const uint8_t*>(a.w);
@@ -769,20 +757,20 @@ static hipError_t launch_m1_swiglu(const GemvArgs& a, const void* w_up, hipStrea
   const _Float16* x = static_cast<const _Float16*>(a.x);
   const dim3 grid(g.blocks[0]), block(WAVES * 64);
   switch (a.k / 4096) {
-    case 1: hipLaunchKernelGGL((gemv_q4k_m1<1, WAVES, 2, OutT, true>), grid, block, 0, stream, x, g); break;
-    case 2: hipLaunchKernelGGL((gemv_q4k_m1<2, WAVES, 2, OutT, true>), grid, block, 0, stream, x, g); break;
-    case 3: hipLaunchKernelGGL((gemv_q4k_m1<3, WAVES, 2, OutT, true>), grid, block, 0, stream, x, g); break;
-    case 4: hipLaunchKernelGGL((gemv_q4k_m1<4, WAVES, 2, OutT, true>), grid, block, 0, stream, x, g); break;
+    case 1: hipLaunchKernelGGL((gemv_q4k_m1<1, WAVES, 2, OutT, true, TYPE>), grid, block, 0, stream, x, g); break;
+    case 2: hipLaunchKernelGGL((gemv_q4k_m1<2, WAVES, 2, OutT, true, TYPE>), grid, block, 0, stream, x, g); break;
+    case 3: hipLaunchKernelGGL((gemv_q4k_m1<3, WAVES, 2, OutT, true, TYPE>), grid, block, 0, stream, x, g); break;
+    case 4: hipLaunchKernelGGL((gemv_q4k_m1<4, WAVES, 2, OutT, true, TYPE>), grid, block, 0, stream, x, g); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-template <typename OutT>
+template <typename OutT, int TYPE>
 static hipError_t launch_m1_swiglu_waves(const GemvArgs& a, const void* w_up, hipStream_t stream, int waves) {
   switch (waves > 0 ? waves : 8) {
-    case 8: return launch_m1_swiglu<8, OutT>(a, w_up, stream);
-    case 16: return launch_m1_swiglu<16, OutT>(a, w_up, stream);
+    case 8: return launch_m1_swiglu<8, OutT, TYPE>(a, w_up, stream);
+    case 16: return launch_m1_swiglu<16, OutT, TYPE>(a, w_up, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -791,8 +779,11 @@ hipError_t launch_gemv_q4k_swiglu_fast(const GemvArgs& a, const void* w_up, hipS
                                        int waves) {
   *handled = gemv_q4k_group_supported(a.m, a.k);
   if (!*handled) return hipSuccess;
-  return a.out_half ? launch_m1_swiglu_waves<_Float16>(a, w_up, stream, waves)
-                    : launch_m1_swiglu_waves<float>(a, w_up, stream, waves);
+  if (a.type == kQ5_K)
+    return a.out_half ? launch_m1_swiglu_waves<_Float16, kQ5_K>(a, w_up, stream, waves)
+                      : launch_m1_swiglu_waves<float, kQ5_K>(a, w_up, stream, waves);
+  return a.out_half ? launch_m1_swiglu_waves<_Float16, kQ4_K>(a, w_up, stream, waves)
+                    : launch_m1_swiglu_waves<float, kQ4_K>(a, w_up, stream, waves);
 }
 
 }  // namespace tensor_gguf

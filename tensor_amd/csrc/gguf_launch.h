@@ -43,14 +43,14 @@ hipError_t launch_gemv(const GemvArgs& args, hipStream_t stream);
 // Q4_K fast paths (LDS dot2 kernel for M = 1, MFMA kernel for M >= 2); sets
 // *handled to false when the shape is not covered by them.
 hipError_t launch_gemv_q4k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
-// Grouped M = 1 Q4_K GEMV: `count` (<= kGemvGroupMax) matrices sharing x and K in one launch.
+// Grouped M = 1 Q4_K (or Q5_K) GEMV: `count` (<= kGemvGroupMax) matrices sharing x and K in one launch.
 bool gemv_q4k_group_supported(int m, int k);
 // waves: rows (one per wave) per workgroup; 0 takes the default, 4 / 8 / 16 fix it (for sweeps)
 hipError_t launch_gemv_q4k_group(const GemvArgs* args, int count, hipStream_t stream, int waves = 0);
 // Decode GEMV with the SwiGLU epilogue of an MLP: out = silu(x W_gate^T) * (x W_up^T),
 // args.w the gate matrix, w_up the up matrix of the same shape and encoding.
 hipError_t launch_gemv_swiglu(const GemvArgs& gate, const void* w_up, hipStream_t stream);
-// Its Q4_K M = 1 path (gate and up rows of one workgroup); waves: 8 or 16 per workgroup, 0 the default.
+// Its Q4_K / Q5_K M = 1 path (gate and up rows of one workgroup); waves: 8 or 16 per workgroup, 0 the default.
 hipError_t launch_gemv_q4k_swiglu_fast(const GemvArgs& gate, const void* w_up, hipStream_t stream, bool* handled,
                                        int waves = 0);
 // Q5_K fast path (the M = 1 Q4_K kernel with the fifth bits; K a multiple of 4096, at most 16384).

@@ -201,7 +201,8 @@ int32_t group_call(const TensorCallV1* call, TensorErrorV1* error) {
   if (int32_t s = check_device(call, error)) return s;
   hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
   hipError_t status = hipSuccess;
-  if (args[0].type == (int)TENSOR_GGML_Q4_K && tensor_gguf::gemv_q4k_group_supported((int)m, (int)k)) {
+  if ((args[0].type == (int)TENSOR_GGML_Q4_K || args[0].type == (int)TENSOR_GGML_Q5_K) &&
+      tensor_gguf::gemv_q4k_group_supported((int)m, (int)k)) {
     status = tensor_gguf::launch_gemv_q4k_group(args, count, stream);
   } else {
     // no grouped kernel for this shape or encoding: one launch per matrix, same stream order

@@ -182,6 +182,7 @@ def test_gemv_q4k_multirow_configurations(hip_device, m, n, k):
     ("q6_k", 1, 4096),    # no grouped kernel: one launch per matrix
     ("q8_0", 2, 2560),
     ("q5_k", 1, 2048),
+    ("q5_k", 1, 4096),    # the grouped M = 1 kernel with the fifth bits
 ])
 @pytest.mark.parametrize("count", [1, 2, 3])
 def test_gemv_group_parity(hip_device, encoding, m, k, count):
@@ -251,6 +252,7 @@ def run_swiglu(device, encoding, x, gate, up, out_dtype):
     ("q8_0", 2, 100, 2560),
     ("q4_0", 8, 65, 1024),
     ("q5_k", 1, 300, 2048),
+    ("q5_k", 1, 1003, 8192),    # Q5_K through the fused M = 1 kernel
     ("q3_k", 3, 77, 512),
     ("q2_k", 1, 64, 4096),
     ("q4_1", 2, 100, 1024),

@@ -518,6 +518,8 @@ def run_details(device, x4096, log, only=None):
         layer.release()
 
     gemm_case("C4_q4k_gemm_m512_12288x4096", "q4_k", 512, 12288, 4096)
+    for encoding in ("q5_k", "q8_0", "q4_0"):
+        gemm_case(f"enc_{encoding}_gemm_m512_12288x4096", encoding, 512, 12288, 4096)
     gemm_case("C4_q4k_gemm_m2048_12288x4096", "q4_k", 2048, 12288, 4096, launches=4)
 
     # C5: q, k, v, o, gate, up (Q4_K) and down (Q6_K) chained on one stream

@@ -60,6 +60,13 @@ struct Geometry<kQ4_K, TPR> {
   static constexpr int W0 = QB / 4, W1 = 4;  // dwords: quants, header
 };
 
+// Q5_K: Q4_K's slices plus the fifth-bit bytes at the same positions of the 32-byte qh run.
+template <int TPR>
+struct Geometry<kQ5_K, TPR> {
+  static constexpr int QB = 32 / TPR;
+  static constexpr int W0 = QB / 4, W1 = 4 + QB / 4;  // dwords: quants; header, then fifth bits
+};
+
 // Q6_K: TPR threads per weight row, each EPT = 64 / TPR consecutive elements.
 template <int TPR>
 struct Geometry<kQ6_K, TPR> {
@@ -96,7 +103,8 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const _Float16* _
   static_assert(XL * THREADS == BM * 8 && TPR * BN == THREADS && (TPR == 1 || TPR == 2 || TPR == 4), "tile shape");
   using G = Geometry<TYPE, TPR>;
   using RawT = Raw<XL, G::W0, G::W1>;
-  constexpr int BYTES = TYPE == kQ4_K ? 144 : 210;
+  constexpr int BYTES = Block<TYPE>::BYTES;
+  constexpr bool KQ = TYPE == kQ4_K || TYPE == kQ5_K;  // Q4_K's header and nibble layout
   constexpr int STAGE = 2 * (BM + BN) * ROW;  // halves of one group's double-buffered tiles
   __shared__ __attribute__((aligned(16))) _Float16 stage[KS * STAGE];
   // wave-uniform (THREADS is a multiple of 64): keeps the step counter and the
@@ -125,12 +133,16 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const _Float16* _
       r.x[4 * i] = v.x; r.x[4 * i + 1] = v.y; r.x[4 * i + 2] = v.z; r.x[4 * i + 3] = v.w;
     }
     const uint8_t* blk = wbase + (size_t)(k0 >> 8) * BYTES;
-    if constexpr (TYPE == kQ4_K) {
+    if constexpr (KQ) {
       const uint4 hd = load16(blk);
       r.b[0] = hd.x; r.b[1] = hd.y; r.b[2] = hd.z; r.b[3] = hd.w;
-      const uint8_t* q = blk + 16 + 32 * (step & 3) + G::QB * wpart;
+      const uint8_t* q = blk + (TYPE == kQ5_K ? 48 : 16) + 32 * (step & 3) + G::QB * wpart;
 #pragma unroll
       for (int i = 0; i < G::W0; ++i) r.a[i] = load4(q + 4 * i);
+      if constexpr (TYPE == kQ5_K) {
+#pragma unroll
+        for (int i = 0; i < G::W0; ++i) r.b[4 + i] = load4(blk + 16 + G::QB * wpart + 4 * i);
+      }
     } else {
       const int h = (step & 3) >> 1, e0 = G::EPT * wpart;  // element offset inside the step
       const int quarter = 2 * (step & 1) + (e0 >> 5), l0 = e0 & 31;
@@ -152,7 +164,7 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const _Float16* _
       const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
       *reinterpret_cast<uint4*>(&xs[row * ROW + c8]) = make_uint4(r.x[4 * i], r.x[4 * i + 1], r.x[4 * i + 2], r.x[4 * i + 3]);
     }
-    if constexpr (TYPE == kQ4_K) {
+    if constexpr (KQ) {
       int sc_lo, mn_lo, sc_hi, mn_hi;
       q4k_scale_pair(r.b[1], r.b[2], r.b[3], step & 3, sc_lo, mn_lo, sc_hi, mn_hi);
       const float d = half_bits_to_float(r.b[0]), dmin = half_bits_to_float(r.b[0] >> 16);
@@ -163,9 +175,18 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const _Float16* _
 #pragma unroll
       for (int i = 0; i < G::W0; ++i) {
         const uint32_t q = r.a[i];  // low nibbles: sub-block 2j, high nibbles: 2j+1
-        *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(q & 0x000F000Fu, (q >> 8) & 0x000F000Fu, ds_lo, dm_lo);
-        *reinterpret_cast<uint2*>(dst + 32 + 4 * i) =
-            affine4((q >> 4) & 0x000F000Fu, (q >> 12) & 0x000F000Fu, ds_hi, dm_hi);
+        uint32_t lo02 = q & 0x000F000Fu, lo13 = (q >> 8) & 0x000F000Fu;
+        uint32_t hi02 = (q >> 4) & 0x000F000Fu, hi13 = (q >> 12) & 0x000F000Fu;
+        if constexpr (TYPE == kQ5_K) {
+          // fifth bits: bit 2j (sub-block 2j) and 2j+1 of the qh byte at the quant byte's position
+          const uint32_t h = r.b[4 + i] >> (2 * (step & 3));
+          lo02 |= (h & 0x00010001u) << 4;
+          lo13 |= ((h >> 8) & 0x00010001u) << 4;
+          hi02 |= ((h >> 1) & 0x00010001u) << 4;
+          hi13 |= ((h >> 9) & 0x00010001u) << 4;
+        }
+        *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(lo02, lo13, ds_lo, dm_lo);
+        *reinterpret_cast<uint2*>(dst + 32 + 4 * i) = affine4(hi02, hi13, ds_hi, dm_hi);
       }
     } else {
       const int e0 = G::EPT * wpart;
@@ -331,6 +352,7 @@ static hipError_t launch_config(const GemvArgs& a, hipStream_t stream, int confi
 
 hipError_t launch_gemm_pipe_config(const GemvArgs& a, hipStream_t stream, int config) {
   if (a.type == kQ4_K) return a.out_half ? launch_config<kQ4_K, _Float16>(a, stream, config) : launch_config<kQ4_K, float>(a, stream, config);
+  if (a.type == kQ5_K) return a.out_half ? launch_config<kQ5_K, _Float16>(a, stream, config) : launch_config<kQ5_K, float>(a, stream, config);
   if (a.type == kQ6_K) return a.out_half ? launch_config<kQ6_K, _Float16>(a, stream, config) : launch_config<kQ6_K, float>(a, stream, config);
   return hipErrorInvalidValue;
 }
@@ -338,6 +360,7 @@ hipError_t launch_gemm_pipe_config(const GemvArgs& a, hipStream_t stream, int co
 hipError_t launch_gemm_pipe(const GemvArgs& a, hipStream_t stream, bool* handled) {
   *handled = true;
   if (a.type == kQ4_K) return a.out_half ? launch_type<kQ4_K, _Float16>(a, stream) : launch_type<kQ4_K, float>(a, stream);
+  if (a.type == kQ5_K) return a.out_half ? launch_type<kQ5_K, _Float16>(a, stream) : launch_type<kQ5_K, float>(a, stream);
   if (a.type == kQ6_K) return a.out_half ? launch_type<kQ6_K, _Float16>(a, stream) : launch_type<kQ6_K, float>(a, stream);
   *handled = false;
   return hipSuccess;

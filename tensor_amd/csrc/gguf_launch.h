@@ -59,7 +59,7 @@ hipError_t launch_gemv_q5k_fast(const GemvArgs& args, hipStream_t stream, bool* 
 hipError_t launch_gemv_q6k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 hipError_t launch_dequant(const DequantArgs& args, hipStream_t stream);
 hipError_t launch_gemm(const GemvArgs& args, hipStream_t stream);
-// Pipelined dequant-GEMM for Q4_K and Q6_K (K a multiple of 256); sets
+// Pipelined dequant-GEMM for Q4_K, Q5_K and Q6_K (K a multiple of 256); sets
 // *handled to false for the encodings it does not cover.
 hipError_t launch_gemm_pipe(const GemvArgs& args, hipStream_t stream, bool* handled);
 // One tile configuration of the pipelined GEMM by index (tile sweeps and tests).

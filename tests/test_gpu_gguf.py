@@ -354,7 +354,7 @@ def test_gemm_parity_baseline_shapes(hip_device, c_oracle, encoding, m, n, k):
     assert R.relative_l2(got, expected) <= TOLERANCE
 
 
-@pytest.mark.parametrize("encoding", ["q4_k", "q6_k"])
+@pytest.mark.parametrize("encoding", ["q4_k", "q5_k", "q6_k"])
 @pytest.mark.parametrize("m,n,k", [
     (384, 7168, 512),    # 128x128 tile, K split over 2 wave groups
     (520, 4096, 512),    # 128x128, K split 2, ragged M
@@ -376,7 +376,7 @@ def test_gemm_tile_configurations(hip_device, c_oracle, encoding, m, n, k):
     assert R.relative_l2(got, expected) <= 1e-5
 
 
-@pytest.mark.parametrize("encoding", ["q4_k", "q6_k"])
+@pytest.mark.parametrize("encoding", ["q4_k", "q5_k", "q6_k"])
 @pytest.mark.parametrize("k,n", [
     (512, 10240),   # 256x128 tile
     (1024, 2560),   # 128x128, K split 2
@@ -445,8 +445,8 @@ def tie_blocks(encoding, n, k):
 
 @pytest.mark.parametrize("encoding", ["q4_k", "q5_k"])
 def test_fp16_weights_are_the_cast_of_the_fp32_dequantization(hip_device, c_oracle, encoding):
-    """Dequantizer fp16 output and the weights the GEMMs stage in fp16 (the pipelined Q4_K
-    kernel, the generic kernel for Q5_K) round the fp32 value, not the exact value."""
+    """Dequantizer fp16 output and the weights the pipelined GEMM stages in fp16 (Q4_K and
+    Q5_K) round the fp32 value, not the exact value."""
     code = Q.ggml_type(encoding)
     n, k = 256, 512
     note("fp16-tie", encoding)

@@ -497,6 +497,8 @@ def run_details(device, x4096, log, only=None):
         down.release()
         fused.release()
 
+    # C1's shape (the reference runs it on its CPU provider) on the GPU
+    gemv_case("C1_q8_0_gemv_m1_4096x4096", "q8_0", 1, 4096, 4096, "float16")
     for m in (1, 4, 8):
         gemv_case(f"C2_q4k_gemv_m{m}_12288x4096", "q4_k", m, 12288, 4096, "float16")
         gemv_case(f"C2_q4k_gemv_m{m}_4096x12288", "q4_k", m, 4096, 12288, "float16")

@@ -248,7 +248,11 @@ __global__ __launch_bounds__(256) void gemv_q6k(const _Float16* __restrict__ x,
 
 // ------------------------------------------------------------ Q8_0, Q4_0 ---
 // Lane plan: one 32-element block per lane, 64 blocks per step.
-template <int TYPE, int M, int R, typename OutT, bool SWIGLU = false>
+//
+// XLDS = true stages x (M * K halves, dynamic LDS) once per workgroup behind one barrier and
+// reads the per-block activations from LDS: read from global memory, each lane's 64 bytes
+// of x per 18 or 34 weight bytes made the L1 path, not HBM, the limit.
+template <int TYPE, int M, int R, typename OutT, bool SWIGLU = false, bool XLDS = false>
 __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
                                                 const uint8_t* __restrict__ w,
                                                 OutT* __restrict__ out, int n_rows, int k,
@@ -257,6 +261,13 @@ __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
   // bias removed per block: 1024 from the fp16 widening, plus 128 for the
   // sign flip of Q8_0 codes or 8 for the Q4_0 code offset
   constexpr float kBias = TYPE == kQ8_0 ? 1152.0f : 1032.0f;
+  extern __shared__ __attribute__((aligned(16))) uint8_t xl[];
+  if constexpr (XLDS) {
+    const int chunks = M * k / 8;
+    for (int c = threadIdx.x; c < chunks; c += 256)
+      *reinterpret_cast<uint4*>(xl + 16 * c) = load16(reinterpret_cast<const uint8_t*>(x) + 16 * (size_t)c);
+    __syncthreads();
+  }
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (SWIGLU ? 1 : R);
   if (row0 >= n_rows) return;
@@ -269,14 +280,21 @@ __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
 
+#pragma unroll 2
   for (int b = lane; b < blocks; b += 64) {
     uint4 xs[M][4];
     float sx[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const uint8_t* xp = reinterpret_cast<const uint8_t*>(x + (size_t)m * k + b * 32);
+      if constexpr (XLDS) {
+        const uint4* xp = reinterpret_cast<const uint4*>(xl + 2 * ((size_t)m * k + b * 32));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) xs[m][i] = load16(xp + 16 * i);
+        for (int i = 0; i < 4; ++i) xs[m][i] = xp[i];
+      } else {
+        const uint8_t* xp = reinterpret_cast<const uint8_t*>(x + (size_t)m * k + b * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xs[m][i] = load16(xp + 16 * i);
+      }
     }
     uint32_t head[R];
     uint4 q0[R], q1[R];
@@ -284,7 +302,7 @@ __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
     for (int r = 0; r < R; ++r) {
       if (r < rows) {
         const uint8_t* block = pair_row<SWIGLU>(w, w2, row0, r, row_bytes) + (size_t)b * kBytes;
-        head[r] = (uint32_t)block[0] | ((uint32_t)block[1] << 8);
+        head[r] = load4(block);  // fp16 d in the low half
         q0[r] = load16(block + 2);
         if (TYPE == kQ8_0) q1[r] = load16(block + 18);
       }
@@ -424,6 +442,11 @@ static hipError_t launch_m(const GemvArgs& a, hipStream_t stream) {
   constexpr int R = M <= 2 ? 4 : (M <= 4 ? 2 : 1);
   const int waves = (a.n + R - 1) / R;
   const dim3 grid((waves + 3) / 4), block(256);
+  // Q8_0 / Q4_0: x in LDS when it takes at most 64 KB, shared by the workgroup's waves, and one
+  // row per wave (rows per wave only served the reuse of x loaded from global memory)
+  const size_t xbytes = (size_t)M * a.k * 2;
+  const bool xlds = xbytes <= 64 * 1024;
+  const dim3 grid1((a.n + 3) / 4);
   switch (a.type) {
     case kQ4_K:
       hipLaunchKernelGGL((gemv_q4k<M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
@@ -432,10 +455,12 @@ static hipError_t launch_m(const GemvArgs& a, hipStream_t stream) {
       hipLaunchKernelGGL((gemv_q6k<M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
       break;
     case kQ8_0:
-      hipLaunchKernelGGL((gemv_q32<kQ8_0, M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
+      if (xlds) hipLaunchKernelGGL((gemv_q32<kQ8_0, M, 1, OutT, false, true>), grid1, block, xbytes, stream, x, w, out, a.n, a.k);
+      else hipLaunchKernelGGL((gemv_q32<kQ8_0, M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
       break;
     case kQ4_0:
-      hipLaunchKernelGGL((gemv_q32<kQ4_0, M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
+      if (xlds) hipLaunchKernelGGL((gemv_q32<kQ4_0, M, 1, OutT, false, true>), grid1, block, xbytes, stream, x, w, out, a.n, a.k);
+      else hipLaunchKernelGGL((gemv_q32<kQ4_0, M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
       break;
     default:
       if (!launch_blocks<M, OutT, false>(a, nullptr, stream)) return hipErrorInvalidValue;

@@ -499,6 +499,8 @@ def run_details(device, x4096, log, only=None):
 
     # C1's shape (the reference runs it on its CPU provider) on the GPU
     gemv_case("C1_q8_0_gemv_m1_4096x4096", "q8_0", 1, 4096, 4096, "float16")
+    # C5's Q6_K down projection on its own
+    gemv_case("C5_q6k_gemv_m1_4096x12288", "q6_k", 1, 4096, 12288, "float16")
     for m in (1, 4, 8):
         gemv_case(f"C2_q4k_gemv_m{m}_12288x4096", "q4_k", m, 12288, 4096, "float16")
         gemv_case(f"C2_q4k_gemv_m{m}_4096x12288", "q4_k", m, 4096, 12288, "float16")

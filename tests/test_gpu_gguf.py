@@ -108,6 +108,7 @@ def test_gemv_parity_small(hip_device, encoding, m, k):
     ("q4_k", 4096, 12288, 8, "float16"),
     ("q6_k", 151936, 4096, 1, "float32"),  # C3 LM head, fp32 logits
     ("q6_k", 4096, 12288, 1, "float16"),   # C5 down (Q6_K)
+    ("q6_k", 1001, 12288, 1, "float32"),   # three steps per row, ragged last workgroup
     ("q8_0", 4096, 4096, 1, "float16"),    # C1 shape
     ("q5_k", 12288, 4096, 1, "float16"),   # Q5_K through the M = 1 kernel (16 rows per workgroup)
     ("q5_k", 4096, 12288, 1, "float32"),   # three 4096-column steps, 8 rows per workgroup

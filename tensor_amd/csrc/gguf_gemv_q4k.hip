@@ -340,9 +340,13 @@ __device__ __forceinline__ void pair_codes(const uint4& hd, int j, uint32_t& scs
   }
 }
 
-template <int M, typename OutT>
+// SWIGLU = true: the workgroup's two tile slots are tile blockIdx.x of the gate matrix (w) and
+// the same tile of the up matrix (w2); the wave that sums the gate tile also sums the up tile's
+// partials and stores silu(gate) * up.
+template <int M, typename OutT, bool SWIGLU = false>
 __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict__ x, const uint8_t* __restrict__ w,
-                                                     OutT* __restrict__ out, int n_rows, int k, int tiles) {
+                                                     OutT* __restrict__ out, int n_rows, int k, int tiles,
+                                                     const uint8_t* __restrict__ w2 = nullptr) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int XCH = 8;  // x chunks per thread (the host checks M * K / 8 <= XCH * threads)
   const int KW = k >> 10;
@@ -361,8 +365,8 @@ __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict_
     const int c = threadIdx.x + i * (int)blockDim.x;
     if (c < chunks) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * (size_t)c);
   }
-  const int tile = blockIdx.x * tiles + t;
-  const uint8_t* base = w + (size_t)min(tile * 16 + n, n_rows - 1) * row_bytes + q * 576 + 16 * g;
+  const int tile = SWIGLU ? (int)blockIdx.x : blockIdx.x * tiles + t;
+  const uint8_t* base = (SWIGLU && t == 1 ? w2 : w) + (size_t)min(tile * 16 + n, n_rows - 1) * row_bytes + q * 576 + 16 * g;
   uint4 v[9];
 #pragma unroll
   for (int c = 0; c < kSecEarlyLoads; ++c) v[c] = load16(base + 64 * c);
@@ -448,10 +452,16 @@ __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict_
   float4v_t* partial = reinterpret_cast<float4v_t*>(lds);
   partial[wv * 64 + lane] = total;
   __syncthreads();
-  if (q != 0 || tile * 16 >= n_rows) return;
+  if (q != 0 || tile * 16 >= n_rows || (SWIGLU && t != 0)) return;
   // wave (t, 0) sums its tile's K ranges in order and stores it
   float4v_t sum = partial[t * KW * 64 + lane];
   for (int p = 1; p < KW; ++p) sum += partial[(t * KW + p) * 64 + lane];
+  if constexpr (SWIGLU) {
+    float4v_t up = partial[KW * 64 + lane];
+    for (int p = 1; p < KW; ++p) up += partial[(KW + p) * 64 + lane];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sum[i] = swiglu(sum[i], up[i]);
+  }
   const int col = tile * 16 + n;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -698,6 +708,36 @@ static hipError_t launch_sec(const GemvArgs& a, hipStream_t stream, bool* handle
   return hipGetLastError();
 }
 
+// SwiGLU pairs at 2 <= M <= 8 on the sector-aligned kernel: one gate tile and the same up tile
+// per workgroup (2 x K/1024 waves, so K <= 8192), x in LDS.
+template <int M, typename OutT>
+static hipError_t launch_sec_swiglu(const GemvArgs& a, const void* w_up, hipStream_t stream, bool* handled) {
+  *handled = false;
+  const int kw = a.k / 1024, tiles = (a.n + 15) / 16, threads = 2 * kw * 64;
+  if (a.k % 1024 != 0 || kw > 8) return hipSuccess;
+  const size_t lds = std::max(sec_lds_bytes(M, a.k), (size_t)threads * sizeof(float4v_t));
+  if ((long)M * a.k / 8 > 8L * threads || lds > kSecMaxLds) return hipSuccess;
+  *handled = true;
+  hipLaunchKernelGGL((gemv_q4k_sec<M, OutT, true>), dim3(tiles), dim3(threads), lds, stream,
+                     static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out),
+                     a.n, a.k, 2, static_cast<const uint8_t*>(w_up));
+  return hipGetLastError();
+}
+
+template <typename OutT>
+static hipError_t launch_swiglu_multirow(const GemvArgs& a, const void* w_up, hipStream_t stream, bool* handled) {
+  switch (a.m) {
+    case 2: return launch_sec_swiglu<2, OutT>(a, w_up, stream, handled);
+    case 3: return launch_sec_swiglu<3, OutT>(a, w_up, stream, handled);
+    case 4: return launch_sec_swiglu<4, OutT>(a, w_up, stream, handled);
+    case 5: return launch_sec_swiglu<5, OutT>(a, w_up, stream, handled);
+    case 6: return launch_sec_swiglu<6, OutT>(a, w_up, stream, handled);
+    case 7: return launch_sec_swiglu<7, OutT>(a, w_up, stream, handled);
+    case 8: return launch_sec_swiglu<8, OutT>(a, w_up, stream, handled);
+    default: *handled = false; return hipSuccess;
+  }
+}
+
 // 2 <= M <= 8: the sector-aligned kernel, else the LDS multi-tile kernel, else one super-block per step.
 template <int M, typename OutT>
 static hipError_t launch_multirow(const GemvArgs& a, hipStream_t stream) {
@@ -777,6 +817,9 @@ static hipError_t launch_m1_swiglu_waves(const GemvArgs& a, const void* w_up, hi
 
 hipError_t launch_gemv_q4k_swiglu_fast(const GemvArgs& a, const void* w_up, hipStream_t stream, bool* handled,
                                        int waves) {
+  if (a.type == kQ4_K && a.m >= 2)
+    return a.out_half ? launch_swiglu_multirow<_Float16>(a, w_up, stream, handled)
+                      : launch_swiglu_multirow<float>(a, w_up, stream, handled);
   *handled = gemv_q4k_group_supported(a.m, a.k);
   if (!*handled) return hipSuccess;
   if (a.type == kQ5_K)

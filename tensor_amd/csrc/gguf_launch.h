@@ -50,7 +50,8 @@ hipError_t launch_gemv_q4k_group(const GemvArgs* args, int count, hipStream_t st
 // Decode GEMV with the SwiGLU epilogue of an MLP: out = silu(x W_gate^T) * (x W_up^T),
 // args.w the gate matrix, w_up the up matrix of the same shape and encoding.
 hipError_t launch_gemv_swiglu(const GemvArgs& gate, const void* w_up, hipStream_t stream);
-// Its Q4_K / Q5_K M = 1 path (gate and up rows of one workgroup); waves: 8 or 16 per workgroup, 0 the default.
+// Its fast paths: Q4_K / Q5_K at M = 1 (gate and up rows of one workgroup; waves: 8 or 16 per
+// workgroup, 0 the default) and Q4_K at 2 <= M <= 8 (a gate tile and its up tile per workgroup).
 hipError_t launch_gemv_q4k_swiglu_fast(const GemvArgs& gate, const void* w_up, hipStream_t stream, bool* handled,
                                        int waves = 0);
 // Q5_K fast path (the M = 1 Q4_K kernel with the fifth bits; K a multiple of 4096, at most 16384).

@@ -247,7 +247,11 @@ def run_swiglu(device, encoding, x, gate, up, out_dtype):
     ("q4_k", 1, 12288, 4096),   # C2 gate / up: the fused M = 1 kernel
     ("q4_k", 1, 1003, 8192),    # fused kernel, two column steps, ragged last workgroup
     ("q4_k", 1, 301, 2560),     # K not a multiple of 4096: generic gate / up pairs
-    ("q4_k", 4, 301, 4096),     # M > 1: generic pairs
+    ("q4_k", 4, 301, 4096),     # M > 1: a gate tile and its up tile per workgroup (sector-aligned kernel)
+    ("q4_k", 8, 12288, 4096),   # C2 gate / up at M = 8
+    ("q4_k", 2, 1003, 8192),    # sixteen waves per workgroup, ragged last tile
+    ("q4_k", 5, 77, 3072),      # three K ranges per tile
+    ("q4_k", 3, 100, 2560),     # K not a multiple of 1024: generic pairs
     ("q6_k", 1, 300, 4096),
     ("q6_k", 3, 77, 512),
     ("q8_0", 2, 100, 2560),

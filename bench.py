@@ -501,7 +501,19 @@ def run_details(device, x4096, log, only=None):
     gemv_case("C1_q8_0_gemv_m1_4096x4096", "q8_0", 1, 4096, 4096, "float16")
     # C5's Q6_K down projection on its own
     gemv_case("C5_q6k_gemv_m1_4096x12288", "q6_k", 1, 4096, 12288, "float16")
-    # the SwiGLU pair at M = 4 and 8 (generic gate / up row pairs)
+    # gate + up as one grouped launch at M = 4 and 8
+    for m in (4, 8):
+        name = f"C2_q4k_gemv_group_m{m}_2x12288x4096"
+        if wanted(name):
+            copies = copies_for(2 * weight_bytes("q4_k", 12288, 4096))
+            group = GroupLinear(device, "q4_k", m, [(12288, 4096), (12288, 4096)], "float16", copies, 70 + m)
+            seconds = time_launches(device, [group.calls[i % copies].launch for i in range(60)]) / 60
+            gbs = group.bytes / seconds / 1e9
+            details[name] = {"us": round(seconds * 1e6, 3), "GB/s": round(gbs, 1),
+                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
+            log(name, details[name])
+            group.release()
+    # the SwiGLU pair at M = 4 and 8
     for m in (4, 8):
         name = f"C2_q4k_gemv_swiglu_m{m}_12288x4096"
         if wanted(name):

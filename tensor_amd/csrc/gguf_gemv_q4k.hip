@@ -340,13 +340,16 @@ __device__ __forceinline__ void pair_codes(const uint4& hd, int j, uint32_t& scs
   }
 }
 
-// SWIGLU = true: the workgroup's two tile slots are tile blockIdx.x of the gate matrix (w) and
-// the same tile of the up matrix (w2); the wave that sums the gate tile also sums the up tile's
-// partials and stores silu(gate) * up.
-template <int M, typename OutT, bool SWIGLU = false>
+// PAIR = 1 (SwiGLU) or 2 (two outputs): the workgroup's two tile slots are tile blockIdx.x of w
+// and the same tile of w2, a second matrix of the same shape. PAIR = 1: the wave that sums the w
+// (gate) tile also sums the w2 (up) tile's partials and stores silu(gate) * up to out. PAIR = 2:
+// each tile is stored, to out and out2 (the grouped GEMV of two equal matrices in one launch).
+template <int M, typename OutT, int PAIR = 0>
 __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict__ x, const uint8_t* __restrict__ w,
                                                      OutT* __restrict__ out, int n_rows, int k, int tiles,
-                                                     const uint8_t* __restrict__ w2 = nullptr) {
+                                                     const uint8_t* __restrict__ w2 = nullptr,
+                                                     OutT* __restrict__ out2 = nullptr) {
+  constexpr bool SWIGLU = PAIR == 1;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int XCH = 8;  // x chunks per thread (the host checks M * K / 8 <= XCH * threads)
   const int KW = k >> 10;
@@ -365,8 +368,8 @@ __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict_
     const int c = threadIdx.x + i * (int)blockDim.x;
     if (c < chunks) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * (size_t)c);
   }
-  const int tile = SWIGLU ? (int)blockIdx.x : blockIdx.x * tiles + t;
-  const uint8_t* base = (SWIGLU && t == 1 ? w2 : w) + (size_t)min(tile * 16 + n, n_rows - 1) * row_bytes + q * 576 + 16 * g;
+  const int tile = PAIR ? (int)blockIdx.x : blockIdx.x * tiles + t;
+  const uint8_t* base = (PAIR && t == 1 ? w2 : w) + (size_t)min(tile * 16 + n, n_rows - 1) * row_bytes + q * 576 + 16 * g;
   uint4 v[9];
 #pragma unroll
   for (int c = 0; c < kSecEarlyLoads; ++c) v[c] = load16(base + 64 * c);
@@ -462,11 +465,12 @@ __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict_
 #pragma unroll
     for (int i = 0; i < 4; ++i) sum[i] = swiglu(sum[i], up[i]);
   }
+  OutT* dst = PAIR == 2 && t == 1 ? out2 : out;
   const int col = tile * 16 + n;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = 4 * g + i;
-    if (m < M && col < n_rows) store_out<OutT>(out, (size_t)m * n_rows + col, sum[i]);
+    if (m < M && col < n_rows) store_out<OutT>(dst, (size_t)m * n_rows + col, sum[i]);
   }
 }
 
@@ -710,30 +714,31 @@ static hipError_t launch_sec(const GemvArgs& a, hipStream_t stream, bool* handle
 
 // SwiGLU pairs at 2 <= M <= 8 on the sector-aligned kernel: one gate tile and the same up tile
 // per workgroup (2 x K/1024 waves, so K <= 8192), x in LDS.
-template <int M, typename OutT>
-static hipError_t launch_sec_swiglu(const GemvArgs& a, const void* w_up, hipStream_t stream, bool* handled) {
+template <int M, typename OutT, int PAIR>
+static hipError_t launch_sec_pair(const GemvArgs& a, const void* w2, void* out2, hipStream_t stream, bool* handled) {
   *handled = false;
   const int kw = a.k / 1024, tiles = (a.n + 15) / 16, threads = 2 * kw * 64;
   if (a.k % 1024 != 0 || kw > 8) return hipSuccess;
   const size_t lds = std::max(sec_lds_bytes(M, a.k), (size_t)threads * sizeof(float4v_t));
   if ((long)M * a.k / 8 > 8L * threads || lds > kSecMaxLds) return hipSuccess;
   *handled = true;
-  hipLaunchKernelGGL((gemv_q4k_sec<M, OutT, true>), dim3(tiles), dim3(threads), lds, stream,
+  hipLaunchKernelGGL((gemv_q4k_sec<M, OutT, PAIR>), dim3(tiles), dim3(threads), lds, stream,
                      static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out),
-                     a.n, a.k, 2, static_cast<const uint8_t*>(w_up));
+                     a.n, a.k, 2, static_cast<const uint8_t*>(w2), static_cast<OutT*>(out2));
   return hipGetLastError();
 }
 
-template <typename OutT>
-static hipError_t launch_swiglu_multirow(const GemvArgs& a, const void* w_up, hipStream_t stream, bool* handled) {
+template <typename OutT, int PAIR>
+static hipError_t launch_pair_multirow(const GemvArgs& a, const void* w2, void* out2, hipStream_t stream,
+                                       bool* handled) {
   switch (a.m) {
-    case 2: return launch_sec_swiglu<2, OutT>(a, w_up, stream, handled);
-    case 3: return launch_sec_swiglu<3, OutT>(a, w_up, stream, handled);
-    case 4: return launch_sec_swiglu<4, OutT>(a, w_up, stream, handled);
-    case 5: return launch_sec_swiglu<5, OutT>(a, w_up, stream, handled);
-    case 6: return launch_sec_swiglu<6, OutT>(a, w_up, stream, handled);
-    case 7: return launch_sec_swiglu<7, OutT>(a, w_up, stream, handled);
-    case 8: return launch_sec_swiglu<8, OutT>(a, w_up, stream, handled);
+    case 2: return launch_sec_pair<2, OutT, PAIR>(a, w2, out2, stream, handled);
+    case 3: return launch_sec_pair<3, OutT, PAIR>(a, w2, out2, stream, handled);
+    case 4: return launch_sec_pair<4, OutT, PAIR>(a, w2, out2, stream, handled);
+    case 5: return launch_sec_pair<5, OutT, PAIR>(a, w2, out2, stream, handled);
+    case 6: return launch_sec_pair<6, OutT, PAIR>(a, w2, out2, stream, handled);
+    case 7: return launch_sec_pair<7, OutT, PAIR>(a, w2, out2, stream, handled);
+    case 8: return launch_sec_pair<8, OutT, PAIR>(a, w2, out2, stream, handled);
     default: *handled = false; return hipSuccess;
   }
 }
@@ -778,6 +783,18 @@ hipError_t launch_gemv_q4k_fast(const GemvArgs& a, hipStream_t stream, bool* han
 
 bool gemv_q4k_group_supported(int m, int k) { return m == 1 && k % 4096 == 0 && k <= 4 * 4096; }
 
+// Up to M = 4 (gate + up 2 x 12288 x 4096 at M = 4: 17.4 us against 21.4 us for two launches; at
+// M = 8 the 64 KB of x staged for two tiles per workgroup makes the pair slower, 24.6 against 23.1).
+bool gemv_q4k_pair_supported(const GemvArgs* a, int count) {
+  return count == 2 && a[0].type == kQ4_K && a[0].m >= 2 && a[0].m <= 4 && a[1].n == a[0].n &&
+         a[0].k % 1024 == 0 && a[0].k <= 8192;
+}
+
+hipError_t launch_gemv_q4k_pair(const GemvArgs* a, hipStream_t stream, bool* handled) {
+  return a[0].out_half ? launch_pair_multirow<_Float16, 2>(a[0], a[1].w, a[1].out, stream, handled)
+                       : launch_pair_multirow<float, 2>(a[0], a[1].w, a[1].out, stream, handled);
+}
+
 hipError_t launch_gemv_q4k_group(const GemvArgs* a, int count, hipStream_t stream, int waves) {
   if (a[0].type == kQ5_K)
     return a[0].out_half ? launch_m1_group<_Float16, kQ5_K>(a, count, stream, waves)
@@ -818,8 +835,8 @@ static hipError_t launch_m1_swiglu_waves(const GemvArgs& a, const void* w_up, hi
 hipError_t launch_gemv_q4k_swiglu_fast(const GemvArgs& a, const void* w_up, hipStream_t stream, bool* handled,
                                        int waves) {
   if (a.type == kQ4_K && a.m >= 2)
-    return a.out_half ? launch_swiglu_multirow<_Float16>(a, w_up, stream, handled)
-                      : launch_swiglu_multirow<float>(a, w_up, stream, handled);
+    return a.out_half ? launch_pair_multirow<_Float16, 1>(a, w_up, nullptr, stream, handled)
+                      : launch_pair_multirow<float, 1>(a, w_up, nullptr, stream, handled);
   *handled = gemv_q4k_group_supported(a.m, a.k);
   if (!*handled) return hipSuccess;
   if (a.type == kQ5_K)

@@ -47,6 +47,11 @@ hipError_t launch_gemv_q4k_fast(const GemvArgs& args, hipStream_t stream, bool* 
 bool gemv_q4k_group_supported(int m, int k);
 // waves: rows (one per wave) per workgroup; 0 takes the default, 4 / 8 / 16 fix it (for sweeps)
 hipError_t launch_gemv_q4k_group(const GemvArgs* args, int count, hipStream_t stream, int waves = 0);
+// Two Q4_K matrices of one shape sharing x at 2 <= M <= 4 (K a multiple of 1024, at most 8192):
+// one launch of the sector-aligned kernel with a tile of each per workgroup; *handled is false
+// when x does not fit the kernel's LDS.
+bool gemv_q4k_pair_supported(const GemvArgs* args, int count);
+hipError_t launch_gemv_q4k_pair(const GemvArgs* args, hipStream_t stream, bool* handled);
 // Decode GEMV with the SwiGLU epilogue of an MLP: out = silu(x W_gate^T) * (x W_up^T),
 // args.w the gate matrix, w_up the up matrix of the same shape and encoding.
 hipError_t launch_gemv_swiglu(const GemvArgs& gate, const void* w_up, hipStream_t stream);

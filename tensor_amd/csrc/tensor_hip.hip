@@ -201,9 +201,13 @@ int32_t group_call(const TensorCallV1* call, TensorErrorV1* error) {
   if (int32_t s = check_device(call, error)) return s;
   hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
   hipError_t status = hipSuccess;
+  bool paired = false;
   if ((args[0].type == (int)TENSOR_GGML_Q4_K || args[0].type == (int)TENSOR_GGML_Q5_K) &&
       tensor_gguf::gemv_q4k_group_supported((int)m, (int)k)) {
     status = tensor_gguf::launch_gemv_q4k_group(args, count, stream);
+  } else if (tensor_gguf::gemv_q4k_pair_supported(args, count) &&
+             (status = tensor_gguf::launch_gemv_q4k_pair(args, stream, &paired), paired)) {
+    // two equal Q4_K matrices at M > 1: one launch of the multi-row kernel
   } else {
     // no grouped kernel for this shape or encoding: one launch per matrix, same stream order
     for (int i = 0; i < count && status == hipSuccess; ++i) status = tensor_gguf::launch_gemv(args[i], stream);

@@ -179,7 +179,7 @@ def test_gemv_q4k_multirow_configurations(hip_device, m, n, k):
 @pytest.mark.parametrize("encoding,m,k", [
     ("q4_k", 1, 4096),    # one launch of the grouped M = 1 kernel
     ("q4_k", 1, 12288),   # three 4096-column steps per row
-    ("q4_k", 4, 4096),    # M > 1: one launch per matrix
+    ("q4_k", 4, 4096),    # M > 1: two equal matrices in one multi-row launch, else one launch per matrix
     ("q6_k", 1, 4096),    # no grouped kernel: one launch per matrix
     ("q8_0", 2, 2560),
     ("q5_k", 1, 2048),
@@ -483,3 +483,28 @@ def test_generic_gemm_one_hot_rows_give_dequantized_weights(hip_device, c_oracle
     x[np.arange(k), perm] = 1.0
     got = run_linear(hip_device, "gguf_gemm", encoding, x, raw, "float32")
     assert np.array_equal(got, deq[:, perm].T), encoding
+
+
+@pytest.mark.parametrize("m,n,k", [(4, 1003, 4096), (8, 12288, 4096), (2, 300, 8192), (3, 200, 2560)])
+def test_gemv_group_pair_of_equal_matrices(hip_device, m, n, k):
+    """Two Q4_K matrices of one shape at 2 <= M <= 4 (gate and up) in one grouped launch: the
+    multi-row kernel with a tile of each per workgroup (M = 8 and K = 2560 take one launch per
+    matrix)."""
+    note("gemv-group-pair", m, n, k)
+    x = cases.activation(m, k, 200 + m)
+    raws = [cases.weight(n, k, "q4_k", 201 + i) for i in range(2)]
+    for out_dtype in ("float16", "float32"):
+        exe = hip_device.load("gguf_gemv_group", encoding="q4_k", out_dtype=out_dtype, count=2)
+        xb = hip_device.from_numpy(x)
+        wbs = [hip_device.from_numpy(r) for r in raws]
+        outs = [hip_device.empty((m, n), out_dtype) for _ in range(2)]
+        for out in outs:
+            hip_device.fill_bytes(out, 0xFF)
+        exe.launch(xb, wbs[0], outs[0], wbs[1], outs[1])
+        for raw, out in zip(raws, outs):
+            got = out.to_numpy()
+            assert not np.isnan(got).any(), out_dtype
+            err = R.relative_l2(got, R.gemv_reference(x, raw, Q.Q4_K, n, k))
+            assert err <= TOLERANCE, (m, n, k, out_dtype, err)
+        for b in [xb, *wbs, *outs]:
+            b.release()

@@ -355,10 +355,10 @@ __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
 }
 
 // ------------------------------------------------------ other encodings ---
-// Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K: each lane decodes 8-element groups with the
-// dequantizer's arithmetic (decode8) and accumulates their products with the
+// Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K: each lane decodes 16-element groups with the
+// dequantizer's arithmetic (decode8, twice) and accumulates their products with the
 // activations in fp32.  Consecutive lanes take consecutive groups, so one wave
-// pass covers 512 consecutive elements of its rows; the activation group is
+// pass covers 1024 consecutive elements of its rows; the activation group is
 // loaded once and reused for all R rows.
 template <int TYPE, int M, int R, typename OutT, bool SWIGLU = false>
 __global__ __launch_bounds__(256) void gemv_blocks(const _Float16* __restrict__ x,
@@ -377,30 +377,36 @@ __global__ __launch_bounds__(256) void gemv_blocks(const _Float16* __restrict__ 
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
 
-#pragma unroll 4
-  for (int g = lane; g < (k >> 3); g += 64) {
-    const int e = 8 * g;
-    float xv[M][8];
+  // 16 elements per lane and pass: one scale group of Q2_K / Q3_K, half a 32-element block
+  // (the two decode8 calls share the block's header loads)
+#pragma unroll 2
+  for (int g = lane; g < (k >> 4); g += 64) {
+    const int e = 16 * g;
+    float xv[M][16];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const uint4 raw = load16(reinterpret_cast<const uint8_t*>(x + (size_t)m * k + e));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const half2_t pair = as_half2(word(raw, i));
-        xv[m][2 * i] = (float)pair.x;
-        xv[m][2 * i + 1] = (float)pair.y;
+      for (int h = 0; h < 2; ++h) {
+        const uint4 raw = load16(reinterpret_cast<const uint8_t*>(x + (size_t)m * k + e + 8 * h));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const half2_t pair = as_half2(word(raw, i));
+          xv[m][8 * h + 2 * i] = (float)pair.x;
+          xv[m][8 * h + 2 * i + 1] = (float)pair.y;
+        }
       }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (r >= rows) break;
       const uint8_t* block = pair_row<SWIGLU>(w, w2, row0, r, row_bytes) + (size_t)(e / QK) * BYTES;
-      float v[8];
+      float v[16];
       decode8<TYPE>(block, e % QK, v);
+      decode8<TYPE>(block, e % QK + 8, v + 8);
 #pragma unroll
       for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[m][r] = fmaf(v[i], xv[m][i], acc[m][r]);
+        for (int i = 0; i < 16; ++i) acc[m][r] = fmaf(v[i], xv[m][i], acc[m][r]);
     }
   }
   store_rows<SWIGLU>(acc, out, n_rows, row0, rows, lane);

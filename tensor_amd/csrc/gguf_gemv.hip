@@ -378,8 +378,11 @@ __global__ __launch_bounds__(256) void gemv_blocks(const _Float16* __restrict__ 
     for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
 
   // 16 elements per lane and pass: one scale group of Q2_K / Q3_K, half a 32-element block
-  // (the two decode8 calls share the block's header loads)
-#pragma unroll 2
+  // (the two decode8 calls share the block's header loads).  Q3_K at M=1 is not unrolled: at
+  // 64 VGPRs it keeps 8 waves per SIMD (65 and 7 waves unrolled), 22.1 against 25.1 us at
+  // 12288x4096.
+  constexpr int UNROLL = (M == 1 && TYPE == kQ3_K) ? 1 : 2;
+#pragma unroll UNROLL
   for (int g = lane; g < (k >> 4); g += 64) {
     const int e = 16 * g;
     float xv[M][16];

@@ -6,25 +6,33 @@ shapes, M = 1.  One *step* is one decode MLP's linears through the C ABI: gate
 down [4096 x 12288].  ``value`` is the algorithmic bytes of all K steps
 (packed weights + fp16 x + fp16 out) divided by the timed region.
 
-Protocol (after benchmarks/kernels/showcase/benchmark.py:66-94): every launch
-is bound once (allocation-free BoundCall), the K steps are captured into one
-HIP graph, and the graph replay is timed with HIP events recorded on the
-launch stream.  Weights rotate through distinct copies (>= 3 x 256 MiB per
-rotation) so no launch finds its weights in the 256 MiB MALL.  Before the timed
-replays every sequence is replayed, untimed, for WARM_SECONDS: an MI355X that
-has idled through the host-side set-up of a case starts in deep sleep and needs
-~30 ms of sustained load to reach its steady clocks (measured on the LM head:
-123 us per launch over the first 100 launches, 93 us from the fourth hundred
-on), so shorter warm-ups time the clock ramp instead of the kernel.
+Timing protocol (after benchmarks/kernels/showcase/benchmark.py:66-94 and
+:1007-1013): every launch is bound once (allocation-free BoundCall), a case's
+launches are captured into one HIP graph, the graph is replayed REPLAYS (>= 11)
+times with HIP events recorded on the launch stream around each replay, and
+the case reports the median, min, max and every sample.  The detail cases run
+in a seeded shuffled order, kept in the output.  Weights rotate through
+distinct copies (>= 3 x 256 MiB per rotation) so no launch finds its weights in
+the 256 MiB MALL, except the showcase cases, which keep the reference's
+hot-cache protocol (one weight copy, N = K = 1024).  Before the timed replays
+every sequence is replayed, untimed, for WARM_SECONDS: an MI355X that has idled
+through the host-side set-up of a case starts in deep sleep and needs ~30 ms of
+sustained load to reach its steady clocks (measured on the LM head: 123 us per
+launch over the first 100 launches, 93 us from the fourth hundred on).
 
-Also reported: ``roofline`` for the dominant kernel (the grouped gate + up
-GEMV, 2 x 12288 x 4096; its HBM ``traffic`` is the per-launch figure measured
-with rocprofv3 FETCH_SIZE / WRITE_SIZE and recorded in
-profiles/gemv_q4k_m1_qwen3_mlp.md), ``cpu_baseline`` (the C restatement in
-oracle/, invoked through its TensorKernelV1 entry exactly as the reference CPU
-provider invokes images), and ``details`` for the other BASELINE
-configurations (C2 M = 4/8 and the three-launch step, C3 LM head, C4 prefill
-GEMM, C5 decoder-layer chain at M = 1 and M = 256).
+Also reported:
+
+* ``roofline`` for the dominant kernel (the grouped gate + up GEMV, 2 x
+  12288 x 4096): ``achieved`` from the live event-timed graph of 200 launches,
+  ``profiled`` the per-dispatch average and HBM ``traffic`` that the committed
+  rocprofv3 summary (profiles/gemv_q4k_m1_qwen3_mlp.md) records for it;
+* ``cpu_baseline``: the C restatement in oracle/, invoked through its
+  TensorKernelV1 entry exactly as the reference CPU provider invokes images,
+  on the headline step and on every other configuration (``per_config``);
+* ``details`` for the other BASELINE configurations (C1's shape, C2 M = 4/8,
+  C3 LM head, C4 prefill GEMM, C5 decoder-layer chain at M = 1 and M = 256),
+  the showcase's packed call at its own shapes, and the resident-dequantized
+  torch.mm lower bound (benchmark.py:478-488) measured in a torch-first child.
 """
 
 from __future__ import annotations
@@ -33,19 +41,27 @@ import argparse
 import json
 import math
 import os
+import random
 import statistics
+import subprocess
 import sys
 import time
 
 import numpy as np
 
+ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 FP16_PEAK_TFLOPS = 2516.6   # MI355X dense fp16 MFMA
 MALL_BYTES = 256 << 20
 ROTATION_BYTES = 3 * MALL_BYTES
+REPLAYS = 11                # timed replays per case (median, min, max and samples reported)
 METRIC = "Q4_K/Q6_K decode GEMV GB/s (% HBM peak); prefill dequant-GEMM TFLOP/s"
 GEOMETRY = {"q4_0": (32, 18), "q8_0": (32, 34), "q4_k": (256, 144), "q6_k": (256, 210), "q4_1": (32, 20),
             "q5_0": (32, 22), "q5_1": (32, 24), "q2_k": (256, 84), "q3_k": (256, 110), "q5_k": (256, 176)}
+# The reference's published showcase figures (NVIDIA L4, hot L2, research/studies/cuda-showcase/
+# evidence/l4-20261024/REPORT.md:19-24): context for the showcase cases, not a same-node target.
+L4_SHOWCASE_US = {("q4_0", 1): 2.355, ("q4_0", 32): 8.924, ("q4_k", 1): 2.729, ("q4_k", 32): 13.829,
+                  ("q6_k", 1): 3.261, ("q6_k", 32): 13.332}
 
 
 def log(*parts):
@@ -57,128 +73,18 @@ def weight_bytes(encoding, n, k):
     return n * (k // qk) * block
 
 
-def gemv_bytes(encoding, m, n, k, out_itemsize):
-    return weight_bytes(encoding, n, k) + 2 * m * k + out_itemsize * m * n
-
-
-class Linear:
-    """One linear layer: R rotated weight copies, its input and output, bound calls."""
-
-    def __init__(self, device, kernel, encoding, m, n, k, out_dtype, copies, seed, x=None):
-        from tests import gguf_cases as cases
-
-        self.device, self.encoding, self.m, self.n, self.k = device, encoding, m, n, k
-        self.out_dtype = out_dtype
-        raw = cases.weight(n, k, encoding, seed)
-        first = device.from_numpy(raw)
-        self.weights = [first] + [device.empty(raw.shape, "uint8").copy_from(first) for _ in range(copies - 1)]
-        self.x = x if x is not None else device.from_numpy(cases.activation(m, k, seed + 1))
-        self.out = device.empty((m, n), out_dtype)
-        self.exe = device.load(kernel, encoding=encoding, out_dtype=out_dtype)
-        self.calls = [self.exe.bind(self.x, w, self.out) for w in self.weights]
-        self.bytes = gemv_bytes(encoding, m, n, k, np.dtype(out_dtype).itemsize)
-        self.flops = 2 * m * n * k
-
-    def release(self):
-        for b in self.weights + [self.out]:
-            b.release()
-
-
-class GroupLinear:
-    """Matrices sharing one activation input, launched as one grouped GEMV call."""
-
-    def __init__(self, device, encoding, m, shapes, out_dtype, copies, seed, x=None):
-        from tests import gguf_cases as cases
-
-        k = shapes[0][1]
-        assert all(sk == k for _, sk in shapes)
-        self.device, self.encoding, self.m, self.k = device, encoding, m, k
-        self.weights = []
-        for i, (n, _) in enumerate(shapes):
-            raw = cases.weight(n, k, encoding, seed + 2 * i)
-            first = device.from_numpy(raw)
-            self.weights.append([first] + [device.empty(raw.shape, "uint8").copy_from(first)
-                                           for _ in range(copies - 1)])
-        self.x = x if x is not None else device.from_numpy(cases.activation(m, k, seed + 1))
-        self.outs = [device.empty((m, n), out_dtype) for n, _ in shapes]
-        self.exe = device.load("gguf_gemv_group", encoding=encoding, out_dtype=out_dtype, count=len(shapes))
-        self.calls = []
-        for c in range(copies):
-            args = [self.x]
-            for ws, out in zip(self.weights, self.outs):
-                args += [ws[c], out]
-            self.calls.append(self.exe.bind(*args))
-        itemsize = np.dtype(out_dtype).itemsize
-        self.bytes = sum(weight_bytes(encoding, n, k) + itemsize * m * n for n, _ in shapes) + 2 * m * k
-        self.flops = sum(2 * m * n * k for n, _ in shapes)
-
-    def release(self):
-        for ws in self.weights:
-            for b in ws:
-                b.release()
-        for b in self.outs:
-            b.release()
-
-
-class SwigluLinear:
-    """An MLP's gate and up matrices launched as one SwiGLU GEMV: out = silu(x Wg^T) * (x Wu^T)."""
-
-    def __init__(self, device, encoding, m, n, k, out_dtype, copies, seed, x=None):
-        from tests import gguf_cases as cases
-
-        self.device, self.encoding, self.m, self.n, self.k = device, encoding, m, n, k
-        self.weights = []
-        for i in range(2):
-            raw = cases.weight(n, k, encoding, seed + 2 * i)
-            first = device.from_numpy(raw)
-            self.weights.append([first] + [device.empty(raw.shape, "uint8").copy_from(first) for _ in range(copies - 1)])
-        self.x = x if x is not None else device.from_numpy(cases.activation(m, k, seed + 1))
-        self.out = device.empty((m, n), out_dtype)
-        self.exe = device.load("gguf_gemv_swiglu", encoding=encoding, out_dtype=out_dtype)
-        self.calls = [self.exe.bind(self.x, self.weights[0][c], self.weights[1][c], self.out) for c in range(copies)]
-        self.bytes = 2 * weight_bytes(encoding, n, k) + 2 * m * k + np.dtype(out_dtype).itemsize * m * n
-        self.flops = 4 * m * n * k
-
-    def release(self):
-        for ws in self.weights:
-            for b in ws:
-                b.release()
-        self.out.release()
-
-
-PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_q4k_m1_qwen3_mlp.md")
-
-
-def measured_traffic():
-    """HBM bytes per launch of the roofline kernel, from the committed rocprofv3 summary
-    (FETCH_SIZE and WRITE_SIZE passes scaled by a 256 MiB copy); None if it is absent."""
-    try:
-        with open(PROFILE) as f:
-            for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1])
-    except OSError:
-        pass
-    return None
+def gemv_bytes(encoding, m, n, k, out_itemsize, x_itemsize=2):
+    return weight_bytes(encoding, n, k) + x_itemsize * m * k + out_itemsize * m * n
 
 
 def copies_for(bytes_per_rotation_unit):
     return max(2, math.ceil(ROTATION_BYTES / bytes_per_rotation_unit))
 
 
-TIMING = "graph"  # set from --timing in main()
+# ------------------------------------------------------------------ timing --
 
-
-def time_launches(device, launches, replays=3):
-    """Median seconds of one pass over ``launches`` (callables), timed with HIP events on the
-    launch stream: replayed from one captured HIP graph (``--timing graph``) or enqueued
-    eagerly on the stream (``--timing eager``)."""
-    if TIMING == "eager":
-        return time_eager(device, launches, replays)
-    return time_graph(device, launches, replays)
-
-
-WARM_SECONDS = 0.1  # untimed replay before each timed sequence (steady clocks; module docstring)
+TIMING = "graph"    # --timing
+WARM_SECONDS = 0.1  # --warm-seconds
 
 
 def warm(device, run):
@@ -191,53 +97,167 @@ def warm(device, run):
             return
 
 
-def time_eager(device, launches, replays=3):
-    warm(device, lambda: [launch() for launch in launches])
-    samples = []
-    for _ in range(replays):
-        start = device.record_event(timing=True)
-        for launch in launches:
-            launch()
-        stop = device.record_event(timing=True)
-        stop.synchronize()
-        samples.append(device.elapsed_ms(start, stop) * 1e-3)
-        start.release()
-        stop.release()
-    return statistics.median(samples)
+def summarize(samples_s, per):
+    """Per-unit statistics of replay samples (seconds per replay, ``per`` units per replay)."""
+    us = [s / per * 1e6 for s in samples_s]
+    return {"median_us": round(statistics.median(us), 3), "min_us": round(min(us), 3),
+            "max_us": round(max(us), 3), "samples_us": [round(u, 3) for u in us]}
 
 
-def time_graph(device, launches, replays=3):
-    """Capture ``launches`` (callables) into one graph; return the median seconds of one replay."""
-    graph = device.graph(lambda: [launch() for launch in launches])
-    try:
-        warm(device, graph.replay)
+def time_launches(device, launches, per=1, replays=REPLAYS):
+    """Time one pass over ``launches`` (callables that enqueue work): replayed from one
+    captured HIP graph (``--timing graph``) or enqueued eagerly (``--timing eager``), each
+    replay bracketed by HIP events on the launch stream.  Returns per-unit statistics."""
+    def timed(run):
         samples = []
         for _ in range(replays):
             start = device.record_event(timing=True)
-            graph.replay()
+            run()
             stop = device.record_event(timing=True)
             stop.synchronize()
             samples.append(device.elapsed_ms(start, stop) * 1e-3)
             start.release()
             stop.release()
-        return statistics.median(samples)
+        return samples
+
+    if TIMING == "eager":
+        def run():
+            for launch in launches:
+                launch()
+        warm(device, run)
+        return summarize(timed(run), per)
+    graph = device.graph(lambda: [launch() for launch in launches])
+    try:
+        warm(device, graph.replay)
+        return summarize(timed(graph.replay), per)
     finally:
         graph.close()
 
 
+def rate(stats, work, unit):
+    """Throughput at the median (and the spread in the same unit) for ``work`` per unit."""
+    scale = 1e-3 if unit == "GB/s" else 1e-6  # bytes/us -> GB/s; flops/us -> TFLOP/s
+    return {unit: round(work / stats["median_us"] * scale, 2),
+            f"{unit}_best": round(work / stats["min_us"] * scale, 2)}
+
+
+# ------------------------------------------------------------------ layers --
+
+def rotated(device, raw, copies):
+    first = device.from_numpy(raw)
+    return [first] + [device.empty(raw.shape, "uint8").copy_from(first) for _ in range(copies - 1)]
+
+
+class Linear:
+    """One linear layer: rotated weight copies, its input and output, bound calls."""
+
+    def __init__(self, device, kernel, encoding, m, n, k, out_dtype, copies, seed, x=None):
+        from tests import gguf_cases as cases
+
+        self.m, self.n, self.k = m, n, k
+        self.weights = rotated(device, cases.weight(n, k, encoding, seed), copies)
+        self.owned = [] if x is not None else [device.from_numpy(cases.activation(m, k, seed + 1))]
+        self.x = x if x is not None else self.owned[0]
+        self.out = device.empty((m, n), out_dtype)
+        exe = device.load(kernel, encoding=encoding, out_dtype=out_dtype)
+        self.calls = [exe.bind(self.x, w, self.out) for w in self.weights]
+        self.bytes = gemv_bytes(encoding, m, n, k, np.dtype(out_dtype).itemsize)
+        self.flops = 2 * m * n * k
+
+    def release(self):
+        for b in self.weights + [self.out] + self.owned:
+            b.release()
+
+
+class GroupLinear:
+    """Matrices sharing one activation input, launched as one grouped GEMV call."""
+
+    def __init__(self, device, encoding, m, shapes, out_dtype, copies, seed, x=None):
+        from tests import gguf_cases as cases
+
+        k = shapes[0][1]
+        assert all(sk == k for _, sk in shapes)
+        self.weights = [rotated(device, cases.weight(n, k, encoding, seed + 2 * i), copies)
+                        for i, (n, _) in enumerate(shapes)]
+        self.owned = [] if x is not None else [device.from_numpy(cases.activation(m, k, seed + 1))]
+        self.x = x if x is not None else self.owned[0]
+        self.outs = [device.empty((m, n), out_dtype) for n, _ in shapes]
+        exe = device.load("gguf_gemv_group", encoding=encoding, out_dtype=out_dtype, count=len(shapes))
+        self.calls = []
+        for c in range(copies):
+            args = [self.x]
+            for ws, out in zip(self.weights, self.outs):
+                args += [ws[c], out]
+            self.calls.append(exe.bind(*args))
+        itemsize = np.dtype(out_dtype).itemsize
+        self.bytes = sum(weight_bytes(encoding, n, k) + itemsize * m * n for n, _ in shapes) + 2 * m * k
+        self.flops = sum(2 * m * n * k for n, _ in shapes)
+
+    def release(self):
+        for b in [w for ws in self.weights for w in ws] + self.outs + self.owned:
+            b.release()
+
+
+class SwigluLinear:
+    """An MLP's gate and up matrices launched as one SwiGLU GEMV: out = silu(x Wg^T) * (x Wu^T)."""
+
+    def __init__(self, device, encoding, m, n, k, out_dtype, copies, seed, x=None):
+        from tests import gguf_cases as cases
+
+        self.weights = [rotated(device, cases.weight(n, k, encoding, seed + 2 * i), copies) for i in range(2)]
+        self.owned = [] if x is not None else [device.from_numpy(cases.activation(m, k, seed + 1))]
+        self.x = x if x is not None else self.owned[0]
+        self.out = device.empty((m, n), out_dtype)
+        exe = device.load("gguf_gemv_swiglu", encoding=encoding, out_dtype=out_dtype)
+        self.calls = [exe.bind(self.x, self.weights[0][c], self.weights[1][c], self.out) for c in range(copies)]
+        self.bytes = 2 * weight_bytes(encoding, n, k) + 2 * m * k + np.dtype(out_dtype).itemsize * m * n
+        self.flops = 4 * m * n * k
+
+    def release(self):
+        for b in [w for ws in self.weights for w in ws] + [self.out] + self.owned:
+            b.release()
+
+
 def rotated_launches(linears, steps):
     """``steps`` passes over the linears, each pass using the next weight copy."""
-    out = []
-    for step in range(steps):
-        for layer in linears:
-            out.append(layer.calls[step % len(layer.calls)].launch)
-    return out
+    return [layer.calls[step % len(layer.calls)].launch for step in range(steps) for layer in linears]
+
+
+# -------------------------------------------------------- committed profile --
+
+PROFILE = os.path.join(ROOT, "profiles", "gemv_q4k_m1_qwen3_mlp.md")
+
+
+def profile_figures():
+    """Machine-readable lines of the committed rocprofv3 summary of the roofline kernel:
+    ``traffic_bytes_per_launch`` (FETCH_SIZE / WRITE_SIZE passes scaled by a 256 MiB copy)
+    and ``avg_us_per_launch`` (kernel-trace average); empty if the file is absent."""
+    figures = {}
+    try:
+        with open(PROFILE) as f:
+            for line in f:
+                key, sep, value = line.partition(":")
+                if sep and key in ("traffic_bytes_per_launch", "avg_us_per_launch"):
+                    figures[key] = float(value)
+    except OSError:
+        pass
+    return figures
 
 
 # ------------------------------------------------------------ CPU baseline --
 
-def cpu_baseline(budget_s=10.0):
-    """Time the oracle's TensorKernelV1 CPU entry on the headline step."""
+def cpu_threads():
+    """Threads for the all-cores leg: the CPUs this process may run on, capped by the job's CPU
+    share (OMP_NUM_THREADS, set to the share on the GPU boxes)."""
+    available = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS")
+    return (min(available, int(share)) if share and share.isdigit() and int(share) > 0 else available), available
+
+
+def cpu_baseline(budget_s=20.0):
+    """Time the oracle's TensorKernelV1 CPU entry (tensor_gguf_gemv_cpu_v1) on the headline
+    step and on every other configuration, invoked as the reference CPU provider invokes a
+    native image (ctypes, synchronous call; src/tensor/providers/cpu.py:153-197)."""
     import ctypes as c
 
     from oracle import gguf_ref
@@ -247,53 +267,81 @@ def cpu_baseline(budget_s=10.0):
     if not gguf_ref.LIBRARY.exists():
         gguf_ref.build()
     oracle = gguf_ref.c_oracle()
-    cores = min(16, len(os.sched_getaffinity(0)))
-    layers = [("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
-    copies = 4  # 340 MB of distinct weights per rotation (beyond the host LLC)
-    data = []
-    for i, (_, n, k) in enumerate(layers):
-        first = cases.weight(n, k, "q4_k", 1000 + i)
-        raws = [first] + [first.copy() for _ in range(copies - 1)]
-        x = cases.activation(1, k, 2000 + i)
-        out = np.empty((1, n), np.float16)
-        data.append((raws, x, out, n, k))
+    entry = oracle.entry
+    entry.argtypes = [c.POINTER(abi.CallDescriptor), c.POINTER(abi.ErrorDescriptor)]
+    entry.restype = c.c_int32
+    threads, available = cpu_threads()
+    codes = {"q8_0": 8, "q4_k": 12, "q6_k": 14}
+    dtype_ids = {np.dtype(np.float16): 10, np.dtype(np.float32): 11, np.dtype(np.uint8): 3}
 
-    def call_for(x, raw, out):
-        keep = []
-        args = (abi.Argument * 4)()
-        for j, (arr, dtype) in enumerate(((x, 10), (raw, 3), (out, 10))):
+    def call_for(x, raw, out, code):
+        keep, args = [], (abi.Argument * 4)()
+        for j, arr in enumerate((x, raw, out)):
             shape = (c.c_int64 * 2)(*arr.shape)
             strides = (c.c_int64 * 2)(arr.strides[0], arr.strides[1])
-            keep += [shape, strides]
+            keep += [shape, strides, arr]
+            dtype = dtype_ids[arr.dtype]
             args[j].kind, args[j].dtype = 1, dtype
             args[j].buffer = abi.BufferDescriptor(arr.ctypes.data, arr.nbytes, shape, strides, 2, dtype, 1, 0)
-        args[3].kind, args[3].dtype, args[3].scalar = 2, 7, 12
+        args[3].kind, args[3].dtype, args[3].scalar = 2, 7, code
         call = abi.CallDescriptor(1, 72, args, 4, 0, (c.c_uint32 * 3)(1, 1, 1), (c.c_uint32 * 3)(1, 1, 1), 0,
                                   abi.StreamDescriptor(1, 0, 0))
         return call, keep, args
 
-    calls = [[call_for(x, raw, out) for raw in raws] for raws, x, out, _, _ in data]
-    entry = oracle.entry
-    entry.argtypes = [c.POINTER(abi.CallDescriptor), c.POINTER(abi.ErrorDescriptor)]
-    entry.restype = c.c_int32
-    step_bytes = sum(gemv_bytes("q4_k", 1, n, k, 2) for _, _, _, n, k in data)
+    def layers_for(shapes, m, out_dtype, seed, rotate=True):
+        """Bound CPU calls for each (encoding, n, k), weights rotated past the host LLC."""
+        step_weights = sum(weight_bytes(e, n, k) for e, n, k in shapes)
+        copies = 1 if not rotate or step_weights >= 256 * 2**20 else math.ceil(512 * 2**20 / step_weights)
+        out = []
+        for i, (encoding, n, k) in enumerate(shapes):
+            first = cases.weight(n, k, encoding, seed + i)
+            x = cases.activation(m, k, seed + 100 + i)
+            o = np.empty((m, n), out_dtype)
+            out.append([call_for(x, first if r == 0 else first.copy(), o, codes[encoding]) for r in range(copies)])
+        return out, copies
 
-    def measure(threads, seconds):
-        oracle.set_threads(threads)
+    def measure(calls, threads_, seconds):
+        oracle.set_threads(threads_)
         error = abi.ErrorDescriptor()
         samples, step, begin = [], 0, time.perf_counter()
         while time.perf_counter() - begin < seconds or len(samples) < 3:
             t0 = time.perf_counter()
             for layer in calls:
-                status = entry(c.byref(layer[step % copies][0]), c.byref(error))
-                if status:
+                if entry(c.byref(layer[step % len(layer)][0]), c.byref(error)):
                     raise RuntimeError(error.message.decode())
             samples.append(time.perf_counter() - t0)
             step += 1
         return statistics.median(samples), len(samples)
 
-    multi, n_multi = measure(cores, budget_s * 0.75)
-    single, n_single = measure(1, budget_s * 0.25)
+    def config(name, shapes, m, out_dtype, seconds, seed, single=True):
+        calls, copies = layers_for(shapes, m, out_dtype, seed)
+        nbytes = sum(gemv_bytes(e, m, n, k, np.dtype(out_dtype).itemsize) for e, n, k in shapes)
+        multi, count = measure(calls, threads, seconds)
+        result = {"GB/s": round(nbytes / multi / 1e9, 3), "ms": round(multi * 1e3, 3), "calls": count,
+                  "threads": threads, "weight_copies": copies, "bytes": nbytes}
+        if single:
+            one, count1 = measure(calls, 1, seconds / 2)
+            result.update({"single_thread_GB/s": round(nbytes / one / 1e9, 3),
+                           "single_thread_ms": round(one * 1e3, 3), "single_thread_calls": count1})
+        log("cpu", name, result)
+        return result
+
+    share = budget_s / 10.0
+    per_config = {
+        "C1_q8_0_gemv_m1_4096x4096": config("C1", [("q8_0", 4096, 4096)], 1, np.float16, share, 3000),
+        "C2_q4k_gemv_m4_12288x4096": config("C2 M=4", [("q4_k", 12288, 4096)], 4, np.float16, share, 3100),
+        "C2_q4k_gemv_m8_12288x4096": config("C2 M=8", [("q4_k", 12288, 4096)], 8, np.float16, share, 3200),
+        "C3_q6k_lm_head_m1_151936x4096_fp32": config("C3", [("q6_k", 151936, 4096)], 1, np.float32, share, 3300,
+                                                     single=False),
+        "C5_layer_m1": config("C5 M=1", [("q4_k", 4096, 4096), ("q4_k", 1024, 4096), ("q4_k", 1024, 4096),
+                                         ("q4_k", 4096, 4096), ("q4_k", 12288, 4096), ("q4_k", 12288, 4096),
+                                         ("q6_k", 4096, 12288)], 1, np.float16, share, 3400),
+    }
+    headline_shapes = [("q4_k", 12288, 4096), ("q4_k", 12288, 4096), ("q4_k", 4096, 12288)]
+    calls, copies = layers_for(headline_shapes, 1, np.float16, 1000)
+    step_bytes = sum(gemv_bytes(e, 1, n, k, 2) for e, n, k in headline_shapes)
+    multi, n_multi = measure(calls, threads, budget_s * 0.3)
+    single, n_single = measure(calls, 1, budget_s * 0.2)
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -303,14 +351,277 @@ def cpu_baseline(budget_s=10.0):
     return {
         "value": round(step_bytes / multi / 1e9, 3),
         "unit": "GB/s",
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
-        "sample": f"{n_multi} steps of the headline step (Q4_K GEMV M=1 gate+up+down, {step_bytes} B/step), "
-                  f"median {multi * 1e3:.2f} ms/step on {cores} threads; weights rotated over {copies} copies",
+        "sample": f"{n_multi} headline steps (Q4_K GEMV M=1 gate+up+down, {step_bytes} B/step), median "
+                  f"{multi * 1e3:.2f} ms/step on {threads} threads; weights rotated over {copies} copies",
         "single_thread_gbs": round(step_bytes / single / 1e9, 3),
         "single_thread_ms_per_step": round(single * 1e3, 3),
+        "cores_available": available,
+        "cores_note": "threads = the CPUs this process may use, capped by the job's CPU share (OMP_NUM_THREADS)",
         "cpu_model": model,
+        "per_config": per_config,
     }
+
+
+# -------------------------------------------------------------- torch leg --
+
+def torch_leg():
+    """The reference's resident-dequantized lower bound (benchmark.py:478-488): torch.mm in fp16
+    on weights already dequantized and resident in HBM, at the prefill and showcase shapes,
+    timed with this file's graph protocol.  Runs in its own process, torch imported first, and
+    prints one JSON object.  Weights are seeded N(0, 0.02) in fp16 (torch.mm's time does not
+    depend on the values); the right operand is a contiguous [K, N] copy of W^T."""
+    import torch
+
+    assert torch.cuda.is_available()
+    device = torch.device("cuda")
+    results = {}
+
+    def graph_time(call, iterations):
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(iterations):
+                call()
+        start = time.perf_counter()
+        while time.perf_counter() - start < WARM_SECONDS:
+            graph.replay()
+            torch.cuda.synchronize()
+        samples = []
+        for _ in range(REPLAYS):
+            begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            begin.record()
+            graph.replay()
+            end.record()
+            end.synchronize()
+            samples.append(begin.elapsed_time(end) * 1e-3)
+        del graph
+        return summarize(samples, iterations)
+
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    for name, m, n, k in (("C4_m512_12288x4096", 512, 12288, 4096), ("C4_m2048_12288x4096", 2048, 12288, 4096),
+                          ("C5_m256_q_4096x4096", 256, 4096, 4096), ("C5_m256_k_1024x4096", 256, 1024, 4096),
+                          ("C5_m256_gate_12288x4096", 256, 12288, 4096), ("C5_m256_down_4096x12288", 256, 4096, 12288)):
+        x = torch.randn(m, k, generator=gen).half().to(device)
+        w_t = (torch.randn(k, n, generator=gen) * 0.02).half().to(device)  # W^T, [K, N], contiguous
+        out = torch.empty(m, n, dtype=torch.float16, device=device)
+        stats = graph_time(lambda: torch.mm(x, w_t, out=out), 10)
+        results[name] = dict(stats, **rate(stats, 2 * m * n * k, "TFLOP/s"))
+        print(f"[torch-leg] {name} {stats['median_us']} us", file=sys.stderr, flush=True)
+        del x, w_t, out
+    for m in (1, 32):  # the showcase's own baseline: fp32 x -> fp16, mm, -> fp32 out
+        n = k = 1024
+        x32 = torch.randn(m * k, generator=gen).to(device) * 0.2
+        w_t = (torch.randn(k, n, generator=gen) * 0.02).half().to(device)
+        activation = torch.empty(m, k, dtype=torch.float16, device=device)
+        temp = torch.empty(m, n, dtype=torch.float16, device=device)
+        out = torch.empty(m * n, dtype=torch.float32, device=device)
+
+        def baseline():
+            activation.copy_(x32.reshape(m, k))
+            torch.mm(activation, w_t, out=temp)
+            out.copy_(temp.reshape(-1))
+
+        stats = graph_time(baseline, 30)
+        results[f"showcase_m{m}_1024x1024"] = stats
+        print(f"[torch-leg] showcase m={m} {stats['median_us']} us", file=sys.stderr, flush=True)
+    print(json.dumps({"torch": torch.__version__, "hip": torch.version.hip, "cases": results}))
+
+
+def run_torch_leg():
+    """Run torch_leg() in a child process (torch must own the process's HIP runtime)."""
+    command = [sys.executable, "-u", os.path.abspath(__file__), "--torch-leg", "--warm-seconds", str(WARM_SECONDS)]
+    try:
+        done = subprocess.run(command, capture_output=True, text=True, timeout=600, cwd=ROOT)
+    except subprocess.TimeoutExpired:
+        return {"error": "torch leg timed out"}
+    sys.stderr.write(done.stderr[-3000:])
+    if done.returncode:
+        return {"error": f"torch leg exited with {done.returncode}"}
+    return json.loads(done.stdout.strip().splitlines()[-1])
+
+
+# ---------------------------------------------------------------- details --
+
+def detail_cases(device):
+    """(name, function) for every details case; each builds, times and releases its own buffers."""
+    from tests import gguf_cases as cases
+
+    cases_ = []
+
+    def add(name):
+        def register(function):
+            cases_.append((name, function))
+            return function
+        return register
+
+    def gemv_case(name, encoding, m, n, k, out_dtype, launches=60):
+        @add(name)
+        def run():
+            copies = copies_for(weight_bytes(encoding, n, k))
+            layer = Linear(device, "gguf_gemv", encoding, m, n, k, out_dtype, copies, 7 + m)
+            stats = time_launches(device, [layer.calls[i % copies].launch for i in range(launches)], per=launches)
+            result = dict(stats, **rate(stats, layer.bytes, "GB/s"), copies=copies)
+            result["hbm_frac"] = round(result["GB/s"] / HBM_PEAK_GBS, 4)
+            layer.release()
+            return result
+
+    def mlp_copies():
+        return copies_for(2 * weight_bytes("q4_k", 12288, 4096) + weight_bytes("q4_k", 4096, 12288))
+
+    @add("C2_step_m1_three_launches")
+    def three_launches():
+        copies = mlp_copies()
+        x = device.from_numpy(cases.activation(1, 4096, 2))
+        mlp = [Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 1, x=x),
+               Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 3, x=x),
+               Linear(device, "gguf_gemv", "q4_k", 1, 4096, 12288, "float16", copies, 5)]
+        stats = time_launches(device, rotated_launches(mlp, 50), per=50)
+        result = dict(stats, **rate(stats, sum(layer.bytes for layer in mlp), "GB/s"))
+        result["hbm_frac"] = round(result["GB/s"] / HBM_PEAK_GBS, 4)
+        for layer in mlp:
+            layer.release()
+        x.release()
+        return result
+
+    @add("C2_step_m1_swiglu")
+    def swiglu_step():
+        # the MLP as a decode step runs it: gate + up with the SwiGLU epilogue in one launch,
+        # then down on its output
+        copies = mlp_copies()
+        fused = SwigluLinear(device, "q4_k", 1, 12288, 4096, "float16", copies, 60)
+        down = Linear(device, "gguf_gemv", "q4_k", 1, 4096, 12288, "float16", copies, 64, x=fused.out)
+        stats = time_launches(device, rotated_launches([fused, down], 50), per=50)
+        result = dict(stats, **rate(stats, fused.bytes + down.bytes, "GB/s"), launches=2)
+        result["hbm_frac"] = round(result["GB/s"] / HBM_PEAK_GBS, 4)
+        down.release()
+        fused.release()
+        return result
+
+    for m in (1, 4, 8):
+        @add(f"C2_q4k_gemv_swiglu_m{m}_12288x4096")
+        def swiglu_pair(m=m):
+            copies = copies_for(2 * weight_bytes("q4_k", 12288, 4096))
+            pair = SwigluLinear(device, "q4_k", m, 12288, 4096, "float16", copies, 66 + m)
+            stats = time_launches(device, [pair.calls[i % copies].launch for i in range(60)], per=60)
+            result = dict(stats, **rate(stats, pair.bytes, "GB/s"), copies=copies)
+            result["hbm_frac"] = round(result["GB/s"] / HBM_PEAK_GBS, 4)
+            pair.release()
+            return result
+
+    for m in (4, 8):
+        @add(f"C2_q4k_gemv_group_m{m}_2x12288x4096")
+        def group_pair(m=m):
+            copies = copies_for(2 * weight_bytes("q4_k", 12288, 4096))
+            group = GroupLinear(device, "q4_k", m, [(12288, 4096), (12288, 4096)], "float16", copies, 70 + m)
+            stats = time_launches(device, [group.calls[i % copies].launch for i in range(60)], per=60)
+            result = dict(stats, **rate(stats, group.bytes, "GB/s"), copies=copies)
+            result["hbm_frac"] = round(result["GB/s"] / HBM_PEAK_GBS, 4)
+            group.release()
+            return result
+
+    # C1's shape (the reference runs it on its CPU provider) on the GPU
+    gemv_case("C1_q8_0_gemv_m1_4096x4096", "q8_0", 1, 4096, 4096, "float16")
+    gemv_case("C5_q6k_gemv_m1_4096x12288", "q6_k", 1, 4096, 12288, "float16")
+    for m in (1, 4, 8):
+        gemv_case(f"C2_q4k_gemv_m{m}_12288x4096", "q4_k", m, 12288, 4096, "float16")
+        gemv_case(f"C2_q4k_gemv_m{m}_4096x12288", "q4_k", m, 4096, 12288, "float16")
+    gemv_case("C3_q6k_lm_head_m1_151936x4096_fp32", "q6_k", 1, 151936, 4096, "float32", launches=20)
+    for encoding in ("q6_k", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q5_k"):
+        gemv_case(f"enc_{encoding}_gemv_m1_12288x4096", encoding, 1, 12288, 4096, "float16")
+
+    def gemm_case(name, encoding, m, n, k, launches=10):
+        @add(name)
+        def run():
+            layer = Linear(device, "gguf_gemm", encoding, m, n, k, "float16", 2, 9)
+            stats = time_launches(device, [layer.calls[i % 2].launch for i in range(launches)], per=launches)
+            result = dict(stats, **rate(stats, layer.flops, "TFLOP/s"))
+            result["mfma_frac"] = round(result["TFLOP/s"] / FP16_PEAK_TFLOPS, 4)
+            layer.release()
+            return result
+
+    gemm_case("C4_q4k_gemm_m512_12288x4096", "q4_k", 512, 12288, 4096)
+    gemm_case("C4_q4k_gemm_m2048_12288x4096", "q4_k", 2048, 12288, 4096, launches=4)
+    for encoding in ("q5_k", "q8_0", "q4_0"):
+        gemm_case(f"enc_{encoding}_gemm_m512_12288x4096", encoding, 512, 12288, 4096)
+
+    # C5: q, k, v, o, gate, up (Q4_K) and down (Q6_K) chained on one stream
+    shapes = [("q", "q4_k", 4096, 4096), ("k", "q4_k", 1024, 4096), ("v", "q4_k", 1024, 4096),
+              ("o", "q4_k", 4096, 4096), ("gate", "q4_k", 12288, 4096), ("up", "q4_k", 12288, 4096),
+              ("down", "q6_k", 4096, 12288)]
+    layer_weights = sum(weight_bytes(e, n, k) for _, e, n, k in shapes)
+    for m, kernel in ((1, "gguf_gemv"), (256, "gguf_gemm")):
+        @add(f"C5_layer_m{m}")
+        def layer_chain(m=m, kernel=kernel):
+            copies = copies_for(layer_weights) if m == 1 else 2
+            layers = [Linear(device, kernel, e, m, n, k, "float16", copies, 20 + i)
+                      for i, (_, e, n, k) in enumerate(shapes)]
+            steps = 20 if m == 1 else 4
+            stats = time_launches(device, rotated_launches(layers, steps), per=steps)
+            result = dict(stats, **rate(stats, sum(layer.bytes for layer in layers), "GB/s"),
+                          **rate(stats, sum(layer.flops for layer in layers), "TFLOP/s"))
+            if m > 1:  # each linear on its own, for the per-kernel picture
+                result["per_linear_us"] = {}
+                for (name, *_), layer in zip(shapes, layers):
+                    one = time_launches(device, [layer.calls[i % 2].launch for i in range(10)], per=10)
+                    result["per_linear_us"][name] = one["median_us"]
+            for layer in layers:
+                layer.release()
+            return result
+
+    @add("C5_layer_m1_grouped")
+    def layer_grouped():
+        # C5 at M=1 the way a decode step runs it: q + k + v grouped, o, gate + up grouped, down
+        copies = copies_for(layer_weights)
+        x = device.from_numpy(np.zeros((1, 4096), np.float16) + np.float16(0.5))
+        layers = [GroupLinear(device, "q4_k", 1, [(4096, 4096), (1024, 4096), (1024, 4096)], "float16", copies, 40,
+                              x=x),
+                  Linear(device, "gguf_gemv", "q4_k", 1, 4096, 4096, "float16", copies, 46, x=x),
+                  GroupLinear(device, "q4_k", 1, [(12288, 4096), (12288, 4096)], "float16", copies, 48, x=x),
+                  Linear(device, "gguf_gemv", "q6_k", 1, 4096, 12288, "float16", copies, 52)]
+        stats = time_launches(device, rotated_launches(layers, 20), per=20)
+        result = dict(stats, **rate(stats, sum(layer.bytes for layer in layers), "GB/s"), launches=4)
+        for layer in layers:
+            layer.release()
+        x.release()
+        return result
+
+    # The showcase's packed call at its own shapes (N = K = 1024, M in {1, 32}, fp32 x and out,
+    # benchmark.py:122-126, :460-464), hot-cache as the reference times it (one weight copy).
+    for encoding in ("q4_0", "q4_k", "q6_k"):
+        for m in (1, 32):
+            @add(f"showcase_{encoding}_m{m}_1024x1024")
+            def showcase(encoding=encoding, m=m):
+                n = k = 1024
+                x = (np.random.default_rng(m).standard_normal(m * k, dtype=np.float32) * np.float32(0.2))
+                xb = device.from_numpy(x)
+                wb = device.from_numpy(cases.weight(n, k, encoding, 11).reshape(-1))
+                out = device.empty((m * n,), "float32")
+                call = device.load("gguf_linear", encoding=encoding, m=m, n=n, k=k).bind(xb, wb, out)
+                stats = time_launches(device, [call.launch] * 30, per=30)
+                result = dict(stats, **rate(stats, gemv_bytes(encoding, m, n, k, 4, 4), "GB/s"),
+                              **rate(stats, 2 * m * n * k, "TFLOP/s"))
+                result["l4_reference_us"] = L4_SHOWCASE_US[(encoding, m)]
+                for b in (xb, wb, out):
+                    b.release()
+                return result
+
+    return cases_
+
+
+def run_details(device, only=None):
+    """Every details case whose name starts with ``only`` (all by default), in a seeded shuffled
+    order (benchmark.py:1007-1013 shuffles its providers with random.Random(42))."""
+    chosen = [(name, run) for name, run in detail_cases(device) if only is None or name.startswith(only)]
+    random.Random(42).shuffle(chosen)
+    details = {"measurement_order": [name for name, _ in chosen]}
+    for name, run in chosen:
+        details[name] = run()
+        log(name, {k: v for k, v in details[name].items() if k != "samples_us"})
+    return details
 
 
 # ------------------------------------------------------------------- main --
@@ -323,7 +634,8 @@ def main():
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-details", action="store_true", help="headline only")
-    parser.add_argument("--cpu-seconds", type=float, default=10.0)
+    parser.add_argument("--no-torch", action="store_true", help="skip the resident-dequantized torch.mm leg")
+    parser.add_argument("--cpu-seconds", type=float, default=20.0)
     parser.add_argument("--calibrate", action="store_true",
                         help="first run 5 device copies of 256 MiB (a known-size copy kernel for PMC scaling)")
     parser.add_argument("--timing", choices=("graph", "eager"), default="graph",
@@ -334,6 +646,7 @@ def main():
                         help="stop after the eager warmup launches (for per-dispatch counter runs)")
     parser.add_argument("--warm-seconds", type=float, default=WARM_SECONDS,
                         help="untimed replay before each timed sequence (0: one replay, e.g. for counter runs)")
+    parser.add_argument("--torch-leg", action="store_true", help=argparse.SUPPRESS)
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -343,8 +656,11 @@ def main():
         parser.error("steps must be >= 1 and warmup >= 0")
     TIMING = args.timing
     WARM_SECONDS = max(0.0, args.warm_seconds)
+    if args.torch_leg:
+        torch_leg()
+        return 0
 
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, ROOT)
     import tensor_amd as tx
 
     device = tx.Device(0, provider="hip")
@@ -367,7 +683,7 @@ def main():
         gate_up = GroupLinear(device, "q4_k", 1, [(12288, 4096), (12288, 4096)], "float16", copies, 1)
         down = Linear(device, "gguf_gemv", "q4_k", 1, 4096, 12288, "float16", copies, 5)
         mlp = [gate_up, down]
-        step_bytes = sum(layer.bytes for layer in mlp)
+        step_bytes = gate_up.bytes + down.bytes
         for launch in rotated_launches(mlp, args.warmup):
             launch()
         device.synchronize()
@@ -376,32 +692,48 @@ def main():
             for layer in mlp:
                 layer.release()
             return 0
-        seconds = time_launches(device, rotated_launches(mlp, args.steps), replays=3)
+        headline = time_launches(device, rotated_launches(mlp, args.steps), per=args.steps)
+        seconds = headline["median_us"] * 1e-6 * args.steps
         value = step_bytes * args.steps / seconds / 1e9
-        log(f"headline {value:.1f} GB/s, {seconds / args.steps * 1e6:.2f} us/step")
+        log(f"headline {value:.1f} GB/s, {headline['median_us']:.2f} us/step "
+            f"(min {headline['min_us']}, max {headline['max_us']})")
 
         # ---- roofline of the dominant kernel: the grouped gate + up GEMV, 2 x 12288 x 4096, M=1
         launches = 200
-        kernel_s = time_launches(device, [gate_up.calls[i % copies].launch for i in range(launches)]) / launches
-        achieved = gate_up.bytes / kernel_s / 1e9
+        kernel = time_launches(device, [gate_up.calls[i % copies].launch for i in range(launches)], per=launches)
+        achieved = gate_up.bytes / kernel["median_us"] / 1e3
+        figures = profile_figures()
+        profiled = None
+        if "avg_us_per_launch" in figures:
+            avg = figures["avg_us_per_launch"]
+            profiled = {"avg_us": avg, "achieved": round(gate_up.bytes / avg / 1e3, 1),
+                        "frac": round(gate_up.bytes / avg / 1e3 / HBM_PEAK_GBS, 4),
+                        "source": "profiles/gemv_q4k_m1_qwen3_mlp.md (rocprofv3 --kernel-trace --stats, "
+                                  "per-dispatch average of eager launches)"}
         roofline = {
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(),
+            "traffic": int(figures["traffic_bytes_per_launch"]) if "traffic_bytes_per_launch" in figures else None,
             "kernel": "gemv_q4k_m1<STEPS=1, WAVES=8, MATS=2> gate+up 2 x 12288x4096, M=1, fp16 out",
-            "avg_us": round(kernel_s * 1e6, 3),
+            "timing": f"live: HIP events around a graph of {launches} launches, median of {REPLAYS} replays",
+            "avg_us": kernel["median_us"],
+            "avg_us_min": kernel["min_us"],
+            "avg_us_max": kernel["max_us"],
             "algorithmic_bytes": gate_up.bytes,
+            "profiled": profiled,
         }
-        log(f"roofline kernel {kernel_s * 1e6:.2f} us -> {achieved:.1f} GB/s")
+        log(f"roofline kernel {kernel['median_us']:.2f} us -> {achieved:.1f} GB/s; profiled {profiled}")
+        for layer in mlp:
+            layer.release()
 
         details = {}
         if not args.no_details:
-            details = run_details(device, gate_up.x, log, args.only)
-        for layer in mlp:
-            layer.release()
+            details = run_details(device, args.only)
+    if not args.no_details and not args.no_torch and args.only is None:
+        details["torch_resident_dequantized_lower_bound"] = run_torch_leg()
 
     result = {
         "metric": METRIC,
@@ -424,7 +756,8 @@ def main():
             "hidden": 4096,
             "intermediate": 12288,
             "bytes_per_step": step_bytes,
-            "timing": "HIP graph of all K steps, HIP events on the launch stream",
+            "timing": f"HIP graph of all K steps, HIP events on the launch stream, median of {REPLAYS} replays",
+            "step_us": {k: v for k, v in headline.items()},
         },
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu else cpu_baseline(args.cpu_seconds),
@@ -432,165 +765,6 @@ def main():
     }
     print(json.dumps(result))
     return 0
-
-
-def three_launch_step(device, x4096, log, details):
-    """The headline step as three single-matrix launches (gate, up, down)."""
-    copies = copies_for(2 * weight_bytes("q4_k", 12288, 4096) + weight_bytes("q4_k", 4096, 12288))
-    mlp = [Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 1, x=x4096),
-           Linear(device, "gguf_gemv", "q4_k", 1, 12288, 4096, "float16", copies, 3, x=x4096),
-           Linear(device, "gguf_gemv", "q4_k", 1, 4096, 12288, "float16", copies, 5)]
-    steps = 50
-    seconds = time_launches(device, rotated_launches(mlp, steps)) / steps
-    step_bytes = sum(layer.bytes for layer in mlp)
-    details["C2_step_m1_three_launches"] = {"us": round(seconds * 1e6, 3),
-                                            "GB/s": round(step_bytes / seconds / 1e9, 1),
-                                            "hbm_frac": round(step_bytes / seconds / 1e9 / HBM_PEAK_GBS, 4)}
-    log("C2_step_m1_three_launches", details["C2_step_m1_three_launches"])
-    for layer in mlp:
-        layer.release()
-
-
-def run_details(device, x4096, log, only=None):
-    """Per-config figures for the other BASELINE configurations (those whose name starts with
-    ``only``, when given)."""
-    details = {}
-
-    def wanted(name):
-        return only is None or name.startswith(only)
-
-    def gemv_case(name, encoding, m, n, k, out_dtype, launches=60):
-        if not wanted(name):
-            return
-        copies = copies_for(weight_bytes(encoding, n, k))
-        layer = Linear(device, "gguf_gemv", encoding, m, n, k, out_dtype, copies, 7 + m)
-        seconds = time_launches(device, [layer.calls[i % copies].launch for i in range(launches)]) / launches
-        gbs = layer.bytes / seconds / 1e9
-        details[name] = {"us": round(seconds * 1e6, 3), "GB/s": round(gbs, 1),
-                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
-        log(name, details[name])
-        layer.release()
-
-    # the headline step as three single-matrix launches (gate, up, down)
-    if wanted("C2_step_m1_three_launches"):
-        three_launch_step(device, x4096, log, details)
-
-    # the MLP as a decode step runs it: gate + up with the SwiGLU epilogue in one launch, then
-    # down on its output (the headline step leaves the SwiGLU between them out)
-    if wanted("C2_q4k_gemv_swiglu_m1_12288x4096") or wanted("C2_step_m1_swiglu"):
-        copies = copies_for(2 * weight_bytes("q4_k", 12288, 4096) + weight_bytes("q4_k", 4096, 12288))
-        fused = SwigluLinear(device, "q4_k", 1, 12288, 4096, "float16", copies, 60, x=x4096)
-        launches = 60
-        seconds = time_launches(device, [fused.calls[i % copies].launch for i in range(launches)]) / launches
-        gbs = fused.bytes / seconds / 1e9
-        details["C2_q4k_gemv_swiglu_m1_12288x4096"] = {"us": round(seconds * 1e6, 3), "GB/s": round(gbs, 1),
-                                                       "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
-        log("C2_q4k_gemv_swiglu_m1_12288x4096", details["C2_q4k_gemv_swiglu_m1_12288x4096"])
-        down = Linear(device, "gguf_gemv", "q4_k", 1, 4096, 12288, "float16", copies, 64, x=fused.out)
-        steps = 50
-        seconds = time_launches(device, rotated_launches([fused, down], steps)) / steps
-        step_bytes = fused.bytes + down.bytes
-        details["C2_step_m1_swiglu"] = {"us": round(seconds * 1e6, 3), "GB/s": round(step_bytes / seconds / 1e9, 1),
-                                        "hbm_frac": round(step_bytes / seconds / 1e9 / HBM_PEAK_GBS, 4),
-                                        "launches": 2}
-        log("C2_step_m1_swiglu", details["C2_step_m1_swiglu"])
-        down.release()
-        fused.release()
-
-    # C1's shape (the reference runs it on its CPU provider) on the GPU
-    gemv_case("C1_q8_0_gemv_m1_4096x4096", "q8_0", 1, 4096, 4096, "float16")
-    # C5's Q6_K down projection on its own
-    gemv_case("C5_q6k_gemv_m1_4096x12288", "q6_k", 1, 4096, 12288, "float16")
-    # gate + up as one grouped launch at M = 4 and 8
-    for m in (4, 8):
-        name = f"C2_q4k_gemv_group_m{m}_2x12288x4096"
-        if wanted(name):
-            copies = copies_for(2 * weight_bytes("q4_k", 12288, 4096))
-            group = GroupLinear(device, "q4_k", m, [(12288, 4096), (12288, 4096)], "float16", copies, 70 + m)
-            seconds = time_launches(device, [group.calls[i % copies].launch for i in range(60)]) / 60
-            gbs = group.bytes / seconds / 1e9
-            details[name] = {"us": round(seconds * 1e6, 3), "GB/s": round(gbs, 1),
-                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
-            log(name, details[name])
-            group.release()
-    # the SwiGLU pair at M = 4 and 8
-    for m in (4, 8):
-        name = f"C2_q4k_gemv_swiglu_m{m}_12288x4096"
-        if wanted(name):
-            copies = copies_for(2 * weight_bytes("q4_k", 12288, 4096))
-            pair = SwigluLinear(device, "q4_k", m, 12288, 4096, "float16", copies, 66 + m)
-            seconds = time_launches(device, [pair.calls[i % copies].launch for i in range(60)]) / 60
-            gbs = pair.bytes / seconds / 1e9
-            details[name] = {"us": round(seconds * 1e6, 3), "GB/s": round(gbs, 1),
-                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
-            log(name, details[name])
-            pair.release()
-    for m in (1, 4, 8):
-        gemv_case(f"C2_q4k_gemv_m{m}_12288x4096", "q4_k", m, 12288, 4096, "float16")
-        gemv_case(f"C2_q4k_gemv_m{m}_4096x12288", "q4_k", m, 4096, 12288, "float16")
-    gemv_case("C3_q6k_lm_head_m1_151936x4096_fp32", "q6_k", 1, 151936, 4096, "float32", launches=20)
-    # every other encoding at the C2 gate shape, M = 1 (Q6_K, Q8_0 and Q4_0 on their own kernels,
-    # the rest on the generic per-element decoder)
-    for encoding in ("q6_k", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q5_k"):
-        gemv_case(f"enc_{encoding}_gemv_m1_12288x4096", encoding, 1, 12288, 4096, "float16")
-
-    def gemm_case(name, encoding, m, n, k, launches=10):
-        if not wanted(name):
-            return
-        layer = Linear(device, "gguf_gemm", encoding, m, n, k, "float16", 2, 9)
-        seconds = time_launches(device, [layer.calls[i % 2].launch for i in range(launches)]) / launches
-        tflops = layer.flops / seconds / 1e12
-        details[name] = {"us": round(seconds * 1e6, 2), "TFLOP/s": round(tflops, 2),
-                         "mfma_frac": round(tflops / FP16_PEAK_TFLOPS, 4)}
-        log(name, details[name])
-        layer.release()
-
-    gemm_case("C4_q4k_gemm_m512_12288x4096", "q4_k", 512, 12288, 4096)
-    for encoding in ("q5_k", "q8_0", "q4_0"):
-        gemm_case(f"enc_{encoding}_gemm_m512_12288x4096", encoding, 512, 12288, 4096)
-    gemm_case("C4_q4k_gemm_m2048_12288x4096", "q4_k", 2048, 12288, 4096, launches=4)
-
-    # C5: q, k, v, o, gate, up (Q4_K) and down (Q6_K) chained on one stream
-    shapes = [("q", "q4_k", 4096, 4096), ("k", "q4_k", 1024, 4096), ("v", "q4_k", 1024, 4096),
-              ("o", "q4_k", 4096, 4096), ("gate", "q4_k", 12288, 4096), ("up", "q4_k", 12288, 4096),
-              ("down", "q6_k", 4096, 12288)]
-    layer_weights = sum(weight_bytes(e, n, k) for _, e, n, k in shapes)
-    for m, kernel in ((1, "gguf_gemv"), (256, "gguf_gemm")):
-        if not wanted(f"C5_layer_m{m}"):
-            continue
-        copies = copies_for(layer_weights) if m == 1 else 2
-        layers = [Linear(device, kernel, e, m, n, k, "float16", copies, 20 + i) for i, (_, e, n, k) in enumerate(shapes)]
-        steps = 20 if m == 1 else 4
-        seconds = time_launches(device, rotated_launches(layers, steps)) / steps
-        total_bytes = sum(layer.bytes for layer in layers)
-        total_flops = sum(layer.flops for layer in layers)
-        details[f"C5_layer_m{m}"] = {
-            "us": round(seconds * 1e6, 2),
-            "GB/s": round(total_bytes / seconds / 1e9, 1),
-            "TFLOP/s": round(total_flops / seconds / 1e12, 2),
-        }
-        log(f"C5_layer_m{m}", details[f"C5_layer_m{m}"])
-        for layer in layers:
-            layer.release()
-    # C5 at M=1 the way a decode step runs it: q + k + v grouped, o, gate + up grouped, down
-    if not wanted("C5_layer_m1_grouped"):
-        return details
-    copies = copies_for(layer_weights)
-    x = device.from_numpy(np.zeros((1, 4096), np.float16) + np.float16(0.5))
-    layers = [GroupLinear(device, "q4_k", 1, [(4096, 4096), (1024, 4096), (1024, 4096)], "float16", copies, 40, x=x),
-              Linear(device, "gguf_gemv", "q4_k", 1, 4096, 4096, "float16", copies, 46, x=x),
-              GroupLinear(device, "q4_k", 1, [(12288, 4096), (12288, 4096)], "float16", copies, 48, x=x),
-              Linear(device, "gguf_gemv", "q6_k", 1, 4096, 12288, "float16", copies, 52)]
-    steps = 20
-    seconds = time_launches(device, rotated_launches(layers, steps)) / steps
-    total_bytes = sum(layer.bytes for layer in layers)
-    details["C5_layer_m1_grouped"] = {"us": round(seconds * 1e6, 2), "GB/s": round(total_bytes / seconds / 1e9, 1),
-                                      "launches": 4}
-    log("C5_layer_m1_grouped", details["C5_layer_m1_grouped"])
-    for layer in layers:
-        layer.release()
-    x.release()
-    return details
 
 
 if __name__ == "__main__":

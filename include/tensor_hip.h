@@ -86,6 +86,22 @@ int32_t tensor_gguf_gemm_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 int32_t tensor_gguf_linear_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 
 /*
+ * Quantized linear in the AKAS packed call form, which the showcase launches unchanged
+ * (buffers [x, w, out] at benchmarks/kernels/showcase/benchmark.py:460-464, launched by
+ * TensorCall at :276-290; the kernel is specialised on (m, n, k), kernels.py:114-119, so the
+ * shape travels as scalars a manifest fixes).  Dispatch as the showcase's: M == 1 is the
+ * decode GEMV with x in its own precision (fp32 x times the fp32-decoded weight,
+ * benchmark.py:466-472), M > 1 the prefill GEMM with x rounded to fp16 as it is staged
+ * (benchmark.py:473-477).  Arguments, in order:
+ *   0 x    buffer fp32 or fp16, M*K elements (any rank, contiguous)
+ *   1 w    buffer of any integer dtype, exactly N*(K/QK)*BLOCK bytes of raw GGUF rows
+ *   2 out  buffer fp32 or fp16, M*N elements (any rank, contiguous)
+ *   3 type scalar uint32 GGML type id
+ *   4 m, 5 n, 6 k  scalar uint32; K a multiple of the block's QK
+ */
+int32_t tensor_gguf_packed_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/*
  * Grouped decode GEMV: out_i[m, n] = sum_k x[m, k] * dequant(W_i)[n, k] for
  * 1 <= c <= TENSOR_GGUF_GEMV_GROUP_MAX matrices that share the activations x
  * (a decoder's gate and up projections, or q, k and v).  No counterpart in the
@@ -221,6 +237,9 @@ int32_t tensor_hip_module_launch_v1(uint64_t function, const TensorCallV1 *call,
 
 /* Library build identity: "tensor_hip <abi> <arch>". */
 const char *tensor_hip_version(void);
+/* SHA-256 (hex) of the csrc/ and include/ files the library was built from; the Python
+ * loader refuses a library whose hash differs from the sources beside it. */
+const char *tensor_hip_source_hash(void);
 
 #ifdef __cplusplus
 }

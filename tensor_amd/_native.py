@@ -17,6 +17,7 @@ LIBRARY = Path(__file__).resolve().parent / "libtensor_hip.so"
 
 # Kernel entry points (TensorKernelV1 shape).
 KERNELS = (
+    "tensor_gguf_packed_v1",
     "tensor_gguf_gemv_v1",
     "tensor_gguf_gemm_v1",
     "tensor_gguf_linear_v1",
@@ -124,9 +125,27 @@ def library(path: Path | None = None) -> c.CDLL:
         lib.tensor_hip_module_launch_v1.restype = c.c_int32
         lib.tensor_hip_version.argtypes = []
         lib.tensor_hip_version.restype = c.c_char_p
+        lib.tensor_hip_source_hash.argtypes = []
+        lib.tensor_hip_source_hash.restype = c.c_char_p
         if path is None:
+            _check_fresh(lib, target)
             _library = lib
         return lib
+
+
+def _check_fresh(lib: c.CDLL, target: Path) -> None:
+    """Refuse a library built from other sources than the csrc/ and include/ beside it."""
+    from tensor_amd import build
+
+    if not build.CSRC.is_dir():
+        return  # an installed library without its sources: nothing to compare
+    embedded = lib.tensor_hip_source_hash().decode()
+    current = build.source_hash()
+    if embedded != current:
+        raise NativeLibraryError(
+            f"{target} was built from other sources ({embedded[:12]}) than tensor_amd/csrc and include "
+            f"({current[:12]}); rebuild with `python -m tensor_amd.build`"
+        )
 
 
 def call(name: str, *arguments) -> None:

@@ -132,11 +132,35 @@ def build_executor(verbose: bool = False) -> Path | None:
     return target
 
 
+def source_hash() -> str:
+    """SHA-256 over every file the library is compiled from (csrc/ and include/, by relative
+    path and content).  build() embeds it in the library and the loader refuses a library
+    whose embedded hash differs from the sources beside it, so a stale binary is never
+    tested or benchmarked silently."""
+    import hashlib
+
+    digest = hashlib.sha256()
+    files = sorted(p for d in (CSRC, ROOT / "include") for p in d.rglob("*") if p.is_file())
+    for path in files:
+        digest.update(str(path.relative_to(ROOT)).encode() + b"\0")
+        digest.update(path.read_bytes())
+        digest.update(b"\0")
+    return digest.hexdigest()
+
+
 def build(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
+    identity = source_hash()
+    stamp = BUILD / "source_hash.c"
+    stamp.write_text(f'const char* tensor_hip_source_hash(void) {{ return "{identity}"; }}\n')
+    stamp_obj = BUILD / "source_hash.o"
+    result = subprocess.run([os.environ.get("CC", "gcc"), "-O2", "-fPIC", "-c", str(stamp), "-o", str(stamp_obj)],
+                            capture_output=True, text=True)
+    if result.returncode:
+        raise RuntimeError(f"source hash stamp failed:\n{result.stderr}")
     with ThreadPoolExecutor(max_workers=min(8, len(sources))) as pool:
-        objects = list(pool.map(lambda s: _compile(s, verbose), sources))
+        objects = list(pool.map(lambda s: _compile(s, verbose), sources)) + [stamp_obj]
     tmp = LIBRARY.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     result = subprocess.run(cmd, capture_output=True, text=True)

@@ -46,8 +46,9 @@ __device__ __forceinline__ void q4k_dequant4(uint32_t codes, float ds, float dm,
   hi_pair = pack_half2(c, d);
 }
 
-template <int TYPE, int BM, int BN, int WM, int WN, typename OutT>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_v2(const _Float16* __restrict__ x,
+// XT = float: fp32 activations (the packed call form), rounded to fp16 as they are loaded.
+template <int TYPE, int BM, int BN, int WM, int WN, typename OutT, typename XT = _Float16>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_v2(const XT* __restrict__ x,
                                                         const uint8_t* __restrict__ w,
                                                         OutT* __restrict__ out, int M, int N, int K) {
   using namespace gemm;
@@ -89,8 +90,21 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_v2(const _Float16* __restri
 #pragma unroll
     for (int i = 0; i < X_LOADS; ++i) {
       const int c = i * THREADS + tid, r = c >> 3, c8 = (c & 7) * 8;
-      xr[i] = (m0 + r < M && k0 + c8 < K) ? *reinterpret_cast<const uint4*>(x + (size_t)(m0 + r) * K + k0 + c8)
-                                          : make_uint4(0, 0, 0, 0);
+      if (m0 + r < M && k0 + c8 < K) {
+        const XT* src = x + (size_t)(m0 + r) * K + k0 + c8;
+        if constexpr (sizeof(XT) == 4) {
+          const uint4 lo = load16(reinterpret_cast<const uint8_t*>(src));
+          const uint4 hi = load16(reinterpret_cast<const uint8_t*>(src + 4));
+          xr[i] = make_uint4(half2_from_fp32(__builtin_bit_cast(float, lo.x), __builtin_bit_cast(float, lo.y)),
+                             half2_from_fp32(__builtin_bit_cast(float, lo.z), __builtin_bit_cast(float, lo.w)),
+                             half2_from_fp32(__builtin_bit_cast(float, hi.x), __builtin_bit_cast(float, hi.y)),
+                             half2_from_fp32(__builtin_bit_cast(float, hi.z), __builtin_bit_cast(float, hi.w)));
+        } else {
+          xr[i] = *reinterpret_cast<const uint4*>(src);
+        }
+      } else {
+        xr[i] = make_uint4(0, 0, 0, 0);
+      }
     }
     if (TYPE == kQ4_K && wrow < BN) {
       const uint8_t* blk = wbase + (size_t)(k0 >> 8) * 144;
@@ -191,11 +205,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_v2(const _Float16* __restri
     }
 }
 
-template <int TYPE, int BM, int BN, int WM, int WN, typename OutT>
+template <int TYPE, int BM, int BN, int WM, int WN, typename OutT, typename XT>
 static hipError_t launch_tile(const GemvArgs& a, hipStream_t stream) {
   const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM), block(WM * WN * 64);
-  hipLaunchKernelGGL((gemm_v2<TYPE, BM, BN, WM, WN, OutT>), grid, block, 0, stream,
-                     static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w),
+  hipLaunchKernelGGL((gemm_v2<TYPE, BM, BN, WM, WN, OutT, XT>), grid, block, 0, stream,
+                     static_cast<const XT*>(a.x), static_cast<const uint8_t*>(a.w),
                      static_cast<OutT*>(a.out), a.m, a.n, a.k);
   return hipGetLastError();
 }
@@ -206,8 +220,9 @@ static hipError_t launch_type(const GemvArgs& a, hipStream_t stream) {
   const hipError_t status = launch_gemm_pipe(a, stream, &handled);
   if (handled) return status;
   // 128 x 128 tiles; 256 x 128 once M is large enough to fill the chip with them
-  if (a.m >= 1024) return launch_tile<TYPE, 256, 128, 4, 2, OutT>(a, stream);
-  return launch_tile<TYPE, 128, 128, 2, 2, OutT>(a, stream);
+  if (a.x_f32) return launch_tile<TYPE, 128, 128, 2, 2, OutT, float>(a, stream);
+  if (a.m >= 1024) return launch_tile<TYPE, 256, 128, 4, 2, OutT, _Float16>(a, stream);
+  return launch_tile<TYPE, 128, 128, 2, 2, OutT, _Float16>(a, stream);
 }
 
 template <typename OutT>

@@ -91,8 +91,11 @@ struct Raw {
 // KS groups of WM x WN waves split K: group g takes steps [g S, g S + S), S = steps / KS,
 // with its own LDS staging buffers; the KS partial tiles are summed in LDS at the end
 // (KS = 1: the whole K range in one group).
-template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT>
-__global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const _Float16* __restrict__ x,
+//
+// XT = float: fp32 activations (the packed call form), rounded to fp16 as they are loaded, so
+// the staged tile is fp16(x) as in the reference's prefill numerics (benchmark.py:473-477).
+template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT, typename XT = _Float16>
+__global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restrict__ x,
                                                                const uint8_t* __restrict__ w,
                                                                OutT* __restrict__ out, int M, int N, int K) {
   using namespace pipe;
@@ -129,8 +132,18 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const _Float16* _
     for (int i = 0; i < XL; ++i) {
       const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
       // rows past M reload row M - 1: their products land in output rows that are never stored
-      const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)min(m0 + row, M - 1) * K + k0 + c8);
-      r.x[4 * i] = v.x; r.x[4 * i + 1] = v.y; r.x[4 * i + 2] = v.z; r.x[4 * i + 3] = v.w;
+      const XT* src = x + (size_t)min(m0 + row, M - 1) * K + k0 + c8;
+      if constexpr (sizeof(XT) == 4) {
+        const uint4 lo = load16(reinterpret_cast<const uint8_t*>(src));
+        const uint4 hi = load16(reinterpret_cast<const uint8_t*>(src + 4));
+        r.x[4 * i] = half2_from_fp32(__builtin_bit_cast(float, lo.x), __builtin_bit_cast(float, lo.y));
+        r.x[4 * i + 1] = half2_from_fp32(__builtin_bit_cast(float, lo.z), __builtin_bit_cast(float, lo.w));
+        r.x[4 * i + 2] = half2_from_fp32(__builtin_bit_cast(float, hi.x), __builtin_bit_cast(float, hi.y));
+        r.x[4 * i + 3] = half2_from_fp32(__builtin_bit_cast(float, hi.z), __builtin_bit_cast(float, hi.w));
+      } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(src);
+        r.x[4 * i] = v.x; r.x[4 * i + 1] = v.y; r.x[4 * i + 2] = v.z; r.x[4 * i + 3] = v.w;
+      }
     }
     const uint8_t* blk = wbase + (size_t)(k0 >> 8) * BYTES;
     if constexpr (KQ) {
@@ -298,11 +311,11 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const _Float16* _
     }
 }
 
-template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT>
+template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT, typename XT = _Float16>
 static hipError_t launch_pipe(const GemvArgs& a, hipStream_t stream) {
   const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM), block(WM * WN * 64 * KS);
-  hipLaunchKernelGGL((gemm_pipe<TYPE, BM, BN, WM, WN, KS, OutT>), grid, block, 0, stream,
-                     static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w),
+  hipLaunchKernelGGL((gemm_pipe<TYPE, BM, BN, WM, WN, KS, OutT, XT>), grid, block, 0, stream,
+                     static_cast<const XT*>(a.x), static_cast<const uint8_t*>(a.w),
                      static_cast<OutT*>(a.out), a.m, a.n, a.k);
   return hipGetLastError();
 }
@@ -318,17 +331,23 @@ static long tile_blocks(const GemvArgs& a, int bm, int bn) {
   return (long)((a.m + bm - 1) / bm) * (long)((a.n + bn - 1) / bn);
 }
 
-template <int TYPE, typename OutT>
+template <int TYPE, typename OutT, typename XT = _Float16>
 static hipError_t launch_type(const GemvArgs& a, hipStream_t stream) {
   const int steps = a.k / pipe::BK;  // a multiple of 4 (K is whole super-blocks)
-  if (tile_blocks(a, 256, 128) >= kMinBlocks) return launch_pipe<TYPE, 256, 128, 4, 2, 1, OutT>(a, stream);
+  if (tile_blocks(a, 256, 128) >= kMinBlocks) return launch_pipe<TYPE, 256, 128, 4, 2, 1, OutT, XT>(a, stream);
   if (tile_blocks(a, 128, 128) >= kMinBlocks)
-    return steps % 8 == 0 ? launch_pipe<TYPE, 128, 128, 2, 2, 2, OutT>(a, stream)
-                          : launch_pipe<TYPE, 128, 128, 2, 2, 1, OutT>(a, stream);
-  if (steps % 16 == 0) return launch_pipe<TYPE, 64, 64, 1, 2, 4, OutT>(a, stream);
-  if (steps % 8 == 0) return launch_pipe<TYPE, 64, 64, 1, 2, 2, OutT>(a, stream);
-  if (tile_blocks(a, 128, 64) >= kMinBlocks) return launch_pipe<TYPE, 128, 64, 2, 2, 1, OutT>(a, stream);
-  return launch_pipe<TYPE, 64, 64, 1, 2, 1, OutT>(a, stream);
+    return steps % 8 == 0 ? launch_pipe<TYPE, 128, 128, 2, 2, 2, OutT, XT>(a, stream)
+                          : launch_pipe<TYPE, 128, 128, 2, 2, 1, OutT, XT>(a, stream);
+  if (steps % 16 == 0) return launch_pipe<TYPE, 64, 64, 1, 2, 4, OutT, XT>(a, stream);
+  if (steps % 8 == 0) return launch_pipe<TYPE, 64, 64, 1, 2, 2, OutT, XT>(a, stream);
+  if (tile_blocks(a, 128, 64) >= kMinBlocks) return launch_pipe<TYPE, 128, 64, 2, 2, 1, OutT, XT>(a, stream);
+  return launch_pipe<TYPE, 64, 64, 1, 2, 1, OutT, XT>(a, stream);
+}
+
+template <int TYPE>
+static hipError_t launch_any(const GemvArgs& a, hipStream_t stream) {
+  if (a.x_f32) return a.out_half ? launch_type<TYPE, _Float16, float>(a, stream) : launch_type<TYPE, float, float>(a, stream);
+  return a.out_half ? launch_type<TYPE, _Float16>(a, stream) : launch_type<TYPE, float>(a, stream);
 }
 
 // Tile configuration by index, for sweeps: 0..3 the KS = 1 tiles above, 4..7 with K split
@@ -351,6 +370,7 @@ static hipError_t launch_config(const GemvArgs& a, hipStream_t stream, int confi
 }
 
 hipError_t launch_gemm_pipe_config(const GemvArgs& a, hipStream_t stream, int config) {
+  if (a.x_f32) return hipErrorInvalidValue;
   if (a.type == kQ4_K) return a.out_half ? launch_config<kQ4_K, _Float16>(a, stream, config) : launch_config<kQ4_K, float>(a, stream, config);
   if (a.type == kQ5_K) return a.out_half ? launch_config<kQ5_K, _Float16>(a, stream, config) : launch_config<kQ5_K, float>(a, stream, config);
   if (a.type == kQ6_K) return a.out_half ? launch_config<kQ6_K, _Float16>(a, stream, config) : launch_config<kQ6_K, float>(a, stream, config);
@@ -359,9 +379,9 @@ hipError_t launch_gemm_pipe_config(const GemvArgs& a, hipStream_t stream, int co
 
 hipError_t launch_gemm_pipe(const GemvArgs& a, hipStream_t stream, bool* handled) {
   *handled = true;
-  if (a.type == kQ4_K) return a.out_half ? launch_type<kQ4_K, _Float16>(a, stream) : launch_type<kQ4_K, float>(a, stream);
-  if (a.type == kQ5_K) return a.out_half ? launch_type<kQ5_K, _Float16>(a, stream) : launch_type<kQ5_K, float>(a, stream);
-  if (a.type == kQ6_K) return a.out_half ? launch_type<kQ6_K, _Float16>(a, stream) : launch_type<kQ6_K, float>(a, stream);
+  if (a.type == kQ4_K) return launch_any<kQ4_K>(a, stream);
+  if (a.type == kQ5_K) return launch_any<kQ5_K>(a, stream);
+  if (a.type == kQ6_K) return launch_any<kQ6_K>(a, stream);
   *handled = false;
   return hipSuccess;
 }

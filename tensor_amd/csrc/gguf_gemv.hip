@@ -360,8 +360,35 @@ __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
 // activations in fp32.  Consecutive lanes take consecutive groups, so one wave
 // pass covers 1024 consecutive elements of its rows; the activation group is
 // loaded once and reused for all R rows.
-template <int TYPE, int M, int R, typename OutT, bool SWIGLU = false>
-__global__ __launch_bounds__(256) void gemv_blocks(const _Float16* __restrict__ x,
+//
+// XT = float takes fp32 activations (the packed call form at M = 1): each product is then
+// the fp32 activation times the fp32 decoded weight, the reference's decode numerics
+// (benchmarks/kernels/showcase/benchmark.py:466-472), for every encoding.
+template <typename XT>
+__device__ __forceinline__ void load_x16(const XT* p, float v[16]) {
+  if constexpr (sizeof(XT) == 4) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 raw = load16(reinterpret_cast<const uint8_t*>(p + 4 * q));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[4 * q + i] = __builtin_bit_cast(float, word(raw, i));
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint4 raw = load16(reinterpret_cast<const uint8_t*>(p + 8 * h));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const half2_t pair = as_half2(word(raw, i));
+        v[8 * h + 2 * i] = (float)pair.x;
+        v[8 * h + 2 * i + 1] = (float)pair.y;
+      }
+    }
+  }
+}
+
+template <int TYPE, int M, int R, typename OutT, bool SWIGLU = false, typename XT = _Float16>
+__global__ __launch_bounds__(256) void gemv_blocks(const XT* __restrict__ x,
                                                    const uint8_t* __restrict__ w,
                                                    OutT* __restrict__ out, int n_rows, int k,
                                                    const uint8_t* __restrict__ w2 = nullptr) {
@@ -387,18 +414,7 @@ __global__ __launch_bounds__(256) void gemv_blocks(const _Float16* __restrict__ 
     const int e = 16 * g;
     float xv[M][16];
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint4 raw = load16(reinterpret_cast<const uint8_t*>(x + (size_t)m * k + e + 8 * h));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const half2_t pair = as_half2(word(raw, i));
-          xv[m][8 * h + 2 * i] = (float)pair.x;
-          xv[m][8 * h + 2 * i + 1] = (float)pair.y;
-        }
-      }
-    }
+    for (int m = 0; m < M; ++m) load_x16<XT>(x + (size_t)m * k + e, xv[m]);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (r >= rows) break;
@@ -439,6 +455,42 @@ static bool launch_blocks(const GemvArgs& a, const uint8_t* w2, hipStream_t stre
     default:
       return false;
   }
+}
+
+// fp32 activations at M = 1 (the packed call form), every encoding: gemv_blocks with the
+// shared per-element decoder, one row per wave.
+template <typename OutT>
+static hipError_t launch_f32x(const GemvArgs& a, hipStream_t stream) {
+  const float* x = static_cast<const float*>(a.x);
+  const uint8_t* w = static_cast<const uint8_t*>(a.w);
+  OutT* out = static_cast<OutT*>(a.out);
+  const dim3 grid((a.n + 3) / 4);
+  switch (a.type) {
+#define TENSOR_GGUF_F32X(T)                                                                                   \
+  case T:                                                                                                     \
+    hipLaunchKernelGGL((gemv_blocks<T, 1, 1, OutT, false, float>), grid, dim3(256), 0, stream, x, w, out, a.n, \
+                       a.k, nullptr);                                                                         \
+    break;
+    TENSOR_GGUF_F32X(kQ4_0)
+    TENSOR_GGUF_F32X(kQ4_1)
+    TENSOR_GGUF_F32X(kQ5_0)
+    TENSOR_GGUF_F32X(kQ5_1)
+    TENSOR_GGUF_F32X(kQ8_0)
+    TENSOR_GGUF_F32X(kQ2_K)
+    TENSOR_GGUF_F32X(kQ3_K)
+    TENSOR_GGUF_F32X(kQ4_K)
+    TENSOR_GGUF_F32X(kQ5_K)
+    TENSOR_GGUF_F32X(kQ6_K)
+#undef TENSOR_GGUF_F32X
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv_f32x(const GemvArgs& a, hipStream_t stream) {
+  if (a.m != 1) return hipErrorInvalidValue;
+  return a.out_half ? launch_f32x<_Float16>(a, stream) : launch_f32x<float>(a, stream);
 }
 
 // --------------------------------------------------------------- launch ---

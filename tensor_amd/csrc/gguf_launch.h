@@ -8,12 +8,15 @@
 namespace tensor_gguf {
 
 struct GemvArgs {
-  const void* x;   // fp16 [m, k]
+  const void* x;   // fp16 [m, k] (fp32 when x_f32)
   const void* w;   // raw GGUF rows [n, row_bytes]
   void* out;       // fp16 or fp32 [m, n]
   int type;        // GGML type id
   int m, n, k;
   bool out_half;
+  // fp32 activations (the packed call form): the M = 1 GEMV multiplies them in fp32, the
+  // GEMM rounds them to fp16 as it stages its activation tiles
+  bool x_f32 = false;
 };
 
 struct DequantArgs {
@@ -40,6 +43,8 @@ struct GemvGroup {
 };
 
 hipError_t launch_gemv(const GemvArgs& args, hipStream_t stream);
+// Decode GEMV of fp32 activations at M = 1, every encoding (args.x_f32).
+hipError_t launch_gemv_f32x(const GemvArgs& args, hipStream_t stream);
 // Q4_K fast paths (LDS dot2 kernel for M = 1, MFMA kernel for M >= 2); sets
 // *handled to false when the shape is not covered by them.
 hipError_t launch_gemv_q4k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);

@@ -253,9 +253,95 @@ int32_t swiglu_call(const TensorCallV1* call, TensorErrorV1* error) {
   return TENSOR_OK;
 }
 
+// A contiguous device buffer of any rank holding `items` elements of one of the allowed
+// dtypes (dtype_b == 0: any integer dtype, the raw-byte argument of the packed form).
+int32_t check_flat(const TensorArgumentV1& arg, const char* name, int ordinal, uint32_t dtype_a, uint32_t dtype_b,
+                   uint64_t bytes_wanted, TensorErrorV1* error) {
+  const TensorBufferV1& b = arg.buffer;
+  uint64_t item = 0;
+  switch (arg.dtype) {
+    case TENSOR_INT8: case TENSOR_UINT8: item = 1; break;
+    case TENSOR_INT16: case TENSOR_UINT16: case TENSOR_FLOAT16: item = 2; break;
+    case TENSOR_INT32: case TENSOR_UINT32: case TENSOR_FLOAT32: item = 4; break;
+    case TENSOR_INT64: case TENSOR_UINT64: item = 8; break;
+    default: break;
+  }
+  const bool integer = arg.dtype >= TENSOR_INT8 && arg.dtype <= TENSOR_UINT64;
+  const bool allowed = dtype_b == 0 ? integer : (arg.dtype == dtype_a || arg.dtype == dtype_b);
+  if (arg.kind != TENSOR_ARG_BUFFER || !allowed || !item || b.dtype != arg.dtype)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "%s: wrong argument kind or dtype", name);
+  if (b.device_type != TENSOR_DEVICE_ROCM || b.device_ordinal != ordinal || !b.address || b.address % 16 ||
+      b.rank < 1 || b.rank > 8 || !b.shape || !b.strides)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "%s: invalid buffer descriptor", name);
+  uint64_t bytes = item;
+  for (int axis = (int)b.rank - 1; axis >= 0; --axis) {
+    if (b.shape[axis] <= 0 || b.shape[axis] >= (int64_t)1 << 40 || b.strides[axis] != (int64_t)bytes)
+      return fail(error, TENSOR_ERROR_ARGUMENT, "%s: shape, stride or size mismatch", name);
+    bytes *= (uint64_t)b.shape[axis];
+    if (bytes > ((uint64_t)1 << 46))
+      return fail(error, TENSOR_ERROR_ARGUMENT, "%s: shape, stride or size mismatch", name);
+  }
+  if (bytes != bytes_wanted)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "%s: holds %llu bytes, the shape needs %llu", name,
+                (unsigned long long)bytes, (unsigned long long)bytes_wanted);
+  if (b.byte_size < bytes)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "%s: insufficient buffer storage", name);
+  return TENSOR_OK;
+}
+
+int32_t check_u32(const TensorArgumentV1& arg, const char* name, uint64_t* value, TensorErrorV1* error) {
+  if (arg.kind != TENSOR_ARG_SCALAR || arg.dtype != TENSOR_UINT32)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "%s: wrong argument kind or dtype", name);
+  if (arg.scalar >> 32) return fail(error, TENSOR_ERROR_ARGUMENT, "%s: noncanonical scalar payload", name);
+  *value = arg.scalar;
+  return TENSOR_OK;
+}
+
+// The packed call form: [x, w, out, type, m, n, k] with flat buffers (see tensor_hip.h).
+int32_t packed_call(const TensorCallV1* call, TensorErrorV1* error) {
+  ok(error);
+  if (int32_t s = check_call(call, 7, error)) return s;
+  const int ordinal = call->stream.device_ordinal;
+  const TensorArgumentV1* a = call->arguments;
+  Format format;
+  if (int32_t s = check_type(a[3], &format, error)) return s;
+  uint64_t m = 0, n = 0, k = 0;
+  if (int32_t s = check_u32(a[4], "m", &m, error)) return s;
+  if (int32_t s = check_u32(a[5], "n", &n, error)) return s;
+  if (int32_t s = check_u32(a[6], "k", &k, error)) return s;
+  if (!m || !n || !k || m >= (1u << 31) || n >= (1u << 31) || k >= (1u << 31) || k % format.qk)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "m, n, k: must be positive int32 with k a multiple of %d", format.qk);
+  const uint64_t x_item = a[0].dtype == TENSOR_FLOAT32 ? 4 : 2, out_item = a[2].dtype == TENSOR_FLOAT32 ? 4 : 2;
+  if (int32_t s = check_flat(a[0], "x", ordinal, TENSOR_FLOAT32, TENSOR_FLOAT16, m * k * x_item, error)) return s;
+  if (int32_t s = check_flat(a[1], "w", ordinal, TENSOR_UINT8, 0, n * (k / format.qk) * format.bytes, error)) return s;
+  if (int32_t s = check_flat(a[2], "out", ordinal, TENSOR_FLOAT32, TENSOR_FLOAT16, m * n * out_item, error)) return s;
+  if (int32_t s = check_device(call, error)) return s;
+  tensor_gguf::GemvArgs args;
+  args.x = reinterpret_cast<const void*>(a[0].buffer.address);
+  args.w = reinterpret_cast<const void*>(a[1].buffer.address);
+  args.out = reinterpret_cast<void*>(a[2].buffer.address);
+  args.type = (int)a[3].scalar;
+  args.m = (int)m;
+  args.n = (int)n;
+  args.k = (int)k;
+  args.out_half = a[2].dtype == TENSOR_FLOAT16;
+  args.x_f32 = a[0].dtype == TENSOR_FLOAT32;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
+  // the showcase's dispatch: gemv_packed for m == 1, _packed otherwise (kernels.py:114-119)
+  hipError_t status;
+  if (m == 1) status = args.x_f32 ? tensor_gguf::launch_gemv_f32x(args, stream) : tensor_gguf::launch_gemv(args, stream);
+  else status = tensor_gguf::launch_gemm(args, stream);
+  if (status != hipSuccess) return hip_fail(error, status, m == 1 ? "GGUF packed GEMV launch" : "GGUF packed GEMM launch");
+  return TENSOR_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int32_t tensor_gguf_packed_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  return packed_call(call, error);
+}
 
 int32_t tensor_gguf_gemv_swiglu_v1(const TensorCallV1* call, TensorErrorV1* error) {
   return swiglu_call(call, error);
@@ -569,6 +655,6 @@ int32_t tensor_hip_module_launch_v1(uint64_t function, const TensorCallV1* call,
   return ok(error);
 }
 
-const char* tensor_hip_version(void) { return "tensor_hip 1.3 gfx950"; }
+const char* tensor_hip_version(void) { return "tensor_hip 1.4 gfx950"; }
 
 }  // extern "C"

@@ -20,6 +20,7 @@ from tensor_amd.gguf.quant import GEOMETRY, NAMES, ggml_type
 GEMV_MAX_M = 8  # TENSOR_GGUF_GEMV_MAX_M
 
 ENTRYPOINTS = {
+    "gguf_packed": "tensor_gguf_packed_v1",
     "gguf_gemv": "tensor_gguf_gemv_v1",
     "gguf_gemm": "tensor_gguf_gemm_v1",
     "gguf_linear": "tensor_gguf_linear_v1",
@@ -44,8 +45,59 @@ def _symbols(kernel: str, count: int | None) -> tuple:
     return ("M", "N", "K")
 
 
-def manifest(kernel: str, encoding, out_dtype: str = "float16", count: int | None = None) -> dict:
+def packed_manifest(encoding, m: int, n: int, k: int, *, x_dtype: str = "float32",
+                    out_dtype: str = "float32") -> dict:
+    """The showcase's own call form, specialised on (m, n, k) as AKAS specialises its kernels
+    (``gguf(m, n, k, encoding)``, benchmarks/kernels/showcase/kernels.py:114-119): arguments
+    ``[x, w, out]`` exactly as ``benchmark.py:460-464`` builds them -- flat fp32 ``x[M*K]``,
+    the flat raw bytes of ``W``, flat fp32 ``out[M*N]`` -- with the GGML type and the shape
+    fixed as constant scalars of ``tensor_gguf_packed_v1``.  M == 1 runs the decode GEMV on
+    fp32 operands, M > 1 the prefill GEMM on fp16-rounded ones (the showcase's dispatch)."""
+    code = ggml_type(encoding)
+    qk, block = GEOMETRY[code]
+    for name, value in (("m", m), ("n", n), ("k", k)):
+        if type(value) is not int or not 1 <= value < 1 << 31:
+            raise ValueError(f"{name} must be a positive int32")
+    if k % qk:
+        raise ValueError(f"k must be a multiple of {qk} for {NAMES[code]}")
+    for name, dtype in (("x_dtype", x_dtype), ("out_dtype", out_dtype)):
+        if str(dtype) not in OUT_DTYPES:
+            raise ValueError(f"{name} must be one of {OUT_DTYPES}")
+    arguments = [
+        {"name": "x", "dtype": str(x_dtype), "shape": [m * k], "alignment": 16},
+        {"name": "w", "dtype": "uint8", "shape": [n * (k // qk) * block], "alignment": 16},
+        {"name": "out", "dtype": str(out_dtype), "shape": [m * n], "alignment": 16},
+        {"name": "type", "dtype": "uint32", "kind": "scalar"},
+        {"name": "m", "dtype": "uint32", "kind": "scalar"},
+        {"name": "n", "dtype": "uint32", "kind": "scalar"},
+        {"name": "k", "dtype": "uint32", "kind": "scalar"},
+    ]
+    return {
+        "name": f"gguf_packed:{NAMES[code]}:{m}x{n}x{k}:{x_dtype}:{out_dtype}",
+        "provider": "hip",
+        "target": "gfx950",
+        "entrypoint": ENTRYPOINTS["gguf_packed"],
+        "runtime_abi": {"major": 1, "minor": 1,
+                        "required_capabilities": ["contiguous", "executable_descriptors", "no_external_workspace",
+                                                  "scalars"]},
+        "arguments": arguments,
+        "abi": [dict(item, kind=item.get("kind", "buffer")) for item in arguments],
+        "outputs": ["out"],
+        "constants": {"type": code, "m": m, "n": n, "k": k},
+        "symbols": {},
+        "launch": {"grid": [1, 1, 1], "block": [256, 1, 1], "shared_memory_bytes": 0},
+        "ggml_type": code,
+    }
+
+
+def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | None = None, *,
+             m: int | None = None, n: int | None = None, k: int | None = None,
+             x_dtype: str | None = None) -> dict:
     """Build the manifest of one built-in GGUF executable.
+
+    With ``m``, ``n`` and ``k`` (``gguf_linear`` or ``gguf_packed`` only) the executable is
+    the showcase's shape-fixed packed form, ``packed_manifest``; ``x_dtype`` applies to it
+    only.
 
     ``gguf_gemv_group`` takes ``count`` (1..3) weight matrices that share the
     activations: arguments ``[x, w0, out0, w1, out1, ..., type]`` with row
@@ -55,8 +107,15 @@ def manifest(kernel: str, encoding, out_dtype: str = "float16", count: int | Non
     """
     if kernel not in ENTRYPOINTS:
         raise ValueError(f"unknown HIP kernel {kernel!r}; choose {', '.join(ENTRYPOINTS)}")
+    shape = (m, n, k)
+    if kernel == "gguf_packed" or any(v is not None for v in shape):
+        if kernel not in ("gguf_linear", "gguf_packed") or any(v is None for v in shape) or count is not None:
+            raise ValueError("m, n and k (all three) select the packed form of gguf_linear / gguf_packed")
+        return packed_manifest(encoding, m, n, k, x_dtype=x_dtype or "float32", out_dtype=out_dtype or "float32")
+    if x_dtype is not None:
+        raise ValueError("x_dtype applies to the packed form (m, n, k) only")
     code = ggml_type(encoding)
-    out_dtype = str(out_dtype)
+    out_dtype = str(out_dtype or "float16")
     if out_dtype not in OUT_DTYPES:
         raise ValueError(f"out_dtype must be one of {OUT_DTYPES}")
     qk, _ = GEOMETRY[code]

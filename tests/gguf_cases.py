@@ -10,16 +10,38 @@ SLAB_ROWS = 2048
 
 
 def weight(n: int, k: int, encoding, seed: int) -> np.ndarray:
-    """Raw GGUF rows [n, row_bytes].  Up to SLAB_ROWS rows are drawn from
-    N(0, 0.02) and quantized; taller matrices repeat that slab, so full-size
-    shapes (a 151936-row LM head) stay cheap to build on the host."""
+    """Raw GGUF rows [n, row_bytes] whose repeats differ in scale.
+
+    Up to SLAB_ROWS rows are drawn from N(0, 0.02) and quantized.  Taller
+    matrices repeat that slab (so a 151936-row LM head stays cheap to build on
+    the host) and then give every row its own seeded factors in [0.5, 0.9) or
+    [1.1, 1.5) on each fp16 scale field of its blocks (d, and dmin / m where the encoding has
+    one).  A kernel that reads row r +- SLAB_ROWS * j, or whose workgroup index
+    wraps, then produces output rows off by the ratio of two factors (all but
+    the ~0.5% of row pairs whose subnormal Q6_K d rounds to the same fp16)."""
     code = Q.ggml_type(encoding)
     rows = min(n, SLAB_ROWS)
     slab = Q.sample_weight(rows, k, code, seed=seed)
     if rows == n:
         return slab
     reps = -(-n // rows)
-    return np.ascontiguousarray(np.tile(slab, (reps, 1))[:n])
+    tall = np.ascontiguousarray(np.tile(slab, (reps, 1))[:n])
+    rescale_rows(tall, code, np.random.default_rng(seed + 7919))
+    return tall
+
+
+def rescale_rows(raw: np.ndarray, code: int, rng) -> None:
+    """Multiply each row's fp16 scale fields, in place, by factors drawn per row and field."""
+    qk, size = Q.GEOMETRY[code]
+    n = raw.shape[0]
+    blocks = raw.reshape(n, -1, size)
+    for offset in HALF_FIELDS[code]:
+        # at least 10% away from 1, so that the rounded fp16 field changes
+        factor = rng.uniform(0.5, 0.9, size=(n, 1)) + 0.6 * rng.integers(0, 2, size=(n, 1))
+        factor = factor.astype(np.float32)
+        field = np.ascontiguousarray(blocks[:, :, offset:offset + 2]).view(np.float16)[..., 0]
+        scaled = (field.astype(np.float32) * factor).astype(np.float16)
+        blocks[:, :, offset:offset + 2] = scaled[..., None].view(np.uint8)
 
 
 def activation(m: int, k: int, seed: int) -> np.ndarray:

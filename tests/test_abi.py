@@ -45,7 +45,8 @@ def test_library_exports_every_declared_symbol():
     assert "tensor_gguf_gemv_v1" in names and "tensor_hip_malloc" in names
     missing = [name for name in names if not hasattr(lib, name)]
     assert not missing, missing
-    assert set(_native.KERNELS) | set(_native.SERVICES) | {"tensor_hip_version", "tensor_hip_module_launch_v1"} == set(names)
+    assert set(_native.KERNELS) | set(_native.SERVICES) | {"tensor_hip_version", "tensor_hip_source_hash",
+                                                          "tensor_hip_module_launch_v1"} == set(names)
 
 
 class Call:
@@ -354,3 +355,74 @@ def test_unknown_kernel_and_encoding():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(_native.NativeLibraryError, match="not built"):
         _native.library(tmp_path / "libtensor_hip.so")
+
+
+class PackedCall:
+    """The showcase's packed call form (benchmark.py:460-464): flat fp32 x [M*K], flat raw w,
+    flat fp32 out [M*N], then type, m, n, k scalars; fake (never dereferenced) addresses."""
+
+    def __init__(self, m=1, n=1024, k=1024, type_=2, qk=32, block=18, w_dtype=3, w_item=1):
+        sizes = [(m * k, 11, 4), (n * k // qk * block // w_item, w_dtype, w_item), (m * n, 11, 4)]
+        self.keep = []
+        self.args = (abi.Argument * 7)()
+        for i, (count, dtype, item) in enumerate(sizes):
+            shp = (c.c_int64 * 1)(count)
+            strides = (c.c_int64 * 1)(item)
+            self.keep += [shp, strides]
+            self.args[i].kind = 1
+            self.args[i].dtype = dtype
+            self.args[i].buffer = abi.BufferDescriptor(0x100000 * (i + 1), count * item, shp, strides, 1, dtype, 10, 0)
+        for i, value in enumerate((type_, m, n, k)):
+            self.args[3 + i].kind = 2
+            self.args[3 + i].dtype = 7
+            self.args[3 + i].scalar = value
+        self.call = abi.CallDescriptor(1, 72, self.args, 7, 0, (c.c_uint32 * 3)(1, 1, 1),
+                                       (c.c_uint32 * 3)(256, 1, 1), 0, abi.StreamDescriptor(10, 0, 0))
+
+    def run(self):
+        error = abi.ErrorDescriptor()
+        status = _native.kernel("tensor_gguf_packed_v1")(c.byref(self.call), c.byref(error))
+        return status, error.message.decode()
+
+
+def packed(**changes):
+    call = PackedCall(**changes.pop("shape", {}))
+    for path, value in changes.items():
+        target = call
+        parts = path.split(".")
+        for part in parts[:-1]:
+            target = target[int(part)] if part.isdigit() else getattr(target, part)
+        setattr(target, parts[-1], value)
+    return call
+
+
+@pytest.mark.parametrize("mutation,code,needle", [
+    ({"call.abi_version": 2}, ERR_ABI, "ABI"),
+    ({"call.struct_size": 8}, ERR_ABI, "ABI"),
+    ({"call.argument_count": 4}, ERR_ARG, "argument count or flags"),
+    ({"call.stream.device_type": 1}, ERR_PROVIDER, "ROCm stream"),
+    ({"args.3.scalar": 9}, ERR_ARG, "unsupported GGML type"),
+    ({"args.4.scalar": 0}, ERR_ARG, "m, n, k"),
+    ({"args.6.scalar": 1000}, ERR_ARG, "m, n, k"),  # not a multiple of QK = 32
+    ({"args.5.dtype": 6}, ERR_ARG, "n: wrong argument kind or dtype"),
+    ({"args.0.dtype": 12}, ERR_ARG, "x: wrong argument kind or dtype"),
+    ({"args.0.buffer.byte_size": 4}, ERR_ARG, "x: insufficient buffer storage"),
+    ({"args.0.buffer.device_type": 1}, ERR_ARG, "x: invalid buffer descriptor"),
+    ({"args.1.dtype": 11, "args.1.buffer.dtype": 11}, ERR_ARG, "w: wrong argument kind or dtype"),
+    ({"args.2.buffer.rank": 0}, ERR_ARG, "out: invalid buffer descriptor"),
+    ({"args.5.scalar": 1023}, ERR_ARG, "w: holds"),  # the shape no longer matches w's bytes
+])
+def test_packed_form_rejects_malformed_calls(mutation, code, needle):
+    status, message = packed(**mutation).run()
+    assert status == code, message
+    assert needle in message, message
+
+
+@pytest.mark.parametrize("shape", [{}, {"m": 32}, {"type_": 12, "qk": 256, "block": 144},
+                                    {"type_": 14, "qk": 256, "block": 210, "w_dtype": 5, "w_item": 2}])
+def test_packed_form_accepts_the_showcase_call(shape):
+    """A well-formed call passes every descriptor check and reaches the device check (the
+    CPU container has no HIP device, so the status is the provider's)."""
+    status, message = PackedCall(**shape).run()
+    assert status == ERR_PROVIDER, message
+    assert "hipGetDevice" in message or "current device" in message, message

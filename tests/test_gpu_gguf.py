@@ -346,9 +346,11 @@ def test_gemm_parity_small(hip_device, encoding, m):
 
 @pytest.mark.parametrize("encoding,m,n,k", [
     ("q4_k", 512, 12288, 4096),   # C4
+    ("q4_k", 2048, 12288, 4096),  # C4 at its larger M
     ("q6_k", 256, 4096, 12288),   # C5 down at M=256
 ])
 def test_gemm_parity_baseline_shapes(hip_device, c_oracle, encoding, m, n, k):
+    """Full-size prefill shapes, every output row against the C oracle (16 threads)."""
     code = Q.ggml_type(encoding)
     note("gemm-full", encoding, m, n, k)
     raw = cases.weight(n, k, encoding, 90)
@@ -356,7 +358,100 @@ def test_gemm_parity_baseline_shapes(hip_device, c_oracle, encoding, m, n, k):
     c_oracle.set_threads(16)
     expected = c_oracle.linear(x, raw, code, n, k, prefill=True)
     got = run_linear(hip_device, "gguf_gemm", encoding, x, raw, "float16")
+    assert not np.isnan(got).any()
     assert R.relative_l2(got, expected) <= TOLERANCE
+    # row by row as well: a misplaced or skipped M tile hides in the L2 of the whole output
+    rows = np.linalg.norm(got.astype(np.float32) - expected, axis=1) / np.linalg.norm(expected, axis=1)
+    assert rows.max() <= 4 * TOLERANCE, int(rows.argmax())
+
+
+@pytest.mark.parametrize("encoding,m,n,k", [
+    ("q4_k", 512, 2304, 4096),    # 256 x 128 tiles, ragged last N tile
+    ("q6_k", 300, 1000, 12288),   # K split inside the workgroup, ragged M and N
+])
+def test_gemm_input_families_and_graph_replay(hip_device, encoding, m, n, k):
+    """The reference's prefill qualification (benchmark.py:499-555): one captured graph
+    replayed after x changes (random, the same x * -1.5, zeros), out pre-filled with NaN
+    before every replay."""
+    code = Q.ggml_type(encoding)
+    note("gemm-graph", encoding, m, n, k)
+    raw = cases.weight(n, k, encoding, 150)
+    x = cases.activation(m, k, 151)
+    exe = hip_device.load("gguf_gemm", encoding=encoding, out_dtype="float16")
+    xb, wb = hip_device.from_numpy(x), hip_device.from_numpy(raw)
+    out = hip_device.empty((m, n), "float16")
+    call = exe.bind(xb, wb, out)
+    graph = hip_device.graph(call.launch)
+    try:
+        for family, xs in (("random", x), ("fresh_scaled", (x.astype(np.float32) * -1.5).astype(np.float16)),
+                           ("zero", np.zeros_like(x))):
+            hip_device.upload(xb, xs)
+            hip_device.fill_bytes(out, 0xFF)
+            graph.replay()
+            got = out.to_numpy()
+            assert not np.isnan(got).any(), family
+            if family == "zero":
+                assert np.array_equal(got, np.zeros_like(got)), family
+            else:
+                err = R.relative_l2(got, R.gemm_reference(xs, raw, code, n, k))
+                assert err <= TOLERANCE, (family, err)
+    finally:
+        graph.close()
+        for b in (xb, wb, out):
+            b.release()
+
+
+# Qwen3-8B decoder-layer linears (C5): name, encoding, N, K, which activation they read
+C5_LAYER = (("q", "q4_k", 4096, 4096, "attn_in"), ("k", "q4_k", 1024, 4096, "attn_in"),
+            ("v", "q4_k", 1024, 4096, "attn_in"), ("o", "q4_k", 4096, 4096, "attn_out"),
+            ("gate", "q4_k", 12288, 4096, "mlp_in"), ("up", "q4_k", 12288, 4096, "mlp_in"),
+            ("down", "q6_k", 4096, 12288, "mlp_mid"))
+
+
+@pytest.mark.parametrize("m", [1, 256])
+def test_c5_layer_chained_in_one_graph(hip_device, c_oracle, m):
+    """C5: the seven linears of a Qwen3-8B decoder layer launched back to back on one
+    stream from one captured graph, replayed twice, each output against the oracle.  At
+    M = 1 the launches are the decode step's (q + k + v and gate + up grouped, since they
+    share x); at M = 256 every linear is one prefill GEMM."""
+    note("c5-layer", m)
+    c_oracle.set_threads(16)
+    widths = {"attn_in": 4096, "attn_out": 4096, "mlp_in": 4096, "mlp_mid": 12288}
+    xs = {name: cases.activation(m, width, 300 + i) for i, (name, width) in enumerate(widths.items())}
+    raws = {name: cases.weight(n, k, enc, 310 + i) for i, (name, enc, n, k, _) in enumerate(C5_LAYER)}
+    xbs = {name: hip_device.from_numpy(x) for name, x in xs.items()}
+    wbs = {name: hip_device.from_numpy(raw) for name, raw in raws.items()}
+    outs = {name: hip_device.empty((m, n), "float16") for name, _, n, _, _ in C5_LAYER}
+    calls = []
+    if m == 1:
+        qkv = hip_device.load("gguf_gemv_group", encoding="q4_k", out_dtype="float16", count=3)
+        calls.append(qkv.bind(xbs["attn_in"], wbs["q"], outs["q"], wbs["k"], outs["k"], wbs["v"], outs["v"]))
+        calls.append(hip_device.load("gguf_gemv", encoding="q4_k", out_dtype="float16")
+                     .bind(xbs["attn_out"], wbs["o"], outs["o"]))
+        pair = hip_device.load("gguf_gemv_group", encoding="q4_k", out_dtype="float16", count=2)
+        calls.append(pair.bind(xbs["mlp_in"], wbs["gate"], outs["gate"], wbs["up"], outs["up"]))
+        calls.append(hip_device.load("gguf_gemv", encoding="q6_k", out_dtype="float16")
+                     .bind(xbs["mlp_mid"], wbs["down"], outs["down"]))
+    else:
+        for name, enc, _, _, source in C5_LAYER:
+            exe = hip_device.load("gguf_gemm", encoding=enc, out_dtype="float16")
+            calls.append(exe.bind(xbs[source], wbs[name], outs[name]))
+    graph = hip_device.graph(lambda: [call.launch() for call in calls])
+    try:
+        for replay in range(2):
+            for out in outs.values():
+                hip_device.fill_bytes(out, 0xFF)
+            graph.replay()
+            for name, enc, n, k, source in C5_LAYER:
+                got = outs[name].to_numpy()
+                assert not np.isnan(got).any(), (name, replay)
+                expected = c_oracle.linear(xs[source], raws[name], Q.ggml_type(enc), n, k, prefill=m > 8)
+                err = R.relative_l2(got, expected)
+                assert err <= TOLERANCE, (name, replay, err)
+    finally:
+        graph.close()
+        for b in [*xbs.values(), *wbs.values(), *outs.values()]:
+            b.release()
 
 
 @pytest.mark.parametrize("encoding", ["q4_k", "q5_k", "q6_k"])
@@ -508,3 +603,84 @@ def test_gemv_group_pair_of_equal_matrices(hip_device, m, n, k):
             assert err <= TOLERANCE, (m, n, k, out_dtype, err)
         for b in [xb, *wbs, *outs]:
             b.release()
+
+
+# ---------------------------------------------------------- packed form --
+
+def showcase_inputs(encoding, m, n, k, seed):
+    """The showcase's GGUF data (benchmark.py:453-464): x = randn(M*K) * 0.2 in fp32, the flat
+    raw bytes of W, out fp32 [M*N]; here seeded numpy draws and this suite's quantizer."""
+    x = (np.random.default_rng(seed).standard_normal(m * k, dtype=np.float32) * np.float32(0.2))
+    raw = cases.weight(n, k, encoding, seed + 1)
+    return x, raw
+
+
+def packed_reference(c_oracle, x, raw, code, m, n, k):
+    """GEMV: fp32 x times the fp32-decoded W (benchmark.py:466-472); M > 1: fp16-rounded x and W,
+    fp32 accumulation (:473-477)."""
+    return c_oracle.linear(x.reshape(m, k), raw, code, n, k, prefill=m > 1).reshape(-1)
+
+
+@pytest.mark.parametrize("encoding", ["q4_0", "q4_k", "q6_k"])
+@pytest.mark.parametrize("m", [1, 32])
+def test_showcase_packed_call_unchanged(hip_device, c_oracle, encoding, m):
+    """The showcase's exact argument list [x fp32 (M*K,), w raw bytes (flat), out fp32 (M*N,)]
+    (benchmark.py:460-464) on an executable specialised on (m, n, k), as AKAS's is
+    (kernels.py:114-119), at the showcase's shapes N = K = 1024, M in {1, 32} (:122-126).
+    Qualified as the showcase does (benchmark.py:499-555): one captured graph replayed after
+    x changes (random, x * -1.5, zeros), out pre-filled with NaN before every replay."""
+    n = k = 1024
+    code = Q.ggml_type(encoding)
+    note("packed", encoding, m, n, k)
+    x, raw = showcase_inputs(encoding, m, n, k, 400 + m)
+    exe = hip_device.load("gguf_linear", encoding=encoding, m=m, n=n, k=k)
+    xb, wb = hip_device.from_numpy(x), hip_device.from_numpy(raw.reshape(-1))
+    out = hip_device.empty((m * n,), "float32")
+    graph = hip_device.graph(exe.bind(xb, wb, out).launch)
+    try:
+        for family, xs in (("random", x), ("fresh_scaled", x * np.float32(-1.5)), ("zero", np.zeros_like(x))):
+            hip_device.upload(xb, xs)
+            hip_device.fill_bytes(out, 0xFF)
+            graph.replay()
+            got = out.to_numpy()
+            assert not np.isnan(got).any(), family
+            expected = packed_reference(c_oracle, xs, raw, code, m, n, k)
+            if family == "zero":
+                assert np.array_equal(got, np.zeros_like(got)), family
+                continue
+            err = R.relative_l2(got, expected)
+            # fp32 operands at M = 1: only the accumulation order differs from the oracle
+            assert err <= (1e-5 if m == 1 else TOLERANCE), (family, err)
+    finally:
+        graph.close()
+        for b in (xb, wb, out):
+            b.release()
+
+
+@pytest.mark.parametrize("encoding", ENCODINGS)
+@pytest.mark.parametrize("x_dtype,m", [("float32", 1), ("float16", 1), ("float32", 5), ("float16", 40)])
+def test_packed_form_every_encoding(hip_device, c_oracle, encoding, x_dtype, m):
+    """The packed entry for every encoding: fp32 x at M = 1 runs the fp32-operand GEMV, fp16 x
+    at M = 1 the fp16 decode kernels, and M > 1 the prefill GEMM (x rounded to fp16 as it is
+    staged), each against its oracle."""
+    n, k = 300, 2048
+    code = Q.ggml_type(encoding)
+    note("packed-enc", encoding, x_dtype, m)
+    x, raw = showcase_inputs(encoding, m, n, k, 500 + m)
+    x = x.astype(x_dtype)
+    for out_dtype in ("float32", "float16"):
+        exe = hip_device.load("gguf_packed", encoding=encoding, m=m, n=n, k=k, x_dtype=x_dtype,
+                              out_dtype=out_dtype)
+        xb, wb = hip_device.from_numpy(x), hip_device.from_numpy(raw.reshape(-1))
+        out = hip_device.empty((m * n,), out_dtype)
+        hip_device.fill_bytes(out, 0xFF)
+        exe.launch(xb, wb, out)
+        got = out.to_numpy()
+        for b in (xb, wb, out):
+            b.release()
+        assert not np.isnan(got).any(), out_dtype
+        expected = packed_reference(c_oracle, x, raw, code, m, n, k)
+        err = R.relative_l2(got, expected)
+        assert err <= TOLERANCE, (out_dtype, err)
+        if m == 1 and x_dtype == "float32" and out_dtype == "float32":
+            assert err <= 1e-5, err

@@ -197,6 +197,60 @@ def check_export(session):
     buffer.release()
 
 
+def check_showcase_call(oracle):
+    """The showcase's GGUF case as benchmark.py runs it, with only the provider changed: a
+    provider session on a torch stream (benchmark.py:840-844), torch tensors
+    [x fp32 (M*K,), raw W bytes, out fp32 (M*N,)] (:453-464) imported with from_dlpack and
+    launched by a TensorCall-style list of kernels (:276-290) on an executable specialised on
+    (m, n, k), qualified by torch graph capture and replay after the input changes, with
+    NaN-filled outputs (:499-555)."""
+    import tensor_amd as tx
+
+    stream = torch.cuda.Stream()
+    with torch.inference_mode(), torch.cuda.stream(stream), \
+            tx.Device(provider="hip", stream=stream.cuda_stream) as device:
+        for encoding in (2, 12, 14):
+            for m in (1, 32):
+                n = k = 1024
+                step(f"showcase packed call encoding={encoding} M={m}")
+                raw = cases.weight(n, k, encoding, 600 + m).reshape(-1)
+                inputs = [torch.randn(m * k, device="cuda", dtype=torch.float32) * 0.2, torch.from_numpy(raw).cuda()]
+                out = torch.empty(m * n, device="cuda", dtype=torch.float32)
+                kernels = [device.load("gguf_linear", encoding=encoding, m=m, n=n, k=k)]
+                buffers = [[device.from_dlpack(t) for t in [*inputs, out]]]
+
+                def call():
+                    for kernel, args in zip(kernels, buffers):
+                        kernel.launch(*args)
+
+                call()
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=torch.cuda.current_stream()):
+                    call()
+                saved = inputs[0].clone()
+                for family in ("random", "fresh_scaled", "zero"):
+                    if family == "fresh_scaled":
+                        inputs[0].copy_(saved * -1.5)
+                    elif family == "zero":
+                        inputs[0].zero_()
+                    out.fill_(float("nan"))
+                    graph.replay()
+                    torch.cuda.synchronize()
+                    got = out.cpu().numpy()
+                    x = inputs[0].cpu().numpy().reshape(m, k)
+                    want = oracle.linear(x, raw, encoding, n, k, prefill=m > 1).reshape(-1)
+                    assert not np.isnan(got).any(), family
+                    error = R.relative_l2(got, want)
+                    assert error <= (1e-5 if m == 1 else TOLERANCE), (encoding, m, family, error)
+                del graph
+                for args in buffers:
+                    for buffer in args:
+                        buffer.release()
+                for kernel in kernels:
+                    kernel.release()
+
+
 def main():
     assert torch.cuda.is_available()
     step(f"torch {torch.__version__} hip {torch.version.hip}")
@@ -213,6 +267,7 @@ def main():
     check_linear(oracle, "q6_k", 3, 1000, 2560, "float32")
     check_compile(oracle)
     check_bundle()
+    check_showcase_call(oracle)
     session = S.session(torch.cuda.current_device())
     check_import(session)
     check_export(session)

@@ -212,6 +212,8 @@ int32_t tensor_hip_event_elapsed(float *milliseconds, uint64_t start, uint64_t s
 /* Stream capture into a graph (the reference's CudaGraph,
  * src/tensor/providers/cuda/graph.py:8-98). */
 int32_t tensor_hip_capture_begin(uint64_t stream, TensorErrorV1 *error);
+/* *graph_exec: an opaque handle of the instantiated graph (and the graph it was made from, kept
+ * until tensor_hip_graph_destroy); 0 on failure. */
 int32_t tensor_hip_capture_end(uint64_t stream, uint64_t *graph_exec, TensorErrorV1 *error);
 int32_t tensor_hip_graph_launch(uint64_t graph_exec, uint64_t stream, TensorErrorV1 *error);
 int32_t tensor_hip_graph_destroy(uint64_t graph_exec, TensorErrorV1 *error);

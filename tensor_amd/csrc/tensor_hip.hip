@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <new>
 
 #include "gguf_launch.h"
 #include "tensor_hip.h"
@@ -568,25 +569,50 @@ int32_t tensor_hip_capture_begin(uint64_t stream, TensorErrorV1* error) {
   return ok(error);
 }
 
+// A captured graph: the instantiated executable graph and the graph it was made from, which
+// lives until the executable graph is destroyed (tools that inspect a launched executable
+// graph may look its nodes up in the source graph).
+struct CapturedGraph {
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+};
+
 int32_t tensor_hip_capture_end(uint64_t stream, uint64_t* graph_exec, TensorErrorV1* error) {
+  if (!graph_exec) return fail(error, TENSOR_ERROR_ARGUMENT, "null graph result pointer");
+  *graph_exec = 0;
   hipGraph_t graph = nullptr;
   HIP_TRY(hipStreamEndCapture(reinterpret_cast<hipStream_t>(stream), &graph), "hipStreamEndCapture");
   hipGraphExec_t exec = nullptr;
   hipError_t status = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-  (void)hipGraphDestroy(graph);
-  if (status != hipSuccess) return hip_fail(error, status, "hipGraphInstantiate");
-  *graph_exec = reinterpret_cast<uint64_t>(exec);
+  if (status != hipSuccess) {
+    (void)hipGraphDestroy(graph);
+    return hip_fail(error, status, "hipGraphInstantiate");
+  }
+  CapturedGraph* captured = new (std::nothrow) CapturedGraph{graph, exec};
+  if (!captured) {
+    (void)hipGraphExecDestroy(exec);
+    (void)hipGraphDestroy(graph);
+    return fail(error, TENSOR_ERROR_PROVIDER, "out of host memory for a captured graph");
+  }
+  *graph_exec = reinterpret_cast<uint64_t>(captured);
   return ok(error);
 }
 
 int32_t tensor_hip_graph_launch(uint64_t graph_exec, uint64_t stream, TensorErrorV1* error) {
-  HIP_TRY(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), reinterpret_cast<hipStream_t>(stream)),
-          "hipGraphLaunch");
+  const CapturedGraph* captured = reinterpret_cast<const CapturedGraph*>(graph_exec);
+  if (!captured) return fail(error, TENSOR_ERROR_ARGUMENT, "null graph handle");
+  HIP_TRY(hipGraphLaunch(captured->exec, reinterpret_cast<hipStream_t>(stream)), "hipGraphLaunch");
   return ok(error);
 }
 
 int32_t tensor_hip_graph_destroy(uint64_t graph_exec, TensorErrorV1* error) {
-  HIP_TRY(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+  CapturedGraph* captured = reinterpret_cast<CapturedGraph*>(graph_exec);
+  if (!captured) return fail(error, TENSOR_ERROR_ARGUMENT, "null graph handle");
+  const hipError_t exec_status = hipGraphExecDestroy(captured->exec);
+  const hipError_t graph_status = hipGraphDestroy(captured->graph);
+  delete captured;
+  if (exec_status != hipSuccess) return hip_fail(error, exec_status, "hipGraphExecDestroy");
+  if (graph_status != hipSuccess) return hip_fail(error, graph_status, "hipGraphDestroy");
   return ok(error);
 }
 

@@ -77,6 +77,7 @@ class Device(Session):
         self._events: set = set()
         self._consumers: set = set()
         self._graphs: set = set()
+        self._capture_log = None  # list of buffers while a HipGraph capture is open
         self._generation = 0
         self._open = False
 
@@ -268,13 +269,11 @@ class Device(Session):
         )
 
     def _dispose_buffer(self, buffer: Buffer) -> None:
-        if buffer._owner is not None:
-            release = getattr(buffer._owner, "release", None)
-            if release is not None:
-                release()
-            buffer._owner = None
-        else:
+        owner = buffer._owner
+        if owner is None:
             _native.call("tensor_hip_free", buffer.pointer)
+        elif hasattr(owner, "release"):
+            owner.release()  # a borrowed DLPack producer goes back to its owner
 
     # -------------------------------------------------------- executables --
     def load(self, artifact, **options) -> Executable:
@@ -333,6 +332,8 @@ class Device(Session):
 
     def _launch(self, executable, call) -> None:
         self._check()
+        if self._capture_log is not None:
+            self._capture_log.extend(call.storage)
         error = ErrorDescriptor()
         if executable.manifest.get("kind") == "hsaco":
             status = _native.library().tensor_hip_module_launch_v1(executable.function, c.byref(call.descriptor),
@@ -376,11 +377,13 @@ class Device(Session):
         _native.call("tensor_hip_event_destroy", event.handle)
 
     # -------------------------------------------------------------- graphs --
-    def graph(self, callback):
-        """Capture the launches ``callback()`` enqueues into a replayable graph."""
+    def graph(self, callback, *, resources=()):
+        """Capture the launches ``callback()`` enqueues into a replayable graph.  The buffers of
+        every call launched during the capture, and ``resources``, are checked before each
+        replay."""
         from tensor_amd.providers.hip_graph import HipGraph
 
-        return HipGraph(self, callback)
+        return HipGraph(self, callback, resources=resources)
 
     # ------------------------------------------------------------ teardown --
     def _cleanup(self) -> None:

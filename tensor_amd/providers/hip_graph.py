@@ -1,9 +1,13 @@
-"""HIP graph capture of fixed-buffer launch plans.
+"""HIP graphs of already-bound launches (the contract of the reference's CudaGraph,
+src/tensor/providers/cuda/graph.py: capture enqueues only loaded kernels on the session
+stream; allocations, copies and host reads happen outside the capture; buffer contents may
+change between replays; a graph whose resources were released is never replayed).
 
-Same contract as the reference's CudaGraph (src/tensor/providers/cuda/graph.py:8-98):
-capture submits only already-loaded kernels on the session stream; allocation,
-copies and host reads happen outside the callback; buffer contents may change
-between replays; a replay is refused once a retained resource was released.
+Every launch the provider submits while a capture is open records the buffers its call
+retains, so a graph knows the device memory its kernels touch without being told; callers
+may add more with ``resources``.  Each replay checks that all of them are still live before
+``hipGraphLaunch``, because a kernel node replayed over freed memory would read or write
+whatever owns that memory now.
 """
 
 from __future__ import annotations
@@ -14,19 +18,30 @@ from tensor_amd import _native
 from tensor_amd._native import HipError
 
 
+def _live(buffer, generation) -> bool:
+    link = buffer
+    while link is not None:
+        if getattr(link, "_released", False) or getattr(link, "_generation", generation) != generation:
+            return False
+        link = getattr(link, "_base", None)
+    return True
+
+
 class HipGraph:
     def __init__(self, device, submit, *, resources=()):
         device._check()
         self.device = device
-        self.resources = tuple(resources)
-        self.executable = 0
-        self._closed = False
         self._generation = device._generation
+        self._closed = False
+        self.handle = 0
+        recorded = []
+        device._capture_log = recorded
         _native.call("tensor_hip_capture_begin", device.stream)
+        handle = c.c_uint64()
         try:
             submit()
         except BaseException:
-            handle = c.c_uint64()
+            device._capture_log = None
             try:
                 _native.call("tensor_hip_capture_end", device.stream, c.byref(handle))
             except HipError:
@@ -35,35 +50,37 @@ class HipGraph:
                 _native.call("tensor_hip_graph_destroy", handle.value)
             self._closed = True
             raise
-        handle = c.c_uint64()
+        device._capture_log = None
         try:
             _native.call("tensor_hip_capture_end", device.stream, c.byref(handle))
         except BaseException:
             self._closed = True
             raise
-        self.executable = handle.value
+        self.handle = handle.value
+        unique = {id(b): b for b in [*resources, *recorded]}
+        self.resources = tuple(unique.values())
         device._graphs.add(self)
 
-    def launch(self):
+    def replay(self) -> None:
+        """Launch the captured work again on the session stream."""
         self.device._check()
         if self._closed or self._generation != self.device._generation:
             raise HipError("HipGraph", 3, "HIP graph is released or belongs to an old session")
-        for resource in self.resources:
-            while resource is not None:
-                if getattr(resource, "_released", False) or getattr(resource, "_generation", self._generation) != self._generation:
-                    raise HipError("HipGraph", 3, "HIP graph references a released resource")
-                resource = getattr(resource, "_base", None)
-        _native.call("tensor_hip_graph_launch", self.executable, self.device.stream)
+        for buffer in self.resources:
+            if not _live(buffer, self._generation):
+                raise HipError("HipGraph", 3, "HIP graph references a released resource")
+        _native.call("tensor_hip_graph_launch", self.handle, self.device.stream)
 
-    replay = launch
+    launch = replay
 
-    def _dispose(self):
+    def _dispose(self) -> None:
         if not self._closed:
             self._closed = True
             self.device._graphs.discard(self)
-            _native.call("tensor_hip_graph_destroy", self.executable)
+            _native.call("tensor_hip_graph_destroy", self.handle)
 
-    def close(self):
+    def close(self) -> None:
+        """Wait for the stream, then destroy the graph and drop its resources."""
         if self._closed:
             return
         self.device._check()

@@ -1,9 +1,9 @@
-"""ctypes mirror of the C call ABI (include/tensor/abi.h) and the call builder.
+"""ctypes mirror of the C call ABI (include/tensor/abi.h) and the bound call.
 
-Layouts and ids are those of the reference's descriptors
-(src/tensor/runtime/abi.py:16-133, src/tensor/include/tensor/abi.h:37-131);
-``BoundCall`` owns the descriptor storage a provider borrows for one submission
-(src/tensor/runtime/abi.py:196-261).
+The structure layouts and ids are the reference's descriptors, byte for byte
+(src/tensor/runtime/abi.py:16-133, src/tensor/include/tensor/abi.h:37-131): they are
+the interface a provider consumes.  ``BoundCall`` holds the TensorCallV1 storage of one
+validated call, which a provider borrows for each submission.
 """
 
 from __future__ import annotations
@@ -11,7 +11,7 @@ from __future__ import annotations
 import ctypes as c
 import sys
 
-from tensor_amd.runtime.signature import SCALAR_TYPES, buffer_argument, evaluate, scalar_value
+from tensor_amd.runtime.signature import SCALAR_TYPES, scalar_value
 
 ABI_MAJOR = 1
 ABI_MINOR = 3
@@ -117,79 +117,75 @@ for _structure, _size in SIZES.items():
     assert c.sizeof(_structure) == _size, (_structure.__name__, c.sizeof(_structure))
 
 
+_HOST_OK = c.sizeof(c.c_void_p) == 8 and sys.byteorder == "little"
+
+
 def check_requirement(requirement: dict, capabilities=KNOWN_CAPABILITIES) -> None:
-    """Reject unknown major versions, newer minors and missing capabilities
-    (reference: src/tensor/runtime/abi.py:164-193)."""
-    if (
-        not isinstance(requirement, dict)
-        or set(requirement) != {"major", "minor", "required_capabilities"}
-        or type(requirement["major"]) is not int
-        or requirement["major"] != ABI_MAJOR
-        or type(requirement["minor"]) is not int
-        or not 0 <= requirement["minor"] <= ABI_MINOR
-    ):
+    """Accept a manifest's ``runtime_abi`` only for ABI major 1, a minor this runtime knows and
+    capabilities the provider has (the reference's rule, src/tensor/runtime/abi.py:164-193)."""
+    if not isinstance(requirement, dict) or sorted(requirement) != ["major", "minor", "required_capabilities"]:
         raise ValueError("unsupported Tensor runtime ABI version")
-    required = requirement["required_capabilities"]
-    if not isinstance(required, list) or any(not isinstance(n, str) for n in required) or len(set(required)) != len(required):
+    major, minor, needed = requirement["major"], requirement["minor"], requirement["required_capabilities"]
+    if type(major) is not int or major != ABI_MAJOR or type(minor) is not int or not 0 <= minor <= ABI_MINOR:
+        raise ValueError("unsupported Tensor runtime ABI version")
+    if not isinstance(needed, list) or not all(isinstance(name, str) for name in needed) \
+            or len(needed) != len(set(needed)):
         raise ValueError("invalid runtime capabilities")
-    missing = set(required) - set(capabilities)
-    if missing:
-        raise ValueError(f"missing runtime capabilities: {sorted(missing)}")
+    absent = sorted(set(needed).difference(capabilities))
+    if absent:
+        raise ValueError(f"missing runtime capabilities: {absent}")
+
+
+def _scalar_bits(value, dtype: str) -> int:
+    """The little-endian payload of a scalar argument: its value in the low bytes, zeros above."""
+    raw = bytes(SCALAR_TYPES[dtype](value))
+    return int.from_bytes(raw, "little")
 
 
 class BoundCall:
-    """Descriptor storage for one validated call, kept alive while borrowed.
+    """A validated call, packed once into TensorCallV1 storage and submitted any number of times.
 
-    Scalar arguments come from the supplied values, the manifest's
-    ``constants`` (values an executable fixes when it is loaded, such as the
-    GGML type of a GGUF kernel) or the bound dimension symbols.
+    ``values`` maps argument names to buffers and canonical scalars; a scalar the caller did not
+    pass is a manifest constant (fixed when the executable was loaded, such as a GGUF kernel's
+    GGML type) or a bound dimension of the same name.  The buffers are retained in ``storage``
+    so their descriptors stay valid while the call lives.
     """
 
-    def __init__(self, device, manifest, values, symbols, launch, *, validated=False, executable=None):
-        if c.sizeof(c.c_void_p) != 8 or sys.byteorder != "little":
-            raise ValueError("Tensor ABI 1 requires a 64-bit little-endian host")
-        abi = manifest.get("abi", [dict(item, kind="buffer") for item in manifest["arguments"]])
-        constants = manifest.get("constants", {})
-        self.storage = []
+    def __init__(self, executable, values: dict, symbols: dict, launch: dict, stream: StreamDescriptor):
+        if not _HOST_OK:
+            raise ValueError("Tensor ABI 1 needs a 64-bit little-endian host")
+        signature = executable.signature
         self.executable = executable
-        self.arguments = (Argument * len(abi))()
-        for argument, descriptor in zip(self.arguments, abi):
-            name, dtype = descriptor["name"], descriptor["dtype"]
-            argument.dtype = DTYPES[dtype]
-            if buffer_argument(descriptor):
-                value = values[name]
-                self.storage.append(value)
-                argument.kind = 1
-                argument.buffer = value._descriptor
-                continue
-            if name in values:
-                value = values[name]
-            elif name in constants:
-                value = constants[name]
+        self.storage = []
+        self.arguments = (Argument * len(signature.abi))()
+        for slot, (name, dtype, is_buffer) in zip(self.arguments, signature.abi):
+            slot.dtype = DTYPES[dtype]
+            if is_buffer:
+                buffer = values[name]
+                self.storage.append(buffer)
+                slot.kind = 1
+                slot.buffer = buffer._descriptor
             else:
-                value = evaluate({"var": name}, symbols)
-            scalar = SCALAR_TYPES[dtype](value if validated and name in values else scalar_value(value, dtype, name))
-            argument.kind = 2
-            c.memmove(c.addressof(argument) + Argument.scalar.offset, c.byref(scalar), c.sizeof(scalar))
-        self.descriptor = CallDescriptor(
-            ABI_MAJOR,
-            c.sizeof(CallDescriptor),
-            self.arguments,
-            len(abi),
-            0,
-            (c.c_uint32 * 3)(*launch["grid"]),
-            (c.c_uint32 * 3)(*launch["block"]),
-            launch["shared_memory_bytes"],
-            device.stream_descriptor(),
-        )
+                value = values[name] if name in values else signature.constants.get(name, symbols.get(name))
+                if value is None:
+                    raise ValueError(f"scalar {name} has no value")
+                slot.kind = 2
+                slot.scalar = _scalar_bits(scalar_value(value, dtype, name), dtype)
+        grid, block = (c.c_uint32 * 3)(*launch["grid"]), (c.c_uint32 * 3)(*launch["block"])
+        self.descriptor = CallDescriptor(ABI_MAJOR, c.sizeof(CallDescriptor), self.arguments, len(self.arguments),
+                                         0, grid, block, launch["shared_memory_bytes"], stream)
 
-    def launch(self):
-        """Submit again with the retained descriptors (no allocation, no re-binding)."""
-        if self.executable is None:
-            raise ValueError("bind this call through Executable.bind before submission")
-        self.executable._check()
+    @property
+    def buffers(self) -> tuple:
+        return tuple(self.storage)
+
+    def launch(self) -> None:
+        """Submit again: the descriptors are reused as they are (no allocation, no re-binding);
+        a released executable or buffer is refused before the provider sees the call."""
+        executable = self.executable
+        executable._check()
         for buffer in self.storage:
             buffer._check()
-        self.executable.device._launch(self.executable, self)
+        executable.device._launch(executable, self)
 
     __call__ = launch

@@ -1,4 +1,6 @@
-"""Provider-owned completion events (reference: src/tensor/runtime/event.py:11-51)."""
+"""Completion events on a session's stream (the reference's Event surface,
+src/tensor/runtime/event.py).  An event marks the work enqueued before it; the buffers that
+work uses stay borrowed until the host waits on it or the device is synchronized."""
 
 from __future__ import annotations
 
@@ -9,48 +11,37 @@ from tensor_amd.runtime.errors import TensorRuntimeError
 
 
 class Event:
-    """A completion point on the device's stream; buffers stay borrowed."""
-
     def __init__(self, device, handle):
-        from tensor_amd.runtime.session import _identities
-
         self.device, self.handle = device, handle
-        self._generation = device._generation
+        self._session = device._generation
         self._released = False
-        self._descriptor = EventDescriptor(
-            ABI_MAJOR,
-            c.sizeof(EventDescriptor),
-            device.device_type,
-            device.ordinal,
-            device._session_id,
-            next(_identities),
-            int("async_launch" not in device.capabilities),
-            0,
-        )
+        ticket = device._registry.ticket()
+        flags = 0 if "async_launch" in device.capabilities else 1  # TENSOR_EVENT_KNOWN_COMPLETE
+        self._descriptor = EventDescriptor(ABI_MAJOR, c.sizeof(EventDescriptor), device.device_type, device.ordinal,
+                                           device._session_id, ticket, flags, 0)
 
     @property
     def descriptor(self):
+        """A copy of the native descriptor that names this event inside its session."""
         self._check(self.device)
         return EventDescriptor.from_buffer_copy(self._descriptor)
 
-    def _check(self, device):
-        if (
-            self._released
-            or self._generation != self.device._generation
-            or device.device_type != self.device.device_type
-            or device.ordinal != self.device.ordinal
-        ):
+    def _check(self, device) -> None:
+        mine = self.device
+        if self._released or self._session != mine._generation \
+                or (device.device_type, device.ordinal) != (mine.device_type, mine.ordinal):
             raise TensorRuntimeError("event is released or belongs to a different provider/device")
-        self.device._check()
+        mine._check()
 
-    def synchronize(self):
-        """Block the host until the work recorded before this event is done."""
+    def synchronize(self) -> None:
+        """Block the host until the work recorded before this event has finished."""
         self._check(self.device)
         self.device._synchronize_event(self)
 
-    def release(self):
-        if not self._released:
-            self._check(self.device)
-            self.device._dispose_event(self)
-            self.device._events.remove(self)
-            self._released = True
+    def release(self) -> None:
+        if self._released:
+            return
+        self._check(self.device)
+        self.device._dispose_event(self)
+        self.device._events.discard(self)
+        self._released = True

@@ -1,10 +1,15 @@
-"""Scalar, symbolic-shape and launch binding for executable manifests.
+"""Executable signatures: argument slots, symbolic shapes and launch geometry.
 
-Behaviour follows the reference's provider-neutral binder
-(src/tensor/runtime/signature.py:28-216): scalars are range-checked before a
-ctypes value is built (ctypes would silently wrap), shapes may name symbols
-(``{"var": "K"}``) or bounded integer expressions (``{"op": "mul", "args":
-[...]}``), and no Python ``eval`` is ever used.
+A manifest (the reference's executable schema, src/tensor/runtime/executable.py:87-149 and
+signature.py:137-200) lists an executable's arguments -- buffers and scalars with their dtypes
+-- and gives every buffer extent as an integer, a symbol ``{"var": "K"}`` or an integer
+expression ``{"op": "mul", "args": [a, b]}`` / ``{"cast": "int32", "value": e}``.
+
+``Signature`` compiles those expressions into closures once, when an executable is loaded:
+binding a call then runs the closures instead of walking JSON, symbols are taken from the
+extents that name them directly, every other extent is checked against its expression, and
+scalars are range-checked before any ctypes value exists (ctypes would wrap them silently).
+Nothing here calls ``eval``.
 """
 
 from __future__ import annotations
@@ -12,160 +17,224 @@ from __future__ import annotations
 import ctypes
 import math
 import numbers
+import operator
+
+import numpy as np
 
 SCALAR_TYPES = {
-    "bool": ctypes.c_bool,
-    "int8": ctypes.c_int8,
-    "int16": ctypes.c_int16,
-    "int32": ctypes.c_int32,
-    "int64": ctypes.c_int64,
-    "uint8": ctypes.c_uint8,
-    "uint16": ctypes.c_uint16,
-    "uint32": ctypes.c_uint32,
-    "uint64": ctypes.c_uint64,
-    "float32": ctypes.c_float,
-    "float64": ctypes.c_double,
+    "bool": ctypes.c_bool, "int8": ctypes.c_int8, "int16": ctypes.c_int16, "int32": ctypes.c_int32,
+    "int64": ctypes.c_int64, "uint8": ctypes.c_uint8, "uint16": ctypes.c_uint16, "uint32": ctypes.c_uint32,
+    "uint64": ctypes.c_uint64, "float32": ctypes.c_float, "float64": ctypes.c_double,
 }
-INTEGER_TYPES = frozenset(SCALAR_TYPES) - {"bool", "float32", "float64"}
-OPERATIONS = {
-    "add": lambda a, b: a + b,
-    "sub": lambda a, b: a - b,
-    "mul": lambda a, b: a * b,
-    "floordiv": lambda a, b: a // b,
-    "floormod": lambda a, b: a % b,
-    "min": min,
-    "max": max,
-}
-_INT64 = (-(1 << 63), (1 << 63) - 1)
-
-
-def scalar_value(value, dtype: str, name: str):
-    """Validate a Python scalar for ``dtype``; returns the canonical value."""
-    if dtype not in SCALAR_TYPES:
-        raise ValueError(f"{name}: unsupported scalar dtype {dtype}")
-    if dtype == "bool":
-        if not isinstance(value, bool):
-            raise ValueError(f"{name} needs a bool")
-        return value
-    if dtype in INTEGER_TYPES:
-        if isinstance(value, bool) or not isinstance(value, numbers.Integral):
-            raise ValueError(f"{name} needs an integer {dtype}")
-        value = int(value)
-        bits = ctypes.sizeof(SCALAR_TYPES[dtype]) * 8
-        signed = not dtype.startswith("u")
-        low = -(1 << (bits - 1)) if signed else 0
-        high = (1 << (bits - 1)) - 1 if signed else (1 << bits) - 1
-        if not low <= value <= high:
-            raise ValueError(f"{name} is outside the {dtype} range")
-        return value
-    if isinstance(value, bool) or not isinstance(value, numbers.Real):
-        raise ValueError(f"{name} needs a real {dtype}")
-    try:
-        value = float(value)
-    except OverflowError as exc:
-        raise ValueError(f"{name} must be finite and fit {dtype}") from exc
-    converted = SCALAR_TYPES[dtype](value).value
-    if not (math.isfinite(value) and math.isfinite(converted)):
-        raise ValueError(f"{name} must be finite and fit {dtype}")
-    return converted
-
-
-def evaluate(expression, symbols: dict) -> int:
-    """Evaluate an integer expression tree against bound symbols."""
-    if type(expression) is int:
-        return expression
-    if not isinstance(expression, dict):
-        raise ValueError("invalid integer expression")
-    if set(expression) == {"var"}:
-        name = expression["var"]
-        if name not in symbols:
-            raise ValueError(f"cannot bind dimension {name}; supply a matching input or {name}=VALUE")
-        return symbols[name]
-    if set(expression) == {"cast", "value"}:
-        return scalar_value(evaluate(expression["value"], symbols), expression["cast"], "dimension cast")
-    if set(expression) != {"op", "args"} or expression["op"] not in OPERATIONS:
-        raise ValueError("invalid integer expression operation")
-    if len(expression["args"]) != 2:
-        raise ValueError("integer expressions take two operands")
-    left, right = (evaluate(value, symbols) for value in expression["args"])
-    if expression["op"] in ("floordiv", "floormod") and right == 0:
-        raise ValueError("division by zero in integer expression")
-    result = OPERATIONS[expression["op"]](left, right)
-    if not _INT64[0] <= result <= _INT64[1]:
-        raise ValueError("integer expression overflow")
-    return result
+# integer dtype -> inclusive (low, high) range
+_RANGES = {name: (int(np.iinfo(name).min), int(np.iinfo(name).max))
+           for name in SCALAR_TYPES if name not in ("bool", "float32", "float64")}
+INTEGER_TYPES = frozenset(_RANGES)
+_EXPRESSION_RANGE = _RANGES["int64"]
 
 
 def buffer_argument(descriptor: dict) -> bool:
+    """Arguments are buffers unless the manifest marks them ``"kind": "scalar"``."""
     return descriptor.get("kind", "buffer") == "buffer"
 
 
-def resolve_shape(shape: list, symbols: dict) -> tuple:
-    result = tuple(evaluate(value, symbols) for value in shape)
-    if any(value < 1 for value in result):
-        raise ValueError("buffer shape must contain positive extents")
-    return result
+def scalar_value(value, dtype: str, name: str):
+    """The canonical Python value of a scalar argument, or ValueError when it does not fit."""
+    if dtype == "bool":
+        if type(value) is not bool:
+            raise ValueError(f"{name} needs a bool")
+        return value
+    if dtype in _RANGES:
+        if isinstance(value, bool) or not isinstance(value, numbers.Integral):
+            raise ValueError(f"{name} needs an integer {dtype}")
+        low, high = _RANGES[dtype]
+        if not low <= int(value) <= high:
+            raise ValueError(f"{name} is outside the {dtype} range [{low}, {high}]")
+        return int(value)
+    if dtype not in SCALAR_TYPES:
+        raise ValueError(f"{name}: unsupported scalar dtype {dtype}")
+    if isinstance(value, bool) or not isinstance(value, numbers.Real):
+        raise ValueError(f"{name} needs a real {dtype}")
+    try:
+        as_float = float(value)
+    except OverflowError:
+        as_float = math.inf
+    stored = SCALAR_TYPES[dtype](as_float).value
+    if not (math.isfinite(as_float) and math.isfinite(stored)):
+        raise ValueError(f"{name} must be finite and representable as {dtype}")
+    return stored
+
+
+# ------------------------------------------------------------ expressions --
+
+def _checked(operation):
+    def apply(left, right):
+        if operation in (operator.floordiv, operator.mod) and right == 0:
+            raise ValueError("division by zero in a shape expression")
+        result = operation(left, right)
+        if not _EXPRESSION_RANGE[0] <= result <= _EXPRESSION_RANGE[1]:
+            raise ValueError("shape expression overflows int64")
+        return result
+    return apply
+
+
+_OPERATIONS = {"add": _checked(operator.add), "sub": _checked(operator.sub), "mul": _checked(operator.mul),
+               "floordiv": _checked(operator.floordiv), "floormod": _checked(operator.mod),
+               "min": _checked(min), "max": _checked(max)}
+
+
+def compile_expression(tree):
+    """A closure ``symbols -> int`` for one integer expression tree."""
+    if type(tree) is int:
+        return lambda symbols: tree
+    if not isinstance(tree, dict):
+        raise ValueError(f"invalid shape expression {tree!r}")
+    keys = set(tree)
+    if keys == {"var"}:
+        name = tree["var"]
+
+        def symbol(symbols):
+            try:
+                return symbols[name]
+            except KeyError:
+                raise ValueError(f"dimension {name} is not bound; pass a buffer that fixes it or {name}=VALUE") \
+                    from None
+        return symbol
+    if keys == {"cast", "value"}:
+        inner, dtype = compile_expression(tree["value"]), tree["cast"]
+        return lambda symbols: scalar_value(inner(symbols), dtype, "dimension cast")
+    if keys == {"op", "args"} and tree["op"] in _OPERATIONS and len(tree["args"]) == 2:
+        operation = _OPERATIONS[tree["op"]]
+        left, right = (compile_expression(arg) for arg in tree["args"])
+        return lambda symbols: operation(left(symbols), right(symbols))
+    raise ValueError(f"invalid shape expression {tree!r}")
+
+
+def evaluate(tree, symbols: dict) -> int:
+    return compile_expression(tree)(symbols)
+
+
+# -------------------------------------------------------------- signature --
+
+class Slot:
+    """One manifest argument: name, kind, dtype and, for buffers, compiled extents."""
+
+    __slots__ = ("name", "buffer", "dtype", "extents", "symbols", "alignment", "rank")
+
+    def __init__(self, descriptor: dict):
+        self.name, self.dtype = descriptor["name"], str(descriptor["dtype"])
+        self.buffer = buffer_argument(descriptor)
+        shape = descriptor.get("shape", ()) if self.buffer else ()
+        self.rank = len(shape)
+        self.extents = tuple(compile_expression(extent) for extent in shape)
+        # the symbol an extent names directly (None for constants and expressions)
+        self.symbols = tuple(extent["var"] if isinstance(extent, dict) and set(extent) == {"var"} else None
+                             for extent in shape)
+        self.alignment = int(descriptor.get("alignment", 256))
+
+    def shape(self, symbols: dict) -> tuple:
+        shape = tuple(extent(symbols) for extent in self.extents)
+        if any(extent < 1 for extent in shape):
+            raise ValueError(f"{self.name}: buffer extents must be positive, got {list(shape)}")
+        return shape
+
+
+class Signature:
+    """The compiled form of a manifest's arguments, symbols, limits and launch geometry."""
+
+    def __init__(self, manifest: dict):
+        self.slots = [Slot(d) for d in manifest["arguments"]]
+        self.by_name = {slot.name: slot for slot in self.slots}
+        self.symbol_types = dict(manifest.get("symbols", {}))
+        self.domains = {k: tuple(v) for k, v in manifest.get("shape_domain", {}).items()}
+        self.divisors = dict(manifest.get("shape_divisors", {}))
+        self.constants = dict(manifest.get("constants", {}))
+        self.outputs = tuple(manifest.get("outputs", ()))
+        launch = manifest["launch"]
+        self._grid = tuple(compile_expression(v) for v in launch["grid"])
+        self._block = tuple(compile_expression(v) for v in launch["block"])
+        self._shared = compile_expression(launch["shared_memory_bytes"])
+        # ABI order (defaults to the argument order)
+        self.abi = [(d["name"], str(d["dtype"]), buffer_argument(d))
+                    for d in manifest.get("abi", manifest["arguments"])]
+
+    def parameters(self, *, outputs: bool = True) -> list:
+        """Slots a caller supplies: every argument but the constants (and outputs, if asked)."""
+        return [s for s in self.slots
+                if s.name not in self.constants and (outputs or s.name not in self.outputs)]
+
+    def bind(self, supplied: dict, dimensions: dict | None = None):
+        """Derive the symbols from ``supplied`` buffers and scalars (plus explicit ``dimensions``),
+        check every buffer against its declared shape and dtype, and return ``(symbols,
+        values)`` with scalars canonicalised."""
+        dimensions = dimensions or {}
+        stray = set(dimensions) - set(self.symbol_types)
+        if stray:
+            raise ValueError(f"unknown dimensions: {sorted(stray)}")
+        symbols = {name: scalar_value(value, self.symbol_types[name], name) for name, value in dimensions.items()}
+        values = dict(supplied)
+
+        def fix(symbol, value, where):
+            known = symbols.setdefault(symbol, value)
+            if known != value:
+                raise ValueError(f"{where}: dimension {symbol} is {value}, but {known} was bound before")
+
+        for slot in self.slots:
+            if slot.name not in values:
+                continue
+            value = values[slot.name]
+            if not slot.buffer:
+                values[slot.name] = scalar_value(value, slot.dtype, slot.name)
+                if slot.name in self.symbol_types:
+                    fix(slot.name, values[slot.name], slot.name)
+                continue
+            shape, dtype = getattr(value, "shape", None), getattr(value, "dtype", None)
+            if shape is None or dtype is None:
+                raise TypeError(f"{slot.name} must be a buffer with a shape and a dtype")
+            if len(shape) != slot.rank or str(dtype) != slot.dtype:
+                raise ValueError(f"{slot.name}: expected a rank-{slot.rank} {slot.dtype} buffer, "
+                                 f"got shape {tuple(shape)} {dtype}")
+            for symbol, extent in zip(slot.symbols, shape):
+                if symbol is not None:
+                    fix(symbol, scalar_value(extent, self.symbol_types[symbol], symbol), slot.name)
+        for slot in self.slots:
+            if slot.buffer and slot.name in values:
+                wanted = slot.shape(symbols)
+                if tuple(values[slot.name].shape) != wanted:
+                    raise ValueError(f"{slot.name}: expected shape {list(wanted)} {slot.dtype}, "
+                                     f"got {list(values[slot.name].shape)}")
+        for name, (low, high) in self.domains.items():
+            if name in symbols and not low <= symbols[name] <= high:
+                raise ValueError(f"dimension {name}={symbols[name]} is outside [{low}, {high}]")
+        for name, divisor in self.divisors.items():
+            if name in symbols and symbols[name] % divisor:
+                raise ValueError(f"dimension {name}={symbols[name]} must be a multiple of {divisor}")
+        return symbols, values
+
+    def launch(self, symbols: dict) -> dict:
+        grid = [f(symbols) for f in self._grid]
+        block = [f(symbols) for f in self._block]
+        shared = self._shared(symbols)
+        if any(not 1 <= v < 1 << 31 for v in grid + block):
+            raise ValueError("launch grid and block extents must be positive int32")
+        if math.prod(block) > 1024:
+            raise ValueError("launch block exceeds 1024 threads")
+        if not 0 <= shared < 1 << 31:
+            raise ValueError("invalid dynamic shared memory size")
+        return {"grid": grid, "block": block, "shared_memory_bytes": shared}
 
 
 def bind_shapes(manifest: dict, supplied: dict, dimensions: dict | None = None):
-    """Bind direct symbols from buffer shapes, then check every buffer shape.
+    """``Signature(manifest).bind(...)`` for callers that hold a manifest only."""
+    return Signature(manifest).bind(supplied, dimensions)
 
-    Returns ``(symbols, values)`` with scalars canonicalised.
-    """
-    definitions = manifest.get("symbols", {})
-    dimensions = dimensions or {}
-    unknown = set(dimensions) - set(definitions)
-    if unknown:
-        raise ValueError(f"unknown dimensions: {sorted(unknown)}")
-    bound = {name: scalar_value(value, definitions[name], name) for name, value in dimensions.items()}
-    values = dict(supplied)
 
-    def bind(symbol, value, where):
-        if symbol in bound and bound[symbol] != value:
-            raise ValueError(f"{where}: dimension {symbol} mismatch; expected {bound[symbol]}, received {value}")
-        bound[symbol] = value
-
-    for descriptor in manifest["arguments"]:
-        name = descriptor["name"]
-        if name not in values:
-            continue
-        value = values[name]
-        if not buffer_argument(descriptor):
-            values[name] = scalar_value(value, descriptor["dtype"], name)
-            if name in definitions:
-                bind(name, values[name], name)
-            continue
-        if not hasattr(value, "shape") or not hasattr(value, "dtype"):
-            raise TypeError(f"{name} must be a buffer with shape and dtype")
-        if len(value.shape) != len(descriptor["shape"]) or str(value.dtype) != descriptor["dtype"]:
-            raise ValueError(f"{name} needs shape {descriptor['shape']} and dtype {descriptor['dtype']}")
-        for extent, actual in zip(descriptor["shape"], value.shape):
-            if isinstance(extent, dict) and set(extent) == {"var"}:
-                symbol = extent["var"]
-                bind(symbol, scalar_value(actual, definitions[symbol], symbol), name)
-    for descriptor in manifest["arguments"]:
-        name = descriptor["name"]
-        if name in values and buffer_argument(descriptor):
-            expected = resolve_shape(descriptor["shape"], bound)
-            if tuple(values[name].shape) != expected:
-                raise ValueError(f"{name} needs shape {list(expected)} and dtype {descriptor['dtype']}")
-    for name, (low, high) in manifest.get("shape_domain", {}).items():
-        if name in bound and not low <= bound[name] <= high:
-            raise ValueError(f"dimension {name}={bound[name]} is outside [{low}, {high}]")
-    for name, divisor in manifest.get("shape_divisors", {}).items():
-        if name in bound and bound[name] % divisor:
-            raise ValueError(f"dimension {name}={bound[name]} must be a multiple of {divisor}")
-    return bound, values
+def resolve_shape(shape, symbols: dict) -> tuple:
+    result = tuple(compile_expression(extent)(symbols) for extent in shape)
+    if any(extent < 1 for extent in result):
+        raise ValueError(f"buffer extents must be positive, got {list(result)}")
+    return result
 
 
 def resolve_launch(launch: dict, symbols: dict) -> dict:
-    result = {name: [evaluate(value, symbols) for value in launch[name]] for name in ("grid", "block")}
-    result["shared_memory_bytes"] = evaluate(launch["shared_memory_bytes"], symbols)
-    for name in ("grid", "block"):
-        if any(value < 1 or value > (1 << 31) - 1 for value in result[name]):
-            raise ValueError(f"launch {name} exceeds positive int32 dimensions")
-    if math.prod(result["block"]) > 1024:
-        raise ValueError("launch block exceeds 1024 threads")
-    if not 0 <= result["shared_memory_bytes"] <= (1 << 31) - 1:
-        raise ValueError("invalid shared memory size")
-    return result
+    return Signature({"arguments": [], "launch": launch}).launch(symbols)

@@ -19,7 +19,7 @@ import pytest
 from tensor_amd import _native
 from tensor_amd.gguf import kernels
 from tensor_amd.runtime import abi
-from tensor_amd.runtime.signature import bind_shapes
+from tensor_amd.runtime.signature import Signature, bind_shapes
 
 ROOT = Path(__file__).resolve().parents[1]
 OK, ERR_ABI, ERR_ARG, ERR_PROVIDER = 0, 1, 2, 3
@@ -335,7 +335,8 @@ def test_bound_call_carries_constant_type_scalar():
         buffers[name] = b
     symbols, values = bind_shapes(manifest, buffers)
     launch = {"grid": [1, 1, 1], "block": [256, 1, 1], "shared_memory_bytes": 0}
-    call = abi.BoundCall(device, manifest, values, symbols, launch, validated=True)
+    executable = SimpleNamespace(signature=Signature(manifest), device=device)
+    call = abi.BoundCall(executable, values, symbols, launch, device.stream_descriptor())
     assert [a.kind for a in call.arguments] == [1, 1, 1, 2]
     assert call.arguments[3].dtype == abi.DTYPES["uint32"] and call.arguments[3].scalar == 14
     assert call.descriptor.stream.device_type == 10

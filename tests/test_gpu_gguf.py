@@ -314,6 +314,39 @@ def test_gemv_input_families_and_graph_replay(hip_device, encoding):
             b.release()
 
 
+def test_graph_replay_refused_once_a_captured_buffer_is_released(hip_device):
+    """A graph records the buffers of every call launched while it was captured (here through
+    a lambda, so nothing is passed explicitly) and refuses to replay once one is released."""
+    from tensor_amd._native import HipError
+
+    note("graph-resources")
+    raw, x = cases.weight(64, 256, "q4_k", 5), cases.activation(1, 256, 6)
+    exe = hip_device.load("gguf_gemv", encoding="q4_k", out_dtype="float32")
+    xb, wb = hip_device.from_numpy(x), hip_device.from_numpy(raw)
+    out = hip_device.empty((1, 64), "float32")
+    call = exe.bind(xb, wb, out)
+    graph = hip_device.graph(lambda: call.launch())
+    assert {id(b) for b in graph.resources} == {id(xb), id(wb), id(out)}
+    graph.replay()
+    expected = out.to_numpy()
+    assert R.relative_l2(expected, R.gemv_reference(x, raw, Q.Q4_K, 64, 256)) <= TOLERANCE
+    out.release()
+    with pytest.raises(HipError, match="released resource"):
+        graph.replay()
+    out2 = hip_device.empty((1, 64), "float32")
+    view = wb.view((64 * 144,))
+    other = hip_device.graph(exe.bind(xb, wb, out2).launch, resources=(view,))
+    other.replay()
+    assert np.array_equal(out2.to_numpy(), expected)
+    wb.release()  # releasing the base invalidates the base and the view the graph holds
+    with pytest.raises(HipError, match="released resource"):
+        other.replay()
+    for g in (graph, other):
+        g.close()
+    for b in (xb, out2):
+        b.release()
+
+
 def test_linear_dispatch_matches_both_kernels(hip_device):
     n, k = 256, 1024
     raw = cases.weight(n, k, "q4_k", 60)

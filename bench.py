@@ -218,6 +218,30 @@ class SwigluLinear:
             b.release()
 
 
+class GroupGemm:
+    """Prefill GEMM of matrices sharing one activation input (gguf_gemm_group), rotated weight
+    copies, on a workspace the caller provides (shared by launches that run one at a time)."""
+
+    def __init__(self, device, encoding, m, k, rows, out_dtype, copies, seed, workspace):
+        from tests import gguf_cases as cases
+
+        self.weights = [rotated(device, cases.weight(n, k, encoding, seed + i), copies) for i, n in enumerate(rows)]
+        self.x = device.from_numpy(cases.activation(m, k, seed + 10))
+        self.outs = [device.empty((m, n), out_dtype) for n in rows]
+        exe = device.load("gguf_gemm_group", encoding=encoding, out_dtype=out_dtype, count=len(rows))
+        self.calls = []
+        for c in range(copies):
+            args = [self.x]
+            for ws, out in zip(self.weights, self.outs):
+                args += [ws[c], out]
+            self.calls.append(exe.bind(*args, workspace))
+        self.flops = sum(2 * m * n * k for n in rows)
+
+    def release(self):
+        for b in [w for ws in self.weights for w in ws] + self.outs + [self.x]:
+            b.release()
+
+
 def rotated_launches(linears, steps):
     """``steps`` passes over the linears, each pass using the next weight copy."""
     return [layer.calls[step % len(layer.calls)].launch for step in range(steps) for layer in linears]
@@ -553,8 +577,32 @@ def detail_cases(device):
               ("o", "q4_k", 4096, 4096), ("gate", "q4_k", 12288, 4096), ("up", "q4_k", 12288, 4096),
               ("down", "q6_k", 4096, 12288)]
     layer_weights = sum(weight_bytes(e, n, k) for _, e, n, k in shapes)
+    @add("C5_layer_m256")
+    def layer_prefill():
+        # the prefill step: q + k + v and gate + up as grouped GEMMs, o, then down, each on the
+        # plan the library picks (K split across workgroups for q + k + v and the Q6_K down)
+        m = 256
+        groups = [("qkv", "q4_k", 4096, [4096, 1024, 1024]), ("o", "q4_k", 4096, [4096]),
+                  ("gate_up", "q4_k", 4096, [12288, 12288]), ("down", "q6_k", 12288, [4096])]
+        need = max(device.gemm_workspace(e, m, k, rows) for _, e, k, rows in groups)
+        workspace = device.empty((max(need, 256),), "uint8")
+        layers = [GroupGemm(device, e, m, k, rows, "float16", 2, 30 + 5 * i, workspace)
+                  for i, (_, e, k, rows) in enumerate(groups)]
+        stats = time_launches(device, rotated_launches(layers, 4), per=4)
+        result = dict(stats, **rate(stats, sum(layer.flops for layer in layers), "TFLOP/s"), launches=len(layers),
+                      workspace_bytes=need)
+        result["mfma_frac"] = round(result["TFLOP/s"] / FP16_PEAK_TFLOPS, 4)
+        result["per_group_us"] = {}
+        for (name, *_), layer in zip(groups, layers):
+            one = time_launches(device, [layer.calls[i % 2].launch for i in range(10)], per=10)
+            result["per_group_us"][name] = one["median_us"]
+        for layer in layers:
+            layer.release()
+        workspace.release()
+        return result
+
     for m, kernel in ((1, "gguf_gemv"), (256, "gguf_gemm")):
-        @add(f"C5_layer_m{m}")
+        @add(f"C5_layer_m{m}" if m == 1 else "C5_layer_m256_seven_launches")
         def layer_chain(m=m, kernel=kernel):
             copies = copies_for(layer_weights) if m == 1 else 2
             layers = [Linear(device, kernel, e, m, n, k, "float16", copies, 20 + i)

@@ -119,6 +119,32 @@ int32_t tensor_gguf_packed_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 int32_t tensor_gguf_gemv_group_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 
 /*
+ * Grouped prefill GEMM: out_i[m, n] = sum_k fp16(x[m, k]) * fp16(dequant(W_i)[n, k]), fp32
+ * accumulate, for 1 <= c <= TENSOR_GGUF_GEMM_GROUP_MAX matrices that share x and K (a layer's
+ * q, k and v, or gate and up) in one launch.  No counterpart in the reference, where each linear
+ * is its own _packed launch (benchmarks/kernels/showcase/kernels.py:114-119).  When the shape
+ * leaves most CUs idle, K is split across workgroups: each writes fp32 partial sums into the
+ * workspace and a second kernel adds them in split order (deterministic) and converts; the
+ * split is chosen to fit the workspace given (any size; a short one only limits the split).
+ * Q4_K, Q5_K and Q6_K use the pipelined kernel; the other encodings take the generic GEMM,
+ * one launch per matrix.  Arguments, in order:
+ *   0        x         buffer fp16  [M, K]
+ *   2i+1     w_i       buffer uint8 [N_i, K/QK*BLOCK]
+ *   2i+2     out_i     buffer [M, N_i], one dtype (fp16 or fp32) for all i
+ *   2c+1     workspace buffer uint8 [bytes], 256-byte aligned (device scratch, clobbered)
+ *   2c+2     type      scalar uint32 GGML type id, shared by the group
+ */
+#define TENSOR_GGUF_GEMM_GROUP_MAX 3
+int32_t tensor_gguf_gemm_group_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/*
+ * Workspace bytes tensor_gguf_gemm_group_v1 would use for this shape (0: it does not split K):
+ * n[0 .. count-1] are the matrices' row counts.
+ */
+int32_t tensor_gguf_gemm_workspace_v1(uint32_t type, int64_t m, int64_t k, const int64_t *n, uint32_t count,
+                                      uint64_t *bytes, TensorErrorV1 *error);
+
+/*
  * Decode GEMV of an MLP's gate and up projections with the SwiGLU epilogue:
  * out[m, n] = silu(g) * u, silu(g) = g / (1 + exp(-g)), where g and u are the
  * fp32 sums x[m, :] . dequant(W_gate)[n, :] and x[m, :] . dequant(W_up)[n, :]

@@ -18,6 +18,7 @@ LIBRARY = Path(__file__).resolve().parent / "libtensor_hip.so"
 # Kernel entry points (TensorKernelV1 shape).
 KERNELS = (
     "tensor_gguf_packed_v1",
+    "tensor_gguf_gemm_group_v1",
     "tensor_gguf_gemv_v1",
     "tensor_gguf_gemm_v1",
     "tensor_gguf_linear_v1",
@@ -79,6 +80,8 @@ SERVICES = {
     "tensor_hip_module_load": [c.c_void_p, _u64, c.POINTER(_u64)],
     "tensor_hip_module_function": [_u64, c.c_char_p, c.POINTER(_u64)],
     "tensor_hip_module_unload": [_u64],
+    "tensor_gguf_gemm_workspace_v1": [c.c_uint32, c.c_int64, c.c_int64, c.POINTER(c.c_int64), c.c_uint32,
+                                      c.POINTER(_u64)],
 }
 
 

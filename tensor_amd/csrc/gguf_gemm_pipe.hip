@@ -24,6 +24,8 @@
 //   Q6_K (triton_kernels.py:163-180): a step covers quarters 2(s%2), 2(s%2)+1
 //     of half h = (s%4)/2: the 64 low-nibble bytes of ql for that half (nibble
 //     s%2), the 32 qh bytes of the half (2 bits per quarter) and 4 scales.
+#include <algorithm>
+
 #include "gguf_common.h"
 #include "gguf_launch.h"
 
@@ -92,12 +94,16 @@ struct Raw {
 // with its own LDS staging buffers; the KS partial tiles are summed in LDS at the end
 // (KS = 1: the whole K range in one group).
 //
+// One launch covers the matrices of a GemmJob (they share x and K): blockIdx.x runs over the
+// BN-wide column tiles of all of them in order.  With job.splits > 1, blockIdx.z also splits
+// K across workgroups: workgroup z takes its split's range of steps and stores its fp32
+// partial tile to job.partial, and gemm_reduce adds the splits in order.
+//
 // XT = float: fp32 activations (the packed call form), rounded to fp16 as they are loaded, so
 // the staged tile is fp16(x) as in the reference's prefill numerics (benchmark.py:473-477).
 template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT, typename XT = _Float16>
-__global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restrict__ x,
-                                                               const uint8_t* __restrict__ w,
-                                                               OutT* __restrict__ out, int M, int N, int K) {
+__global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restrict__ x, const GemmJob job,
+                                                               int M, int K) {
   using namespace pipe;
   constexpr int THREADS = WM * WN * 64;  // per K group
   constexpr int MT = BM / WM / 16, NT = BN / WN / 16;
@@ -120,11 +126,17 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
 
   const int tid = threadIdx.x % THREADS, lane = tid & 63, wave = tid >> 6;
   const int wm = (wave / WN) * (16 * MT), wn = (wave % WN) * (16 * NT);
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  // the matrix of this column tile (workgroup-uniform)
+  const int tile = blockIdx.x;
+  const int mi = tile < job.tile_end[0] ? 0 : tile < job.tile_end[1] ? 1 : 2;
+  const int N = job.n[mi];
+  const int m0 = blockIdx.y * BM, n0 = (tile - (mi ? job.tile_end[mi - 1] : 0)) * BN;
   const int wrow = tid / TPR, wpart = tid % TPR;
-  const uint8_t* wbase = w + (size_t)min(n0 + wrow, N - 1) * (size_t)(K >> 8) * BYTES;
-  // this group's steps; the host guarantees steps % (4 KS) == 0, so each group starts on a super-block
-  const int steps = K / BK / KS, first = group * steps;
+  const uint8_t* wbase = job.w[mi] + (size_t)min(n0 + wrow, N - 1) * (size_t)(K >> 8) * BYTES;
+  // this group's steps of this split; the host guarantees steps % (4 KS splits) == 0, so every
+  // group starts on a super-block
+  const int split_steps = K / BK / job.splits;
+  const int steps = split_steps / KS, first = blockIdx.z * split_steps + group * steps;
 
   auto load = [&](RawT& r, int step) {
     const int k0 = step * BK;
@@ -298,6 +310,9 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[i][j][e] += red[(((g - 1) * MT + i) * NT + j) * 4 * THREADS + e * THREADS + tid];
   }
+  const bool split = job.splits > 1;
+  OutT* const out = static_cast<OutT*>(job.out[mi]);
+  float* const part = split ? job.partial + (size_t)blockIdx.z * M * job.n_total + job.col0[mi] : nullptr;
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -306,84 +321,200 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int row = m0 + wm + 16 * i + 4 * (lane >> 4) + e;
-        if (row < M && col < N) store_out<OutT>(out, (size_t)row * N + col, acc[i][j][e]);
+        if (row < M && col < N) {
+          if (split) part[(size_t)row * job.n_total + col] = acc[i][j][e];
+          else store_out<OutT>(out, (size_t)row * N + col, acc[i][j][e]);
+        }
       }
     }
 }
 
-template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT, typename XT = _Float16>
-static hipError_t launch_pipe(const GemvArgs& a, hipStream_t stream) {
-  const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM), block(WM * WN * 64 * KS);
+// out_i[row, c] = the sum of the splits' partial sums, added in split order (so the result does
+// not depend on which workgroup finished first), converted once to the output type.
+template <typename OutT>
+__global__ __launch_bounds__(256) void gemm_reduce(const GemmJob job, int M) {
+  const size_t total = (size_t)M * job.n_total, plane = total;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (size_t)gridDim.x * 256) {
+    const int row = (int)(e / job.n_total), col = (int)(e % job.n_total);
+    float sum = job.partial[e];
+    for (int z = 1; z < job.splits; ++z) sum += job.partial[z * plane + e];
+    const int mi = job.count > 1 && col >= job.col0[1] ? (job.count > 2 && col >= job.col0[2] ? 2 : 1) : 0;
+    store_out<OutT>(static_cast<OutT*>(job.out[mi]), (size_t)row * job.n[mi] + (col - job.col0[mi]), sum);
+  }
+}
+
+namespace {
+
+// Workgroup tiles of the pipelined GEMM, by index: 0..3 without a K split inside the workgroup,
+// 4..7 with two or four wave groups per workgroup (LDS holds one double-buffered stage per
+// group, so 128 x 128 and 128 x 64 take KS <= 2 and 64 x 64 KS <= 4).
+struct Tile {
+  int bm, bn, ks;
+};
+constexpr Tile kTiles[8] = {{256, 128, 1}, {128, 128, 1}, {128, 64, 1}, {64, 64, 1},
+                            {128, 128, 2}, {128, 64, 2}, {64, 64, 2}, {64, 64, 4}};
+
+long tile_count(const GemmGroupArgs& a, const Tile& t) {
+  long columns = 0;
+  for (int i = 0; i < a.count; ++i) columns += (a.n[i] + t.bn - 1) / t.bn;
+  return (long)((a.m + t.bm - 1) / t.bm) * columns;
+}
+
+int total_columns(const GemmGroupArgs& a) {
+  int n = 0;
+  for (int i = 0; i < a.count; ++i) n += a.n[i];
+  return n;
+}
+
+// The job of one launch: per-matrix column tiles and partial-sum columns.
+GemmJob make_job(const GemmGroupArgs& a, const Tile& t, int splits, void* workspace) {
+  GemmJob job{};
+  int tiles = 0, col = 0;
+  for (int i = 0; i < kGemmGroupMax; ++i) {
+    if (i < a.count) {
+      job.w[i] = static_cast<const uint8_t*>(a.w[i]);
+      job.out[i] = a.out[i];
+      job.n[i] = a.n[i];
+      tiles += (a.n[i] + t.bn - 1) / t.bn;
+      job.col0[i] = col;
+      col += a.n[i];
+    } else {
+      job.col0[i] = col;  // past the last matrix: never selected
+    }
+    job.tile_end[i] = tiles;
+  }
+  job.count = a.count;
+  job.n_total = col;
+  job.splits = splits;
+  job.partial = static_cast<float*>(workspace);
+  return job;
+}
+
+template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT, typename XT>
+hipError_t launch_pipe(const GemmGroupArgs& a, int splits, void* workspace, hipStream_t stream) {
+  const GemmJob job = make_job(a, Tile{BM, BN, KS}, splits, workspace);
+  const dim3 grid(job.tile_end[kGemmGroupMax - 1], (a.m + BM - 1) / BM, splits), block(WM * WN * 64 * KS);
   hipLaunchKernelGGL((gemm_pipe<TYPE, BM, BN, WM, WN, KS, OutT, XT>), grid, block, 0, stream,
-                     static_cast<const XT*>(a.x), static_cast<const uint8_t*>(a.w),
-                     static_cast<OutT*>(a.out), a.m, a.n, a.k);
+                     static_cast<const XT*>(a.x), job, a.m, a.k);
+  if (splits > 1) {
+    const size_t total = (size_t)a.m * job.n_total;
+    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL((gemm_reduce<OutT>), dim3(blocks), dim3(256), 0, stream, job, a.m);
+  }
   return hipGetLastError();
 }
 
-// Largest tile that still gives the 256 CUs work: the workgroup count of a
-// tile must reach kMinBlocks, else a smaller tile is taken, and below 256 x 128
-// the K range is split over two or four wave groups of one workgroup so that
-// every SIMD holds at least one wave (measured at M = 256: 1.4x to 4x faster
-// than the unsplit tiles for the q/k/v/o, gate/up and down shapes).
-constexpr long kMinBlocks = 160;
-
-static long tile_blocks(const GemvArgs& a, int bm, int bn) {
-  return (long)((a.m + bm - 1) / bm) * (long)((a.n + bn - 1) / bn);
-}
-
-template <int TYPE, typename OutT, typename XT = _Float16>
-static hipError_t launch_type(const GemvArgs& a, hipStream_t stream) {
-  const int steps = a.k / pipe::BK;  // a multiple of 4 (K is whole super-blocks)
-  if (tile_blocks(a, 256, 128) >= kMinBlocks) return launch_pipe<TYPE, 256, 128, 4, 2, 1, OutT, XT>(a, stream);
-  if (tile_blocks(a, 128, 128) >= kMinBlocks)
-    return steps % 8 == 0 ? launch_pipe<TYPE, 128, 128, 2, 2, 2, OutT, XT>(a, stream)
-                          : launch_pipe<TYPE, 128, 128, 2, 2, 1, OutT, XT>(a, stream);
-  if (steps % 16 == 0) return launch_pipe<TYPE, 64, 64, 1, 2, 4, OutT, XT>(a, stream);
-  if (steps % 8 == 0) return launch_pipe<TYPE, 64, 64, 1, 2, 2, OutT, XT>(a, stream);
-  if (tile_blocks(a, 128, 64) >= kMinBlocks) return launch_pipe<TYPE, 128, 64, 2, 2, 1, OutT, XT>(a, stream);
-  return launch_pipe<TYPE, 64, 64, 1, 2, 1, OutT, XT>(a, stream);
-}
-
-template <int TYPE>
-static hipError_t launch_any(const GemvArgs& a, hipStream_t stream) {
-  if (a.x_f32) return a.out_half ? launch_type<TYPE, _Float16, float>(a, stream) : launch_type<TYPE, float, float>(a, stream);
-  return a.out_half ? launch_type<TYPE, _Float16>(a, stream) : launch_type<TYPE, float>(a, stream);
-}
-
-// Tile configuration by index, for sweeps: 0..3 the KS = 1 tiles above, 4..7 with K split
-// (LDS holds one double-buffered stage per group: 128 x 128 and 128 x 64 take KS <= 2, 64 x 64 KS <= 4).
-template <int TYPE, typename OutT>
-static hipError_t launch_config(const GemvArgs& a, hipStream_t stream, int config) {
-  const int steps = a.k / pipe::BK;
-  auto ks_ok = [&](int ks) { return steps % (4 * ks) == 0; };
-  switch (config) {
-    case 0: return launch_pipe<TYPE, 256, 128, 4, 2, 1, OutT>(a, stream);
-    case 1: return launch_pipe<TYPE, 128, 128, 2, 2, 1, OutT>(a, stream);
-    case 2: return launch_pipe<TYPE, 128, 64, 2, 2, 1, OutT>(a, stream);
-    case 3: return launch_pipe<TYPE, 64, 64, 1, 2, 1, OutT>(a, stream);
-    case 4: return ks_ok(2) ? launch_pipe<TYPE, 128, 128, 2, 2, 2, OutT>(a, stream) : hipErrorInvalidValue;
-    case 5: return ks_ok(2) ? launch_pipe<TYPE, 128, 64, 2, 2, 2, OutT>(a, stream) : hipErrorInvalidValue;
-    case 6: return ks_ok(2) ? launch_pipe<TYPE, 64, 64, 1, 2, 2, OutT>(a, stream) : hipErrorInvalidValue;
-    case 7: return ks_ok(4) ? launch_pipe<TYPE, 64, 64, 1, 2, 4, OutT>(a, stream) : hipErrorInvalidValue;
+template <int TYPE, typename OutT, typename XT>
+hipError_t launch_tile(const GemmGroupArgs& a, int tile, int splits, void* workspace, hipStream_t stream) {
+  switch (tile) {
+    case 0: return launch_pipe<TYPE, 256, 128, 4, 2, 1, OutT, XT>(a, splits, workspace, stream);
+    case 1: return launch_pipe<TYPE, 128, 128, 2, 2, 1, OutT, XT>(a, splits, workspace, stream);
+    case 2: return launch_pipe<TYPE, 128, 64, 2, 2, 1, OutT, XT>(a, splits, workspace, stream);
+    case 3: return launch_pipe<TYPE, 64, 64, 1, 2, 1, OutT, XT>(a, splits, workspace, stream);
+    case 4: return launch_pipe<TYPE, 128, 128, 2, 2, 2, OutT, XT>(a, splits, workspace, stream);
+    case 5: return launch_pipe<TYPE, 128, 64, 2, 2, 2, OutT, XT>(a, splits, workspace, stream);
+    case 6: return launch_pipe<TYPE, 64, 64, 1, 2, 2, OutT, XT>(a, splits, workspace, stream);
+    case 7: return launch_pipe<TYPE, 64, 64, 1, 2, 4, OutT, XT>(a, splits, workspace, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
+template <int TYPE>
+hipError_t launch_typed(const GemmGroupArgs& a, int tile, int splits, void* workspace, hipStream_t stream) {
+  if (a.x_f32)
+    return a.out_half ? launch_tile<TYPE, _Float16, float>(a, tile, splits, workspace, stream)
+                      : launch_tile<TYPE, float, float>(a, tile, splits, workspace, stream);
+  return a.out_half ? launch_tile<TYPE, _Float16, _Float16>(a, tile, splits, workspace, stream)
+                    : launch_tile<TYPE, float, _Float16>(a, tile, splits, workspace, stream);
+}
+
+bool pipe_type(int type) { return type == kQ4_K || type == kQ5_K || type == kQ6_K; }
+
+// A tile and split count that fit the shape: the steps of a split divide evenly into the
+// workgroup's wave groups, each starting on a super-block.
+bool valid_plan(const GemmGroupArgs& a, int tile, int splits) {
+  const int steps = a.k / pipe::BK;
+  return tile >= 0 && tile < 8 && splits >= 1 && steps % (4 * kTiles[tile].ks * splits) == 0;
+}
+
+// Largest tile that still gives the 256 CUs work: the workgroup count of a tile must reach
+// kMinBlocks, else a smaller tile is taken, and below 256 x 128 the K range is split over two
+// or four wave groups of one workgroup so that every SIMD holds at least one wave (measured at
+// M = 256: 1.4x to 4x faster than the unsplit tiles for the q/k/v/o, gate/up and down shapes).
+constexpr long kMinBlocks = 160;
+
+int base_tile(const GemmGroupArgs& a) {
+  const int steps = a.k / pipe::BK;  // a multiple of 4 (K is whole super-blocks)
+  if (tile_count(a, kTiles[0]) >= kMinBlocks) return 0;
+  if (tile_count(a, kTiles[1]) >= kMinBlocks) return steps % 8 == 0 ? 4 : 1;
+  if (steps % 16 == 0) return 7;
+  if (steps % 8 == 0) return 6;
+  if (tile_count(a, kTiles[2]) >= kMinBlocks) return 2;
+  return 3;
+}
+
+}  // namespace
+
+GemmPlan plan_gemm_group(const GemmGroupArgs& a, size_t workspace_bytes) {
+  GemmPlan plan{base_tile(a), 1};
+  if (!pipe_type(a.type)) return plan;
+  // Split K across workgroups with the 256 x 128 tile when that tile alone leaves most CUs
+  // idle and the small tiles are no better: when even 64 x 64 tiles need more than one round
+  // of 256 workgroups, or K is long (>= 8192).  Measured at M = 256 (q + k + v grouped 68 ->
+  // 34 us with 4 splits, the Q6_K down 4096 x 12288 90 -> 54 us with 8); the 4096 x 4096 o
+  // projection stays on 64 x 64 tiles (25 us against 30 split).  Splits double while the grid
+  // stays within 256 workgroups and each split keeps >= 8 steps (512 of K).
+  const long tiles = tile_count(a, kTiles[0]);
+  const bool big_tile = plan.tile == 0 || plan.tile == 1 || plan.tile == 4;  // already fills the CUs
+  const bool crowded = tile_count(a, kTiles[3]) > 256 || a.k >= 8192;
+  if (a.m < 192 || big_tile || !crowded) return plan;
+  int splits = 1;
+  while (tiles * splits * 2 <= 256 && valid_plan(a, 0, splits * 2) && a.k / pipe::BK / (splits * 2) >= 8 &&
+         (size_t)splits * 2 * a.m * total_columns(a) * sizeof(float) <= workspace_bytes)
+    splits *= 2;
+  if (splits > 1) plan = GemmPlan{0, splits};
+  return plan;
+}
+
+size_t gemm_group_workspace(const GemmGroupArgs& a, const GemmPlan& plan) {
+  return plan.splits > 1 ? (size_t)plan.splits * a.m * total_columns(a) * sizeof(float) : 0;
+}
+
+hipError_t launch_gemm_group_plan(const GemmGroupArgs& a, const GemmPlan& plan, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
+  if (!pipe_type(a.type) || a.count < 1 || a.count > kGemmGroupMax || !valid_plan(a, plan.tile, plan.splits) ||
+      gemm_group_workspace(a, plan) > workspace_bytes || (plan.splits > 1 && !workspace))
+    return hipErrorInvalidValue;
+  if (a.type == kQ4_K) return launch_typed<kQ4_K>(a, plan.tile, plan.splits, workspace, stream);
+  if (a.type == kQ5_K) return launch_typed<kQ5_K>(a, plan.tile, plan.splits, workspace, stream);
+  return launch_typed<kQ6_K>(a, plan.tile, plan.splits, workspace, stream);
+}
+
+static GemmGroupArgs single(const GemvArgs& a) {
+  GemmGroupArgs g{};
+  g.x = a.x;
+  g.w[0] = a.w;
+  g.out[0] = a.out;
+  g.n[0] = a.n;
+  g.count = 1;
+  g.type = a.type;
+  g.m = a.m;
+  g.k = a.k;
+  g.out_half = a.out_half;
+  g.x_f32 = a.x_f32;
+  return g;
+}
+
 hipError_t launch_gemm_pipe_config(const GemvArgs& a, hipStream_t stream, int config) {
-  if (a.x_f32) return hipErrorInvalidValue;
-  if (a.type == kQ4_K) return a.out_half ? launch_config<kQ4_K, _Float16>(a, stream, config) : launch_config<kQ4_K, float>(a, stream, config);
-  if (a.type == kQ5_K) return a.out_half ? launch_config<kQ5_K, _Float16>(a, stream, config) : launch_config<kQ5_K, float>(a, stream, config);
-  if (a.type == kQ6_K) return a.out_half ? launch_config<kQ6_K, _Float16>(a, stream, config) : launch_config<kQ6_K, float>(a, stream, config);
-  return hipErrorInvalidValue;
+  if (a.x_f32 || !pipe_type(a.type)) return hipErrorInvalidValue;
+  return launch_gemm_group_plan(single(a), GemmPlan{config, 1}, nullptr, 0, stream);
 }
 
 hipError_t launch_gemm_pipe(const GemvArgs& a, hipStream_t stream, bool* handled) {
-  *handled = true;
-  if (a.type == kQ4_K) return launch_any<kQ4_K>(a, stream);
-  if (a.type == kQ5_K) return launch_any<kQ5_K>(a, stream);
-  if (a.type == kQ6_K) return launch_any<kQ6_K>(a, stream);
-  *handled = false;
-  return hipSuccess;
+  *handled = pipe_type(a.type);
+  if (!*handled) return hipSuccess;
+  const GemmGroupArgs g = single(a);
+  return launch_gemm_group_plan(g, plan_gemm_group(g, 0), nullptr, 0, stream);
 }
 
 }  // namespace tensor_gguf

@@ -70,6 +70,42 @@ hipError_t launch_gemv_q5k_fast(const GemvArgs& args, hipStream_t stream, bool* 
 hipError_t launch_gemv_q6k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 hipError_t launch_dequant(const DequantArgs& args, hipStream_t stream);
 hipError_t launch_gemm(const GemvArgs& args, hipStream_t stream);
+
+// Prefill GEMM of up to kGemmGroupMax matrices that share x and K in one launch (a layer's q, k
+// and v, or gate and up), optionally with K split across workgroups.
+constexpr int kGemmGroupMax = 3;
+struct GemmGroupArgs {
+  const void* x;                 // fp16 [m, k] (fp32 when x_f32)
+  const void* w[kGemmGroupMax];  // raw GGUF rows [n_i, row_bytes]
+  void* out[kGemmGroupMax];      // fp16 or fp32 [m, n_i]
+  int n[kGemmGroupMax];
+  int count;
+  int type, m, k;
+  bool out_half, x_f32;
+};
+// What one launch of gemm_pipe reads (kernel argument): per-matrix pointers, column-tile
+// boundaries, and for a split launch the fp32 partial sums [splits][m][n_total].
+struct GemmJob {
+  const uint8_t* w[kGemmGroupMax];
+  void* out[kGemmGroupMax];
+  int n[kGemmGroupMax];
+  int tile_end[kGemmGroupMax];  // cumulative column tiles of matrices 0..i
+  int col0[kGemmGroupMax];      // first column of matrix i in the partial sums
+  int count, n_total, splits;
+  float* partial;
+};
+// A workgroup tile (index into the pipelined GEMM's tile table) and a cross-workgroup K split.
+struct GemmPlan {
+  int tile, splits;
+};
+// The plan for a shape given the workspace available (0: no cross-workgroup split).
+GemmPlan plan_gemm_group(const GemmGroupArgs& args, size_t workspace_bytes);
+// Bytes of fp32 partial sums a plan needs (0 when it does not split K).
+size_t gemm_group_workspace(const GemmGroupArgs& args, const GemmPlan& plan);
+// Q4_K / Q5_K / Q6_K only; hipErrorInvalidValue for other encodings, invalid plans or a short
+// workspace.  A split plan also launches the in-order reduction of the partial sums.
+hipError_t launch_gemm_group_plan(const GemmGroupArgs& args, const GemmPlan& plan, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream);
 // Pipelined dequant-GEMM for Q4_K, Q5_K and Q6_K (K a multiple of 256); sets
 // *handled to false for the encodings it does not cover.
 hipError_t launch_gemm_pipe(const GemvArgs& args, hipStream_t stream, bool* handled);

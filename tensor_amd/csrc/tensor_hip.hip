@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <new>
@@ -336,9 +337,116 @@ int32_t packed_call(const TensorCallV1* call, TensorErrorV1* error) {
   return TENSOR_OK;
 }
 
+// Grouped prefill GEMM: [x, w0, out0, .., w(c-1), out(c-1), workspace, type] with a caller's
+// workspace (has_workspace), or [x, w0, out0, .., type] on the library's static scratch.
+int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has_workspace, void* scratch,
+                        size_t scratch_bytes) {
+  ok(error);
+  if (!call || call->abi_version != TENSOR_ABI_VERSION || call->struct_size < sizeof(TensorCallV1))
+    return fail(error, TENSOR_ERROR_ABI, "unsupported call ABI");
+  const uint32_t argc = call->argument_count, fixed = has_workspace ? 3 : 2;
+  if (argc < fixed + 2 || argc > fixed + 2 * tensor_gguf::kGemmGroupMax || (argc - fixed) % 2)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "invalid argument count or flags");
+  if (int32_t s = check_call(call, argc, error)) return s;
+  const int count = (int)(argc - fixed) / 2, ordinal = call->stream.device_ordinal;
+  const TensorArgumentV1* a = call->arguments;
+  Format format;
+  if (int32_t s = check_type(a[argc - 1], &format, error)) return s;
+  if (int32_t s = check_matrix(a[0], "x", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT16, error)) return s;
+  const int64_t m = a[0].buffer.shape[0], k = a[0].buffer.shape[1];
+  if (k % format.qk) return fail(error, TENSOR_ERROR_ARGUMENT, "x: K is not a multiple of the block size");
+  tensor_gguf::GemmGroupArgs group{};
+  group.x = reinterpret_cast<const void*>(a[0].buffer.address);
+  for (int i = 0; i < count; ++i) {
+    const TensorArgumentV1& w = a[1 + 2 * i];
+    const TensorArgumentV1& out = a[2 + 2 * i];
+    if (int32_t s = check_matrix(w, "w", ordinal, TENSOR_UINT8, TENSOR_UINT8, error)) return s;
+    if (int32_t s = check_matrix(out, "out", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT32, error)) return s;
+    if (w.buffer.shape[1] != k / format.qk * format.bytes)
+      return fail(error, TENSOR_ERROR_ARGUMENT, "w%d: shape, stride or size mismatch", i);
+    if (out.buffer.shape[0] != m || out.buffer.shape[1] != w.buffer.shape[0] || out.dtype != a[2].dtype)
+      return fail(error, TENSOR_ERROR_ARGUMENT, "out%d: shape, stride, size or dtype mismatch", i);
+    group.w[i] = reinterpret_cast<const void*>(w.buffer.address);
+    group.out[i] = reinterpret_cast<void*>(out.buffer.address);
+    group.n[i] = (int)w.buffer.shape[0];
+  }
+  group.count = count;
+  group.type = (int)a[argc - 1].scalar;
+  group.m = (int)m;
+  group.k = (int)k;
+  group.out_half = a[2].dtype == TENSOR_FLOAT16;
+  void* workspace = scratch;
+  size_t workspace_bytes = scratch_bytes;
+  if (has_workspace) {
+    const TensorArgumentV1& ws = a[argc - 2];
+    const TensorBufferV1& b = ws.buffer;
+    if (ws.kind != TENSOR_ARG_BUFFER || ws.dtype != TENSOR_UINT8 || b.dtype != TENSOR_UINT8)
+      return fail(error, TENSOR_ERROR_ARGUMENT, "workspace: wrong argument kind or dtype");
+    if (b.device_type != TENSOR_DEVICE_ROCM || b.device_ordinal != ordinal || !b.address || b.address % 256 ||
+        b.rank != 1 || !b.shape || !b.strides || b.shape[0] <= 0 || b.strides[0] != 1 ||
+        b.byte_size < (uint64_t)b.shape[0])
+      return fail(error, TENSOR_ERROR_ARGUMENT, "workspace: invalid buffer descriptor");
+    workspace = reinterpret_cast<void*>(b.address);
+    workspace_bytes = (size_t)b.shape[0];
+  }
+  const tensor_gguf::GemmPlan plan = tensor_gguf::plan_gemm_group(group, workspace_bytes);
+  if (tensor_gguf::gemm_group_workspace(group, plan) > workspace_bytes)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "workspace: the plan needs %zu bytes, %zu available",
+                tensor_gguf::gemm_group_workspace(group, plan), workspace_bytes);
+  if (int32_t s = check_device(call, error)) return s;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
+  hipError_t status = hipSuccess;
+  if (format.qk == 256 && (group.type == (int)TENSOR_GGML_Q4_K || group.type == (int)TENSOR_GGML_Q5_K ||
+                           group.type == (int)TENSOR_GGML_Q6_K)) {
+    status = tensor_gguf::launch_gemm_group_plan(group, plan, workspace, workspace_bytes, stream);
+  } else {
+    // the other encodings take the generic GEMM, one launch per matrix in order
+    for (int i = 0; i < count && status == hipSuccess; ++i) {
+      tensor_gguf::GemvArgs one;
+      one.x = group.x;
+      one.w = group.w[i];
+      one.out = group.out[i];
+      one.type = group.type;
+      one.m = group.m;
+      one.n = group.n[i];
+      one.k = group.k;
+      one.out_half = group.out_half;
+      status = tensor_gguf::launch_gemm(one, stream);
+    }
+  }
+  if (status != hipSuccess) return hip_fail(error, status, "GGUF grouped GEMM launch");
+  return TENSOR_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int32_t tensor_gguf_gemm_group_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  return gemm_group_call(call, error, true, nullptr, 0);
+}
+
+int32_t tensor_gguf_gemm_workspace_v1(uint32_t type, int64_t m, int64_t k, const int64_t* n, uint32_t count,
+                                      uint64_t* bytes, TensorErrorV1* error) {
+  Format format;
+  if (!bytes || !n || count < 1 || count > (uint32_t)tensor_gguf::kGemmGroupMax)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "invalid workspace query");
+  if (!ggml_format(type, &format))
+    return fail(error, TENSOR_ERROR_ARGUMENT, "type: unsupported GGML type %u", type);
+  if (m < 1 || k < 1 || k % format.qk || m >= (int64_t)1 << 31 || k >= (int64_t)1 << 31)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "m, k: must be positive int32 with k a multiple of %d", format.qk);
+  tensor_gguf::GemmGroupArgs group{};
+  for (uint32_t i = 0; i < count; ++i) {
+    if (n[i] < 1 || n[i] >= (int64_t)1 << 31) return fail(error, TENSOR_ERROR_ARGUMENT, "n%u: must be a positive int32", i);
+    group.n[i] = (int)n[i];
+  }
+  group.count = (int)count;
+  group.type = (int)type;
+  group.m = (int)m;
+  group.k = (int)k;
+  *bytes = tensor_gguf::gemm_group_workspace(group, tensor_gguf::plan_gemm_group(group, SIZE_MAX));
+  return ok(error);
+}
 
 int32_t tensor_gguf_packed_v1(const TensorCallV1* call, TensorErrorV1* error) {
   return packed_call(call, error);

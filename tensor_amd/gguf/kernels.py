@@ -25,6 +25,7 @@ ENTRYPOINTS = {
     "gguf_gemm": "tensor_gguf_gemm_v1",
     "gguf_linear": "tensor_gguf_linear_v1",
     "gguf_gemv_group": "tensor_gguf_gemv_group_v1",
+    "gguf_gemm_group": "tensor_gguf_gemm_group_v1",
     "gguf_gemv_swiglu": "tensor_gguf_gemv_swiglu_v1",
     "gguf_dequant": "tensor_gguf_dequant_v1",
 }
@@ -42,7 +43,12 @@ def _symbols(kernel: str, count: int | None) -> tuple:
         return ("N", "K")
     if kernel == "gguf_gemv_group":
         return ("M", "K", *(f"N{i}" for i in range(count)))
+    if kernel == "gguf_gemm_group":
+        return ("M", "K", *(f"N{i}" for i in range(count)), "W")
     return ("M", "N", "K")
+
+
+GROUPS = ("gguf_gemv_group", "gguf_gemm_group")
 
 
 def packed_manifest(encoding, m: int, n: int, k: int, *, x_dtype: str = "float32",
@@ -101,7 +107,9 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
 
     ``gguf_gemv_group`` takes ``count`` (1..3) weight matrices that share the
     activations: arguments ``[x, w0, out0, w1, out1, ..., type]`` with row
-    counts ``N0, N1, ...``; every other kernel takes no ``count``.
+    counts ``N0, N1, ...``; ``gguf_gemm_group`` (the prefill GEMM of such a group,
+    any M) adds a ``workspace`` uint8 buffer before ``type`` (its size
+    ``Device.gemm_workspace`` tells); every other kernel takes no ``count``.
     ``gguf_gemv_swiglu`` takes ``[x, w_gate, w_up, out, type]`` and stores
     silu(x W_gate^T) * (x W_up^T).
     """
@@ -121,9 +129,9 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
     qk, _ = GEOMETRY[code]
     weight = {"name": "w", "dtype": "uint8", "shape": [{"var": "N"}, _row_bytes(code)], "alignment": 16}
     type_argument = {"name": "type", "dtype": "uint32", "kind": "scalar"}
-    if (count is not None) != (kernel == "gguf_gemv_group"):
-        raise ValueError("count applies to gguf_gemv_group only, and gguf_gemv_group needs it")
-    if kernel == "gguf_gemv_group":
+    if (count is not None) != (kernel in GROUPS):
+        raise ValueError("count applies to gguf_gemv_group / gguf_gemm_group only, and they need it")
+    if kernel in GROUPS:
         if not 1 <= int(count) <= GEMV_GROUP_MAX:
             raise ValueError(f"count must be in 1..{GEMV_GROUP_MAX}")
         count = int(count)
@@ -131,6 +139,8 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
         for i in range(count):
             arguments.append({"name": f"w{i}", "dtype": "uint8", "shape": [{"var": f"N{i}"}, _row_bytes(code)], "alignment": 16})
             arguments.append({"name": f"out{i}", "dtype": out_dtype, "shape": [{"var": "M"}, {"var": f"N{i}"}], "alignment": 16})
+        if kernel == "gguf_gemm_group":
+            arguments.append({"name": "workspace", "dtype": "uint8", "shape": [{"var": "W"}], "alignment": 256})
         arguments.append(type_argument)
     elif kernel == "gguf_gemv_swiglu":
         arguments = [
@@ -154,7 +164,7 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
             type_argument,
         ]
     result = {
-        "name": f"{kernel}:{NAMES[code]}:{out_dtype}" + (f":{count}" if kernel == "gguf_gemv_group" else ""),
+        "name": f"{kernel}:{NAMES[code]}:{out_dtype}" + (f":{count}" if kernel in GROUPS else ""),
         "provider": "hip",
         "target": "gfx950",
         "entrypoint": ENTRYPOINTS[kernel],
@@ -165,7 +175,7 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
         },
         "arguments": arguments,
         "abi": [dict(item, kind=item.get("kind", "buffer")) for item in arguments],
-        "outputs": [f"out{i}" for i in range(count)] if kernel == "gguf_gemv_group" else ["out"],
+        "outputs": [f"out{i}" for i in range(count)] if kernel in GROUPS else ["out"],
         "constants": {"type": code},
         "symbols": {name: "int32" for name in _symbols(kernel, count)},
         "shape_divisors": {"K": qk},

@@ -377,6 +377,17 @@ class Device(Session):
         _native.call("tensor_hip_event_destroy", event.handle)
 
     # -------------------------------------------------------------- graphs --
+    def gemm_workspace(self, encoding, m: int, k: int, rows) -> int:
+        """Bytes of workspace ``gguf_gemm_group`` uses for this shape (``rows`` = each matrix's
+        N); 0 when it does not split K.  A smaller workspace is accepted and limits the split."""
+        from tensor_amd.gguf.quant import ggml_type
+
+        rows = [int(n) for n in rows]
+        result = c.c_uint64()
+        _native.call("tensor_gguf_gemm_workspace_v1", ggml_type(encoding), int(m), int(k),
+                     (c.c_int64 * len(rows))(*rows), len(rows), c.byref(result))
+        return result.value
+
     def graph(self, callback, *, resources=()):
         """Capture the launches ``callback()`` enqueues into a replayable graph.  The buffers of
         every call launched during the capture, and ``resources``, are checked before each

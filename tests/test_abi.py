@@ -427,3 +427,71 @@ def test_packed_form_accepts_the_showcase_call(shape):
     status, message = PackedCall(**shape).run()
     assert status == ERR_PROVIDER, message
     assert "hipGetDevice" in message or "current device" in message, message
+
+
+def test_gemm_workspace_query_follows_the_split_plan():
+    """The grouped prefill GEMM splits K across workgroups only where its plan does, and says
+    how many bytes of fp32 partial sums it then needs (splits x M x sum(N) x 4)."""
+    query = lambda t, m, k, rows: _query_workspace(t, m, k, rows)
+    assert query(12, 256, 4096, [4096, 1024, 1024]) == 4 * 256 * 6144 * 4   # C5 q + k + v
+    assert query(14, 256, 12288, [4096]) == 8 * 256 * 4096 * 4             # C5 down (Q6_K)
+    assert query(12, 256, 4096, [4096]) == 0                                # o: small tiles fill the CUs
+    assert query(12, 2048, 4096, [12288]) == 0                              # C4: 256 x 128 tiles fill them
+    assert query(12, 256, 4096, [12288, 12288]) == 0                        # gate + up
+    assert query(8, 256, 12288, [4096]) == 0                                # generic encodings never split
+
+
+def _query_workspace(type_, m, k, rows):
+    result = c.c_uint64()
+    error = abi.ErrorDescriptor()
+    status = _native.library().tensor_gguf_gemm_workspace_v1(type_, m, k, (c.c_int64 * len(rows))(*rows), len(rows),
+                                                             c.byref(result), c.byref(error))
+    assert status == OK, error.message
+    return result.value
+
+
+class GroupGemmCall:
+    """[x, w0, out0, w1, out1, workspace, type] with fake (never dereferenced) addresses."""
+
+    def __init__(self, m=256, k=512, rows=(64, 32), ws=4096):
+        shapes = [((m, k), 10, 2)]
+        for n in rows:
+            shapes += [((n, k // 256 * 144), 3, 1), ((m, n), 10, 2)]
+        self.keep, self.args = [], (abi.Argument * (len(shapes) + 2))()
+        for i, (shape, dtype, item) in enumerate(shapes):
+            shp, strides = (c.c_int64 * 2)(*shape), (c.c_int64 * 2)(shape[1] * item, item)
+            self.keep += [shp, strides]
+            self.args[i].kind, self.args[i].dtype = 1, dtype
+            self.args[i].buffer = abi.BufferDescriptor(0x100000 * (i + 1), shape[0] * shape[1] * item, shp, strides,
+                                                       2, dtype, 10, 0)
+        wshape, wstride = (c.c_int64 * 1)(ws), (c.c_int64 * 1)(1)
+        self.keep += [wshape, wstride]
+        w = len(shapes)
+        self.args[w].kind, self.args[w].dtype = 1, 3
+        self.args[w].buffer = abi.BufferDescriptor(0x4000000, ws, wshape, wstride, 1, 3, 10, 0)
+        self.args[w + 1].kind, self.args[w + 1].dtype, self.args[w + 1].scalar = 2, 7, 12
+        self.call = abi.CallDescriptor(1, 72, self.args, len(shapes) + 2, 0, (c.c_uint32 * 3)(1, 1, 1),
+                                       (c.c_uint32 * 3)(256, 1, 1), 0, abi.StreamDescriptor(10, 0, 0))
+
+    def run(self):
+        error = abi.ErrorDescriptor()
+        status = _native.kernel("tensor_gguf_gemm_group_v1")(c.byref(self.call), c.byref(error))
+        return status, error.message.decode()
+
+
+def test_gemm_group_call_argument_checks():
+    call = GroupGemmCall()
+    status, message = call.run()
+    assert status == ERR_PROVIDER, message  # well formed: stops at the device check
+    call = GroupGemmCall()
+    call.args[5].dtype = call.args[5].buffer.dtype = 11
+    assert call.run() == (ERR_ARG, "workspace: wrong argument kind or dtype")
+    call = GroupGemmCall()
+    call.args[5].buffer.address = 0x4000010  # not 256-byte aligned
+    assert call.run() == (ERR_ARG, "workspace: invalid buffer descriptor")
+    call = GroupGemmCall()
+    call.call.argument_count = 6
+    assert call.run()[0] == ERR_ARG
+    call = GroupGemmCall()
+    call.keep[8][0] = 255  # out1 with 255 rows for M = 256
+    assert call.run() == (ERR_ARG, "out1: shape, stride, size or dtype mismatch")

@@ -466,9 +466,21 @@ def test_c5_layer_chained_in_one_graph(hip_device, c_oracle, m):
         calls.append(hip_device.load("gguf_gemv", encoding="q6_k", out_dtype="float16")
                      .bind(xbs["mlp_mid"], wbs["down"], outs["down"]))
     else:
-        for name, enc, _, _, source in C5_LAYER:
-            exe = hip_device.load("gguf_gemm", encoding=enc, out_dtype="float16")
-            calls.append(exe.bind(xbs[source], wbs[name], outs[name]))
+        # the prefill step: q + k + v and gate + up as grouped GEMMs (K split for q + k + v), o on
+        # its own, the Q6_K down with its K split; one workspace, used by one launch at a time
+        groups = [("attn_in", "q4_k", ("q", "k", "v")), ("attn_out", "q4_k", ("o",)),
+                  ("mlp_in", "q4_k", ("gate", "up")), ("mlp_mid", "q6_k", ("down",))]
+        rows = {name: n for name, _, n, _, _ in C5_LAYER}
+        need = max(hip_device.gemm_workspace(enc, m, widths[src], [rows[n] for n in names])
+                   for src, enc, names in groups)
+        assert need > 0
+        workspace = hip_device.empty((need,), "uint8")
+        for src, enc, names in groups:
+            exe = hip_device.load("gguf_gemm_group", encoding=enc, out_dtype="float16", count=len(names))
+            args = [xbs[src]]
+            for name in names:
+                args += [wbs[name], outs[name]]
+            calls.append(exe.bind(*args, workspace))
     graph = hip_device.graph(lambda: [call.launch() for call in calls])
     try:
         for replay in range(2):
@@ -483,7 +495,7 @@ def test_c5_layer_chained_in_one_graph(hip_device, c_oracle, m):
                 assert err <= TOLERANCE, (name, replay, err)
     finally:
         graph.close()
-        for b in [*xbs.values(), *wbs.values(), *outs.values()]:
+        for b in {id(b): b for call in calls for b in call.buffers}.values():
             b.release()
 
 
@@ -717,3 +729,66 @@ def test_packed_form_every_encoding(hip_device, c_oracle, encoding, x_dtype, m):
         assert err <= TOLERANCE, (out_dtype, err)
         if m == 1 and x_dtype == "float32" and out_dtype == "float32":
             assert err <= 1e-5, err
+
+
+# ------------------------------------------------------- grouped prefill --
+
+def run_gemm_group(device, encoding, x, raws, out_dtype, workspace_bytes=None):
+    """gguf_gemm_group over matrices sharing x; workspace as the library asks, or the given size."""
+    m, k = x.shape
+    rows = [raw.shape[0] for raw in raws]
+    need = device.gemm_workspace(encoding, m, k, rows)
+    size = max(256, need if workspace_bytes is None else workspace_bytes)
+    exe = device.load("gguf_gemm_group", encoding=encoding, out_dtype=out_dtype, count=len(raws))
+    xb = device.from_numpy(x)
+    wbs = [device.from_numpy(raw) for raw in raws]
+    outs = [device.empty((m, n), out_dtype) for n in rows]
+    workspace = device.empty((size,), "uint8")
+    device.fill_bytes(workspace, 0xFF)  # stale partial sums would show up as NaN
+    args = [xb]
+    for wb, out in zip(wbs, outs):
+        device.fill_bytes(out, 0xFF)
+        args += [wb, out]
+    exe.launch(*args, workspace)
+    results = [out.to_numpy() for out in outs]
+    for b in [xb, *wbs, *outs, workspace]:
+        b.release()
+    return results, need
+
+
+@pytest.mark.parametrize("encoding,m,k,rows,split", [
+    ("q4_k", 256, 4096, (4096, 1024, 1024), True),   # C5 q + k + v: K split over 4 workgroups
+    ("q4_k", 256, 4096, (12288, 12288), False),      # C5 gate + up: one launch, 256 x 128 tiles
+    ("q6_k", 256, 12288, (4096,), True),             # C5 down: K split over 8 workgroups
+    ("q4_k", 256, 4096, (4096,), False),             # o: 64 x 64 tiles with the K range inside the workgroup
+    ("q5_k", 300, 8192, (1000, 77), True),           # ragged M and N, Q5_K
+    ("q6_k", 200, 8192, (300, 500, 64), True),       # three ragged matrices, K >= 8192
+    ("q8_0", 64, 1024, (300, 100), False),           # other encodings: one generic launch per matrix
+])
+def test_gemm_group_parity(hip_device, c_oracle, encoding, m, k, rows, split):
+    code = Q.ggml_type(encoding)
+    note("gemm-group", encoding, m, k, rows)
+    x = cases.activation(m, k, 700 + len(rows))
+    raws = [cases.weight(n, k, encoding, 710 + i) for i, n in enumerate(rows)]
+    c_oracle.set_threads(16)
+    for out_dtype in ("float16", "float32"):
+        got, need = run_gemm_group(hip_device, encoding, x, raws, out_dtype)
+        assert (need > 0) == split, need
+        for i, (raw, n) in enumerate(zip(raws, rows)):
+            assert not np.isnan(got[i]).any(), (i, out_dtype)
+            err = R.relative_l2(got[i], c_oracle.linear(x, raw, code, n, k, prefill=True))
+            assert err <= (TOLERANCE if out_dtype == "float16" else 1e-5), (i, out_dtype, err)
+
+
+def test_gemm_group_with_a_short_workspace_splits_less(hip_device, c_oracle):
+    """A workspace shorter than the plan wants limits the split (here to none, or to 2) and the
+    result stays within tolerance of the same oracle."""
+    m, k, rows = 256, 12288, (4096,)
+    x = cases.activation(m, k, 720)
+    raws = [cases.weight(rows[0], k, "q6_k", 721)]
+    expected = c_oracle.linear(x, raws[0], Q.Q6_K, rows[0], k, prefill=True)
+    for size in (256, 2 * m * rows[0] * 4):
+        note("gemm-group-short-workspace", size)
+        got, need = run_gemm_group(hip_device, "q6_k", x, raws, "float32", workspace_bytes=size)
+        assert need > size
+        assert R.relative_l2(got[0], expected) <= 1e-5

@@ -138,6 +138,22 @@ int32_t tensor_gguf_gemv_group_v1(const TensorCallV1 *call, TensorErrorV1 *error
 int32_t tensor_gguf_gemm_group_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 
 /*
+ * tensor_gguf_gemm_group_v1 without the workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, hosts that forbid
+ * hipMalloc): arguments [x, w0, out0, .., w(c-1), out(c-1), type].  No counterpart in the
+ * reference.  The K split's fp32 partials go to a static device array of the library,
+ * TENSOR_GGUF_NOALLOC_SCRATCH_BYTES per GPU, held from load until the process ends; the call
+ * allocates nothing, runs the plan tensor_gguf_gemm_group_v1 runs with the workspace
+ * tensor_gguf_gemm_workspace_v1 reports and so gives the same bits, and refuses a shape whose
+ * split would need more scratch (by construction none does: a split's partials cover at most
+ * 256 tiles of 256 x 128 fp32).  Every partial read is written earlier in the same call, so
+ * nothing needs clearing, but calls that overlap on one GPU (two streams, or two threads)
+ * share the array and race: serialise them.
+ */
+#define TENSOR_GGUF_NOALLOC_SCRATCH_BYTES (32u << 20)
+int32_t tensor_gguf_gemm_group_noalloc_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/*
  * Workspace bytes tensor_gguf_gemm_group_v1 would use for this shape (0: it does not split K):
  * n[0 .. count-1] are the matrices' row counts.
  */

@@ -19,6 +19,7 @@ LIBRARY = Path(__file__).resolve().parent / "libtensor_hip.so"
 KERNELS = (
     "tensor_gguf_packed_v1",
     "tensor_gguf_gemm_group_v1",
+    "tensor_gguf_gemm_group_noalloc_v1",
     "tensor_gguf_gemv_v1",
     "tensor_gguf_gemm_v1",
     "tensor_gguf_linear_v1",

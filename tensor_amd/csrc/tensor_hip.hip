@@ -7,12 +7,41 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 
 #include "gguf_launch.h"
 #include "tensor_hip.h"
 
+// Scratch of tensor_gguf_gemm_group_noalloc_v1: the fp32 partial sums of a K split.  A split
+// plan keeps splits x (256 x 128 tiles) <= 256 workgroups and its partials cover at most
+// those tiles, so splits * M * N_total * 4 <= 256 * 256 * 128 * 4 bytes = 32 MiB for any shape.
+// Each GPU the library runs on holds its own copy until the process ends.  Host code never
+// uses the array's name as an address: scratch_address() resolves this device's copy.
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_device[kScratchDevices];  // by ordinal, nullptr until resolved
+
+// Address of the current device's scratch copy, resolved once per device with that device
+// current (the caller has checked that the stream's ordinal is the current device).
+hipError_t scratch_address(int ordinal, void** address) {
+  if (ordinal < 0 || ordinal >= kScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_device[ordinal]) {
+    void* resolved = nullptr;
+    const hipError_t status = hipGetSymbolAddress(&resolved, HIP_SYMBOL(scratch));
+    if (status != hipSuccess) return status;
+    if (!resolved) return hipErrorInvalidSymbol;
+    scratch_device[ordinal] = resolved;
+  }
+  *address = scratch_device[ordinal];
+  return hipSuccess;
+}
 
 int32_t fail(TensorErrorV1* error, int32_t code, const char* format, ...) {
   if (error) {
@@ -339,8 +368,9 @@ int32_t packed_call(const TensorCallV1* call, TensorErrorV1* error) {
 
 // Grouped prefill GEMM: [x, w0, out0, .., w(c-1), out(c-1), workspace, type] with a caller's
 // workspace (has_workspace), or [x, w0, out0, .., type] on the library's static scratch.
-int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has_workspace, void* scratch,
-                        size_t scratch_bytes) {
+// The scratch form runs the plan the caller's form runs with the workspace that
+// tensor_gguf_gemm_workspace_v1 reports, so the two give the same bits.
+int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has_workspace) {
   ok(error);
   if (!call || call->abi_version != TENSOR_ABI_VERSION || call->struct_size < sizeof(TensorCallV1))
     return fail(error, TENSOR_ERROR_ABI, "unsupported call ABI");
@@ -375,8 +405,8 @@ int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has
   group.m = (int)m;
   group.k = (int)k;
   group.out_half = a[2].dtype == TENSOR_FLOAT16;
-  void* workspace = scratch;
-  size_t workspace_bytes = scratch_bytes;
+  void* workspace = nullptr;
+  size_t workspace_bytes = SIZE_MAX;
   if (has_workspace) {
     const TensorArgumentV1& ws = a[argc - 2];
     const TensorBufferV1& b = ws.buffer;
@@ -390,10 +420,22 @@ int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has
     workspace_bytes = (size_t)b.shape[0];
   }
   const tensor_gguf::GemmPlan plan = tensor_gguf::plan_gemm_group(group, workspace_bytes);
-  if (tensor_gguf::gemm_group_workspace(group, plan) > workspace_bytes)
-    return fail(error, TENSOR_ERROR_ARGUMENT, "workspace: the plan needs %zu bytes, %zu available",
-                tensor_gguf::gemm_group_workspace(group, plan), workspace_bytes);
+  const size_t need = tensor_gguf::gemm_group_workspace(group, plan);
+  if (need > workspace_bytes)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "workspace: the plan needs %zu bytes, %zu available", need,
+                workspace_bytes);
+  if (!has_workspace) {
+    if (need > kScratchBytes)
+      return fail(error, TENSOR_ERROR_ARGUMENT,
+                  "shape too large: the K split needs %zu bytes of scratch, the library holds %zu", need,
+                  kScratchBytes);
+    workspace_bytes = kScratchBytes;
+  }
   if (int32_t s = check_device(call, error)) return s;
+  if (!has_workspace) {
+    const hipError_t status = scratch_address(call->stream.device_ordinal, &workspace);
+    if (status != hipSuccess) return hip_fail(error, status, "hipGetSymbolAddress(scratch)");
+  }
   hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
   hipError_t status = hipSuccess;
   if (format.qk == 256 && (group.type == (int)TENSOR_GGML_Q4_K || group.type == (int)TENSOR_GGML_Q5_K ||
@@ -423,7 +465,11 @@ int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has
 extern "C" {
 
 int32_t tensor_gguf_gemm_group_v1(const TensorCallV1* call, TensorErrorV1* error) {
-  return gemm_group_call(call, error, true, nullptr, 0);
+  return gemm_group_call(call, error, true);
+}
+
+int32_t tensor_gguf_gemm_group_noalloc_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  return gemm_group_call(call, error, false);
 }
 
 int32_t tensor_gguf_gemm_workspace_v1(uint32_t type, int64_t m, int64_t k, const int64_t* n, uint32_t count,

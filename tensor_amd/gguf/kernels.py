@@ -26,6 +26,7 @@ ENTRYPOINTS = {
     "gguf_linear": "tensor_gguf_linear_v1",
     "gguf_gemv_group": "tensor_gguf_gemv_group_v1",
     "gguf_gemm_group": "tensor_gguf_gemm_group_v1",
+    "gguf_gemm_group_noalloc": "tensor_gguf_gemm_group_noalloc_v1",
     "gguf_gemv_swiglu": "tensor_gguf_gemv_swiglu_v1",
     "gguf_dequant": "tensor_gguf_dequant_v1",
 }
@@ -41,14 +42,14 @@ def _row_bytes(code: int) -> dict:
 def _symbols(kernel: str, count: int | None) -> tuple:
     if kernel == "gguf_dequant":
         return ("N", "K")
-    if kernel == "gguf_gemv_group":
+    if kernel in ("gguf_gemv_group", "gguf_gemm_group_noalloc"):
         return ("M", "K", *(f"N{i}" for i in range(count)))
     if kernel == "gguf_gemm_group":
         return ("M", "K", *(f"N{i}" for i in range(count)), "W")
     return ("M", "N", "K")
 
 
-GROUPS = ("gguf_gemv_group", "gguf_gemm_group")
+GROUPS = ("gguf_gemv_group", "gguf_gemm_group", "gguf_gemm_group_noalloc")
 
 
 def packed_manifest(encoding, m: int, n: int, k: int, *, x_dtype: str = "float32",
@@ -109,7 +110,8 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
     activations: arguments ``[x, w0, out0, w1, out1, ..., type]`` with row
     counts ``N0, N1, ...``; ``gguf_gemm_group`` (the prefill GEMM of such a group,
     any M) adds a ``workspace`` uint8 buffer before ``type`` (its size
-    ``Device.gemm_workspace`` tells); every other kernel takes no ``count``.
+    ``Device.gemm_workspace`` tells); ``gguf_gemm_group_noalloc`` is the same GEMM
+    without it, on the library's static scratch; every other kernel takes no ``count``.
     ``gguf_gemv_swiglu`` takes ``[x, w_gate, w_up, out, type]`` and stores
     silu(x W_gate^T) * (x W_up^T).
     """
@@ -130,7 +132,7 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
     weight = {"name": "w", "dtype": "uint8", "shape": [{"var": "N"}, _row_bytes(code)], "alignment": 16}
     type_argument = {"name": "type", "dtype": "uint32", "kind": "scalar"}
     if (count is not None) != (kernel in GROUPS):
-        raise ValueError("count applies to gguf_gemv_group / gguf_gemm_group only, and they need it")
+        raise ValueError(f"count applies to {' / '.join(GROUPS)} only, and they need it")
     if kernel in GROUPS:
         if not 1 <= int(count) <= GEMV_GROUP_MAX:
             raise ValueError(f"count must be in 1..{GEMV_GROUP_MAX}")

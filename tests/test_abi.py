@@ -473,9 +473,9 @@ class GroupGemmCall:
         self.call = abi.CallDescriptor(1, 72, self.args, len(shapes) + 2, 0, (c.c_uint32 * 3)(1, 1, 1),
                                        (c.c_uint32 * 3)(256, 1, 1), 0, abi.StreamDescriptor(10, 0, 0))
 
-    def run(self):
+    def run(self, entry="tensor_gguf_gemm_group_v1"):
         error = abi.ErrorDescriptor()
-        status = _native.kernel("tensor_gguf_gemm_group_v1")(c.byref(self.call), c.byref(error))
+        status = _native.kernel(entry)(c.byref(self.call), c.byref(error))
         return status, error.message.decode()
 
 
@@ -495,3 +495,18 @@ def test_gemm_group_call_argument_checks():
     call = GroupGemmCall()
     call.keep[8][0] = 255  # out1 with 255 rows for M = 256
     assert call.run() == (ERR_ARG, "out1: shape, stride, size or dtype mismatch")
+
+
+def test_gemm_group_noalloc_takes_the_group_without_a_workspace():
+    noalloc = "tensor_gguf_gemm_group_noalloc_v1"
+    call = GroupGemmCall()
+    assert call.run(noalloc) == (ERR_ARG, "invalid argument count or flags")  # a workspace is one too many
+    call = GroupGemmCall()
+    call.args[5] = call.args[6]  # [x, w0, out0, w1, out1, type]
+    call.call.argument_count = 6
+    status, message = call.run(noalloc)
+    assert status == ERR_PROVIDER, message  # well formed: stops at the device check
+    call.keep[8][0] = 255
+    assert call.run(noalloc) == (ERR_ARG, "out1: shape, stride, size or dtype mismatch")
+    call.call.argument_count = 5
+    assert call.run(noalloc)[0] == ERR_ARG

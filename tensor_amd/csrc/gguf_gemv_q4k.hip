@@ -302,49 +302,53 @@ __global__ __launch_bounds__(SPLIT * 64) void gemv_q4k_mfma(const _Float16* __re
 // rows).  Wave (t, q) of a workgroup owns 16-row tile t and the 576-byte range of four
 // super-blocks 4q .. 4q+3 of every row; a workgroup holds TILES tiles x K/1024 waves.
 // Load c (0..8) of a lane (n, g) reads the 16-byte chunk 4c + g of row n's range, so each
-// load instruction covers whole 64-byte sectors of 16 rows.  With 9 chunks per 144-byte
-// super-block this hands every lane exactly one header (super-block b = g, at load 9b/4)
-// and two quant chunks of each super-block, at fixed loads for some lanes and one of two
-// loads for others (one v_cndmask per dword).  A quant chunk r (1..8) is bytes 16(r-1) ..
-// of the 128 quant bytes: pair j = (r-1)/2, half (r-1)%2, low nibbles sub-block 2j and
-// high nibbles 2j+1.  Headers reach the other lanes of their row with ds_bpermute; codes
-// are widened and scaled as in gemv_q4k_mfma (exact sc*q in fp16), d applied per
-// super-block; the min term uses a per-8-element table of x sums staged with x.
+// load instruction covers whole 64-byte sectors of 16 rows.  Chunk 9b of the range is the
+// header of super-block b; it lands in load 2b of lane g = b, so every lane holds exactly one
+// header.  Quant chunk r (1..8) of a super-block is bytes 16(r-1) .. of its 128 quant bytes:
+// pair j = (r-1)/2, low nibbles of sub-block 2j and high nibbles of 2j+1, elements
+// 16((r-1) % 2) ..  Lane g's two quant chunks of super-block b are r and r + 4 (pairs j and
+// j + 2) with r - 1 = (g - b - 1) mod 4, in loads 2b+1, 2b+2 when g <= b, else 2b, 2b+1.
 //
-// Issue order (measured on MI355X): x, then the loads of super-block 0 only; the other six
-// loads follow the barrier that publishes x.  Issued together, the 28 MB weight stream
-// queued the 32-64 KB activation loads behind it (x was staged ~4.5 us after launch);
-// this way x is staged in ~1.5 us while a third of the weights is already in flight.
-constexpr int kSecEarlyLoads = 3;
+// Each lane decodes its own header once, into a per-wave LDS table of pair entries
+// {half2(sc_lo, sc_hi / 16), half2(-1024 sc_lo, -64 sc_hi), dmin m_lo, dmin m_hi} and d.  A
+// code widened to fp16 "1024 + q" (low nibble) or "1024 + 16 q" (high nibble) times the
+// entry's first half plus its second (each broadcast through op_sel) is the exact integer
+// sc * q, so a super-block's MFMA chain takes d once at its end.  The min term is a 16x16x4
+// fp32 MFMA of 16-element x sums (staged with x, a chunk's low- and high-nibble runs side by
+// side) and dmin * m.  Activation rows past M read row M - 1: they reach only output rows
+// that are never stored.
+//
+// Issue order (per-wave s_memrealtime stamps on MI355X, M = 4, 12288 x 4096).  XFIRST: x alone,
+// then every weight load after the barrier that publishes x.  x then reaches LDS 1.6 us after
+// launch; with the four header loads issued ahead of the barrier it took 3.3 us, with all nine
+// 4.8 us (the weight bytes in flight delay it), and every wave waits for x before it computes
+// (10.7 against 11.7 and 11.2 us per launch).  That holds for a grid of one workgroup per CU;
+// where workgroups come in several rounds a late one would stream nothing while its x arrives,
+// so those grids (!XFIRST) put all nine loads in flight behind x (grouped pair at M = 4:
+// 17.2 us against 18.2 x-first).
 constexpr int kSecXPad = 16;               // bytes after each LDS row of x
 constexpr size_t kSecMaxLds = 160 * 1024;  // LDS of one gfx950 workgroup
+constexpr int kSecTableBytes = 64 * 4 * 16 + 64 * 4;  // per wave: 4 pair entries per lane, then d per lane
 
-__device__ __forceinline__ uint4 shfl4(const uint4& v, int src) {
-  return make_uint4(__shfl(v.x, src, 64), __shfl(v.y, src, 64), __shfl(v.z, src, 64), __shfl(v.w, src, 64));
-}
+// Floats per LDS row of x sums: one per 16 elements and 16 bytes of padding, so that the rows of
+// one read fall in different banks.
+__host__ __device__ constexpr int sec_sum_row(int k) { return (k >> 4) + 4; }
 
 __device__ __forceinline__ uint4 select4(bool c, const uint4& a, const uint4& b) {
   return make_uint4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
 }
 
-// Scale and min codes of sub-blocks 2j (bits 0-7) and 2j+1 (bits 8-15), j varying per lane.
-__device__ __forceinline__ void pair_codes(const uint4& hd, int j, uint32_t& scs, uint32_t& mns) {
-  const int shift = 16 * (j & 1);
-  const uint32_t b0 = hd.y >> shift, b1 = hd.z >> shift, b2 = hd.w >> shift;
-  if (j < 2) {
-    scs = b0 & 0x3F3Fu;
-    mns = b1 & 0x3F3Fu;
-  } else {
-    scs = (b2 & 0x0F0Fu) | ((b0 >> 2) & 0x3030u);
-    mns = ((b2 >> 4) & 0x0F0Fu) | ((b1 >> 2) & 0x3030u);
-  }
-}
+// Slot of 16-element run 16 s + 4 j + 2 nib + h of a row (elements 256 s + 64 j + 32 nib + 16 h)
+// in the sum table: 16 s + 4 j + 2 h + nib, the low- and high-nibble runs of a chunk side by side.
+__device__ __forceinline__ int sum_slot(int run) { return (run & ~3) | ((run & 1) << 1) | ((run >> 1) & 1); }
+
+__device__ __forceinline__ uint32_t half2_bits(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
 // PAIR = 1 (SwiGLU) or 2 (two outputs): the workgroup's two tile slots are tile blockIdx.x of w
 // and the same tile of w2, a second matrix of the same shape. PAIR = 1: the wave that sums the w
 // (gate) tile also sums the w2 (up) tile's partials and stores silu(gate) * up to out. PAIR = 2:
 // each tile is stored, to out and out2 (the grouped GEMV of two equal matrices in one launch).
-template <int M, typename OutT, int PAIR = 0>
+template <int M, typename OutT, int PAIR = 0, bool XFIRST = true>
 __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict__ x, const uint8_t* __restrict__ w,
                                                      OutT* __restrict__ out, int n_rows, int k, int tiles,
                                                      const uint8_t* __restrict__ w2 = nullptr,
@@ -353,102 +357,137 @@ __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict_
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int XCH = 8;  // x chunks per thread (the host checks M * K / 8 <= XCH * threads)
   const int KW = k >> 10;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int t = wv / KW, q = wv - t * KW;
-  const int row_bytes = (k >> 8) * 144;
-  const int xrow = 2 * k + kSecXPad;
-  const int chunks = M * k / 8, cpr = k / 8;
-  uint8_t* xl = lds;                                          // M rows of x, then 16 zero bytes
-  float* s8 = reinterpret_cast<float*>(lds + M * xrow + 16);  // sums of 8 x values, then 2 zeros
+  const int row_bytes = (k >> 8) * 144, threads = blockDim.x;
+  const int xrow = 2 * k + kSecXPad, cpr = k >> 3, srow = sec_sum_row(k);
+  uint8_t* xl = lds;                                                       // M rows of x
+  float* s16 = reinterpret_cast<float*>(lds + M * xrow);                   // [M][K/16 + pad] run sums
+  uint8_t* tab = lds + M * xrow + M * srow * 4 + wv * kSecTableBytes;      // this wave's header table:
+  float* dtab = reinterpret_cast<float*>(tab + 64 * 4 * 16);               // entry (b, j, n), then d (b, n)
 
+  // x chunk c = 64 wv + lane + i * threads: the 64 chunks of a wave lie in one row (K / 8 is a
+  // multiple of 128), so row and bounds are wave-uniform
   uint4 xr[XCH];
 #pragma unroll
   for (int i = 0; i < XCH; ++i) {
-    const int c = threadIdx.x + i * (int)blockDim.x;
-    if (c < chunks) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * (size_t)c);
+    const int cw = wv * 64 + i * threads;
+    if (cw < M * cpr) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * (size_t)(cw + lane));
   }
   const int tile = PAIR ? (int)blockIdx.x : blockIdx.x * tiles + t;
   const uint8_t* base = (PAIR && t == 1 ? w2 : w) + (size_t)min(tile * 16 + n, n_rows - 1) * row_bytes + q * 576 + 16 * g;
   uint4 v[9];
+  auto load_weights = [&]() {
 #pragma unroll
-  for (int c = 0; c < kSecEarlyLoads; ++c) v[c] = load16(base + 64 * c);
-  asm volatile("" ::: "memory");
+    for (int c = 0; c < 8; c += 2) v[c] = load16(base + 64 * c);  // the headers first: they are decoded first
+#pragma unroll
+    for (int c = 1; c < 9; c += 2) v[c] = load16(base + 64 * c);
+    v[8] = load16(base + 512);
+  };
+  if constexpr (!XFIRST) {
+    // every wave's x requests enter the CU's memory pipeline ahead of its weight requests (the
+    // barrier orders issue only), and the weights stream while x is staged
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    load_weights();
+    asm volatile("" ::: "memory");
+  }
 #pragma unroll
   for (int i = 0; i < XCH; ++i) {
-    const int c = threadIdx.x + i * (int)blockDim.x;
-    if (c < chunks) {
-      const int m = c / cpr, cc = c - m * cpr;
+    const int cw = wv * 64 + i * threads;
+    if (cw < M * cpr) {
+      const int m = cw / cpr, cc = cw - m * cpr + lane;
       *reinterpret_cast<uint4*>(xl + m * xrow + 16 * cc) = xr[i];
       const uint32_t one = 0x3C003C00u;
-      s8[c] = dot2(xr[i].w, one, dot2(xr[i].z, one, dot2(xr[i].y, one, dot2(xr[i].x, one, 0.f))));
+      float s = dot2(xr[i].w, one, dot2(xr[i].z, one, dot2(xr[i].y, one, dot2(xr[i].x, one, 0.f))));
+      s += __shfl_xor(s, 1, 64);
+      if ((lane & 1) == 0) s16[m * srow + sum_slot(cc >> 1)] = s;
     }
   }
-  if (threadIdx.x == 0) {
-    *reinterpret_cast<uint4*>(xl + M * xrow) = make_uint4(0, 0, 0, 0);
-    s8[chunks] = 0.f;
-    s8[chunks + 1] = 0.f;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  if constexpr (XFIRST) {
+    asm volatile("" ::: "memory");
+    load_weights();
   }
-  __syncthreads();
-#pragma unroll
-  for (int c = kSecEarlyLoads; c < 9; ++c) v[c] = load16(base + 64 * c);
 
-  // as the A operand lane (n, g) holds activation row n; lanes past M read zeros at every offset
-  const bool has_row = n < M;
-  const uint8_t* xn = has_row ? xl + n * xrow + 2048 * q : xl + M * xrow;
-  const int xstep = has_row ? 1 : 0;
-  const float* s8n = has_row ? s8 + n * cpr + 128 * q : s8 + chunks;
+  // this lane's header: row n, super-block g, in load 2g.  The selector is opaque to the
+  // compiler past the barrier, so the decode cannot be hoisted above it.
+  {
+    int hb = g;
+    asm volatile("" : "+v"(hb));
+    const uint4 h = select4(hb < 2, select4(hb == 0, v[0], v[2]), select4(hb == 2, v[4], v[6]));
+    const uint32_t s03 = h.y & 0x3F3F3F3Fu, m03 = h.z & 0x3F3F3F3Fu;
+    const uint32_t s47 = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t m47 = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+    const float dmin = half_bits_to_float(h.x >> 16);
+    // entry (b, j, n) at 16 ((4 b + j) 16 + n): the 16 rows of one (b, j) fill all LDS banks once
+    uint8_t* entry = tab + (4 * g * 16 + n) * 16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t sc = j < 2 ? s03 : s47, mn = j < 2 ? m03 : m47;
+      const int shift = 16 * (j & 1);
+      // fp16 1024 + sc of sub-blocks 2j and 2j + 1, then exactly (sc_lo, sc_hi / 16)
+      const half2_t wide = as_half2(__builtin_amdgcn_perm(kMagic, sc, (j & 1) ? 0x04030402u : 0x04010400u));
+      const half2_t mul = __builtin_elementwise_fma(wide, (half2_t){(_Float16)1.0f, (_Float16)0.0625f},
+                                                    (half2_t){(_Float16)-1024.0f, (_Float16)-64.0f});
+      const half2_t add = mul * (half2_t){(_Float16)-1024.0f, (_Float16)-1024.0f};
+      const float mlo = dmin * (float)((mn >> shift) & 0xFF), mhi = dmin * (float)((mn >> (shift + 8)) & 0xFF);
+      *reinterpret_cast<uint4*>(entry + 256 * j) =
+          make_uint4(half2_bits(mul), half2_bits(add), __float_as_uint(mlo), __float_as_uint(mhi));
+    }
+    dtab[g * 16 + n] = half_bits_to_float(h.x);
+  }
+  // the table is this wave's own: LDS accesses of one wave complete in order
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+
+  const int xm = min(n, M - 1);  // the activation row this lane supplies as the A operand
+  const uint8_t* xn = xl + xm * xrow;
+  const float* sn = s16 + xm * srow;
   float4v_t acc = {0.f, 0.f, 0.f, 0.f}, accmin = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    // the lane's two quant chunks of super-block b (register, chunk index r)
-    uint4 F, S;
-    int rF, rS;
-    if (b == 0) {
-      F = v[1]; rF = 4 + g; S = select4(g == 0, v[2], v[0]); rS = g == 0 ? 8 : g;
-    } else if (b == 1) {
-      F = v[3]; rF = 3 + g; S = select4(g < 2, v[4], v[2]); rS = g < 2 ? 7 + g : g - 1;
-    } else if (b == 2) {
-      F = v[5]; rF = 2 + g; S = select4(g < 3, v[6], v[4]); rS = g < 3 ? 6 + g : 1;
-    } else {
-      F = v[7]; rF = 1 + g; S = v[8]; rS = 5 + g;
-    }
-    const uint4 hd = shfl4(v[(9 * b) / 4], n + 16 * b);
-    const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
+    const int u = (g - b - 1) & 3;  // r - 1 of the lane's first quant chunk
+    const int jf = u >> 1, h = u & 1;
+    const uint4 F = select4(g <= b, v[2 * b + 1], v[2 * b]);
+    const uint4 S = select4(g <= b, v[2 * b + 2], v[2 * b + 1]);
+    const int sb = 4 * q + b;                    // super-block of the row
+    const int e = 256 * sb + 64 * jf + 16 * h;  // first element of chunk F's low-nibble run
+    const uint8_t* entries = tab + ((4 * b + jf) * 16 + n) * 16;
+    const float* sums = sn + 16 * sb + 4 * jf + 2 * h;
     float4v_t cs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint4 C = h == 0 ? F : S;
-      const int r = h == 0 ? rF : rS;
-      const int j = (r - 1) >> 1, half = (r - 1) & 1;
-      uint32_t scs, mns;
-      pair_codes(hd, j, scs, mns);
-      const float sc_lo = (float)(scs & 0xFF), sc_hi = (float)(scs >> 8);
-      // low: (1024 + q) sc - 1024 sc = sc q;  high: (1024 + 16 q) sc / 16 - 64 sc = sc q  (exact)
-      const uint32_t mul_lo = half2_splat(sc_lo), add_lo = half2_splat(-1024.0f * sc_lo);
-      const uint32_t mul_hi = half2_splat(sc_hi * 0.0625f), add_hi = half2_splat(-64.0f * sc_hi);
-      const int e_lo = 256 * b + 64 * j + 16 * half;  // first element of the low-nibble run
+    for (int c = 0; c < 2; ++c) {  // chunk F (pair jf), then S (pair jf + 2: 128 elements on)
+      const uint4 C = c == 0 ? F : S;
+      const uint4 E = *reinterpret_cast<const uint4*>(entries + 512 * c);
+      const float2 sx = *reinterpret_cast<const float2*>(sums + 8 * c);
+      const half2_t mul = as_half2(E.x), add = as_half2(E.y);
 #pragma unroll
       for (int nib = 0; nib < 2; ++nib) {
-        const int e = e_lo + 32 * nib;
+        // low: (1024 + q) sc - 1024 sc = sc q;  high: (1024 + 16 q) sc / 16 - 64 sc = sc q  (exact)
         const uint32_t mask = nib == 0 ? 0x0F0F0F0Fu : 0xF0F0F0F0u;
-        const uint32_t mul = nib == 0 ? mul_lo : mul_hi, add = nib == 0 ? add_lo : add_hi;
+        const half2_t m2 = nib == 0 ? mul.xx : mul.yy, a2 = nib == 0 ? add.xx : add.yy;
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
           const uint32_t ca = word(C, 2 * p) & mask, cb = word(C, 2 * p + 1) & mask;
-          const uint4 bv = make_uint4(pk_fma(magic01(ca), mul, add), pk_fma(magic23(ca), mul, add),
-                                      pk_fma(magic01(cb), mul, add), pk_fma(magic23(cb), mul, add));
-          const uint4 xa = *reinterpret_cast<const uint4*>(xn + xstep * 2 * (e + 8 * p));
+          const uint4 bv = make_uint4(half2_bits(__builtin_elementwise_fma(as_half2(magic01(ca)), m2, a2)),
+                                      half2_bits(__builtin_elementwise_fma(as_half2(magic23(ca)), m2, a2)),
+                                      half2_bits(__builtin_elementwise_fma(as_half2(magic01(cb)), m2, a2)),
+                                      half2_bits(__builtin_elementwise_fma(as_half2(magic23(cb)), m2, a2)));
+          const uint4 xa = *reinterpret_cast<const uint4*>(xn + 2 * (e + 128 * c + 32 * nib + 8 * p));
           cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, xa),
                                                       __builtin_bit_cast(half8_t, bv), cs, 0, 0, 0);
         }
-        // sum of x over the run's 16 elements: two entries of the table
-        const float2 s2 = *reinterpret_cast<const float2*>(s8n + xstep * (e >> 3));
-        const float mv = dmin * (float)(nib == 0 ? (mns & 0xFF) : (mns >> 8));
-        accmin = __builtin_amdgcn_mfma_f32_16x16x4f32(s2.x + s2.y, mv, accmin, 0, 0, 0);
+        accmin = __builtin_amdgcn_mfma_f32_16x16x4f32(nib == 0 ? sx.x : sx.y, __uint_as_float(nib == 0 ? E.z : E.w),
+                                                      accmin, 0, 0, 0);
       }
     }
-    acc += d * cs;
+    acc += dtab[b * 16 + n] * cs;
   }
   const float4v_t total = acc - accmin;
   __syncthreads();  // every wave is done with x: the partial tiles go over it
@@ -686,8 +725,12 @@ static hipError_t launch_mt(const GemvArgs& a, hipStream_t stream, bool* handled
   return wide ? launch_mt_cfg<M, 2, 3, OutT>(a, stream) : launch_mt_cfg<M, 1, 3, OutT>(a, stream);
 }
 
-static size_t sec_lds_bytes(int m, int k) {
-  return (size_t)m * (2 * k + kSecXPad) + 16 + ((size_t)m * k / 8 + 2) * sizeof(float);
+// x rows, the 16-element x sums and one header table per wave; the partial tiles of the
+// epilogue go over x.
+static size_t sec_lds_bytes(int m, int k, int waves) {
+  const size_t staged = (size_t)m * (2 * k + kSecXPad) + (size_t)m * sec_sum_row(k) * sizeof(float) +
+                        (size_t)waves * kSecTableBytes;
+  return std::max(staged, (size_t)waves * 64 * sizeof(float4v_t));
 }
 
 // Sector-aligned kernel for matrices of at least 512 tiles (gate / up, 12288 x 4096: 11.0 us
@@ -702,13 +745,20 @@ static hipError_t launch_sec(const GemvArgs& a, hipStream_t stream, bool* handle
   if (a.k % 1024 != 0 || (tiles < 512 && kw < 8) || kw > 16) return hipSuccess;
   const int per = tiles >= 768 && 3 * kw <= 16 ? 3 : tiles >= 512 && 2 * kw <= 16 ? 2 : 1;
   const int threads = per * kw * 64;
-  const size_t lds = std::max(sec_lds_bytes(M, a.k), (size_t)per * kw * 64 * sizeof(float4v_t));
+  const size_t lds = sec_lds_bytes(M, a.k, per * kw);
   // x is staged with eight 16-byte chunks per thread at most, and must fit in LDS with its sums
   if ((long)M * a.k / 8 > 8L * threads || lds > kSecMaxLds) return hipSuccess;
   *handled = true;
-  hipLaunchKernelGGL((gemv_q4k_sec<M, OutT>), dim3((tiles + per - 1) / per), dim3(threads), lds, stream,
-                     static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out),
-                     a.n, a.k, per);
+  const int grid = (tiles + per - 1) / per;
+  // x first only where every workgroup starts at once: at most one per CU of the 256
+  if (grid <= 256)
+    hipLaunchKernelGGL((gemv_q4k_sec<M, OutT, 0, true>), dim3(grid), dim3(threads), lds, stream,
+                       static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out),
+                       a.n, a.k, per);
+  else
+    hipLaunchKernelGGL((gemv_q4k_sec<M, OutT, 0, false>), dim3(grid), dim3(threads), lds, stream,
+                       static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out),
+                       a.n, a.k, per);
   return hipGetLastError();
 }
 
@@ -719,10 +769,10 @@ static hipError_t launch_sec_pair(const GemvArgs& a, const void* w2, void* out2,
   *handled = false;
   const int kw = a.k / 1024, tiles = (a.n + 15) / 16, threads = 2 * kw * 64;
   if (a.k % 1024 != 0 || kw > 8) return hipSuccess;
-  const size_t lds = std::max(sec_lds_bytes(M, a.k), (size_t)threads * sizeof(float4v_t));
+  const size_t lds = sec_lds_bytes(M, a.k, 2 * kw);
   if ((long)M * a.k / 8 > 8L * threads || lds > kSecMaxLds) return hipSuccess;
   *handled = true;
-  hipLaunchKernelGGL((gemv_q4k_sec<M, OutT, PAIR>), dim3(tiles), dim3(threads), lds, stream,
+  hipLaunchKernelGGL((gemv_q4k_sec<M, OutT, PAIR, false>), dim3(tiles), dim3(threads), lds, stream,
                      static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out),
                      a.n, a.k, 2, static_cast<const uint8_t*>(w2), static_cast<OutT*>(out2));
   return hipGetLastError();

@@ -331,15 +331,55 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
 
 // out_i[row, c] = the sum of the splits' partial sums, added in split order (so the result does
 // not depend on which workgroup finished first), converted once to the output type.
+// A thread takes four consecutive columns of one row (blockIdx.y strides over the rows): one
+// 16-byte load per split when the row width is a multiple of 4 (every row then starts
+// 16-byte aligned in each split's plane), and one 4-wide store when the four columns fall in
+// one matrix at a 4-aligned offset.
 template <typename OutT>
 __global__ __launch_bounds__(256) void gemm_reduce(const GemmJob job, int M) {
-  const size_t total = (size_t)M * job.n_total, plane = total;
-  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (size_t)gridDim.x * 256) {
-    const int row = (int)(e / job.n_total), col = (int)(e % job.n_total);
-    float sum = job.partial[e];
-    for (int z = 1; z < job.splits; ++z) sum += job.partial[z * plane + e];
-    const int mi = job.count > 1 && col >= job.col0[1] ? (job.count > 2 && col >= job.col0[2] ? 2 : 1) : 0;
-    store_out<OutT>(static_cast<OutT*>(job.out[mi]), (size_t)row * job.n[mi] + (col - job.col0[mi]), sum);
+  const int n = job.n_total;
+  const size_t plane = (size_t)M * n;
+  const int c = 4 * (blockIdx.x * 256 + threadIdx.x);
+  if (c >= n) return;
+  const bool wide = (n & 3) == 0;
+  for (int row = blockIdx.y; row < M; row += gridDim.y) {
+    const float* p = job.partial + (size_t)row * n + c;
+    float s[4];
+    if (wide) {
+      float4 v = *reinterpret_cast<const float4*>(p);
+      for (int z = 1; z < job.splits; ++z) {
+        const float4 u = *reinterpret_cast<const float4*>(p + z * plane);
+        v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+      }
+      s[0] = v.x; s[1] = v.y; s[2] = v.z; s[3] = v.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[i] = 0.f;
+        if (c + i < n) {
+          s[i] = p[i];
+          for (int z = 1; z < job.splits; ++z) s[i] += p[z * plane + i];
+        }
+      }
+    }
+    const int mi = job.count > 1 && c >= job.col0[1] ? (job.count > 2 && c >= job.col0[2] ? 2 : 1) : 0;
+    const int local = c - job.col0[mi];
+    OutT* out = static_cast<OutT*>(job.out[mi]) + (size_t)row * job.n[mi];
+    if (wide && local + 4 <= job.n[mi] && ((job.n[mi] | local) & 3) == 0) {
+      if constexpr (sizeof(OutT) == 2) {
+        *reinterpret_cast<uint2*>(out + local) = make_uint2(half2_from_fp32(s[0], s[1]), half2_from_fp32(s[2], s[3]));
+      } else {
+        *reinterpret_cast<float4*>(out + local) = make_float4(s[0], s[1], s[2], s[3]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int col = c + i;
+        if (col >= n) break;
+        const int m = job.count > 1 && col >= job.col0[1] ? (job.count > 2 && col >= job.col0[2] ? 2 : 1) : 0;
+        store_out<OutT>(static_cast<OutT*>(job.out[m]), (size_t)row * job.n[m] + (col - job.col0[m]), s[i]);
+      }
+    }
   }
 }
 
@@ -397,9 +437,9 @@ hipError_t launch_pipe(const GemmGroupArgs& a, int splits, void* workspace, hipS
   hipLaunchKernelGGL((gemm_pipe<TYPE, BM, BN, WM, WN, KS, OutT, XT>), grid, block, 0, stream,
                      static_cast<const XT*>(a.x), job, a.m, a.k);
   if (splits > 1) {
-    const size_t total = (size_t)a.m * job.n_total;
-    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
-    hipLaunchKernelGGL((gemm_reduce<OutT>), dim3(blocks), dim3(256), 0, stream, job, a.m);
+    // four columns per thread across x; rows over y (strided past 65535 rows)
+    const unsigned cols = (unsigned)((job.n_total + 1023) / 1024), rows = (unsigned)std::min(a.m, 65535);
+    hipLaunchKernelGGL((gemm_reduce<OutT>), dim3(cols, rows), dim3(256), 0, stream, job, a.m);
   }
   return hipGetLastError();
 }

@@ -44,131 +44,156 @@ class ArtifactError(ValueError):
     pass
 
 
-def _expression(value, symbols: dict) -> None:
-    """Integers, symbol references and bounded integer expressions (no Python eval)."""
-    probe = {name: 1024 for name in symbols}
+def _require(condition: bool, message: str) -> None:
+    if not condition:
+        raise ArtifactError(message)
+
+
+def _is_name(value) -> bool:
+    return isinstance(value, str) and NAME.fullmatch(value) is not None
+
+
+def _extent(value, symbols: dict, what: str, *, low: int = 1, high: int | None = None) -> None:
+    """An extent is an integer in [low, high) or an integer expression over the symbols; an
+    expression is evaluated once with every symbol at 1024 (no Python eval), so a reference
+    to an undeclared symbol or a malformed node is refused here."""
     try:
-        evaluate(value, probe)
+        evaluate(value, dict.fromkeys(symbols, 1024))
     except (ValueError, TypeError, KeyError, ZeroDivisionError) as exc:
-        raise ArtifactError(f"invalid expression {value!r}: {exc}") from exc
+        raise ArtifactError(f"{what}: invalid expression {value!r}: {exc}") from exc
+    if type(value) is int:
+        _require(value >= low and (high is None or value < high),
+                 f"{what}: {value} is outside [{low}, {high if high is not None else 'inf'})")
 
 
-def validate_manifest(manifest: object) -> dict:
-    """Schema of a `hip` bundle manifest (format.py:35-266, restricted to this provider)."""
-    if not isinstance(manifest, dict):
-        raise ArtifactError("manifest must be an object")
-    if manifest.get("format") != FORMAT or manifest.get("format_version") != FORMAT_VERSION:
-        raise ArtifactError("unsupported Tensor artifact format/version")
-    if manifest.get("provider") != PROVIDER:
-        raise ArtifactError("unsupported runtime provider")
-    if manifest.get("kind") != KIND:
-        raise ArtifactError("invalid executable kind for provider")
-    if not isinstance(manifest.get("target"), str) or not TARGET.fullmatch(manifest["target"]):
-        raise ArtifactError("invalid provider target")
+# Sections of a manifest, each checked by its own function; a later section may use what an
+# earlier one returned (symbols, then the argument table).
+
+def _identity(manifest: dict) -> None:
+    _require(manifest.get("format") == FORMAT and manifest.get("format_version") == FORMAT_VERSION,
+             f"unsupported format/version: expected {FORMAT} {FORMAT_VERSION}")
+    _require(manifest.get("provider") == PROVIDER, f"runtime provider must be {PROVIDER!r}")
+    _require(manifest.get("kind") == KIND, f"executable kind must be {KIND!r} for this provider")
+    target = manifest.get("target")
+    _require(isinstance(target, str) and TARGET.fullmatch(target) is not None, f"invalid gfx target {target!r}")
     try:
         check_requirement(manifest.get("runtime_abi"))
     except ValueError as exc:
         raise ArtifactError(str(exc)) from exc
     compiler = manifest.get("compiler")
-    if not isinstance(compiler, dict) or not isinstance(compiler.get("name"), str) or not isinstance(
-            compiler.get("version"), str):
-        raise ArtifactError("missing compiler provenance")
-    entrypoint = manifest.get("entrypoint")
-    if not isinstance(entrypoint, str) or not NAME.fullmatch(entrypoint):
-        raise ArtifactError("invalid executable entrypoint")
+    _require(isinstance(compiler, dict) and all(isinstance(compiler.get(k), str) for k in ("name", "version")),
+             "compiler provenance needs a name and a version")
+    _require(_is_name(manifest.get("entrypoint")), "the entrypoint must be an identifier")
+
+
+def _symbols(manifest: dict) -> dict:
     symbols = manifest.get("symbols", {})
-    if not isinstance(symbols, dict) or len(symbols) > 128 or any(
-            not isinstance(n, str) or not NAME.fullmatch(n) or d not in INTEGER_TYPES for n, d in symbols.items()):
-        raise ArtifactError("invalid dimension symbols")
+    _require(isinstance(symbols, dict) and len(symbols) <= 128, "symbols must be a table of at most 128")
+    for name, dtype in symbols.items():
+        _require(_is_name(name) and dtype in INTEGER_TYPES, f"invalid dimension symbol {name!r}: {dtype!r}")
+    return symbols
+
+
+def _launch(manifest: dict, symbols: dict) -> None:
     launch = manifest.get("launch")
-    if not isinstance(launch, dict) or set(launch) != {"grid", "block", "shared_memory_bytes"}:
-        raise ArtifactError("invalid launch description")
+    _require(isinstance(launch, dict) and set(launch) == {"grid", "block", "shared_memory_bytes"},
+             "launch needs exactly grid, block and shared_memory_bytes")
     for field in ("grid", "block"):
         dims = launch[field]
-        if not isinstance(dims, list) or len(dims) != 3:
-            raise ArtifactError(f"{field} must contain three dimensions")
-        for extent in dims:
-            _expression(extent, symbols)
-            if type(extent) is int and not 1 <= extent < (1 << 31):
-                raise ArtifactError(f"{field} must have positive int32 dimensions")
-    if all(type(v) is int for v in launch["block"]) and launch["block"][0] * launch["block"][1] * launch["block"][2] > 1024:
-        raise ArtifactError("launch block exceeds 1024 threads")
-    _expression(launch["shared_memory_bytes"], symbols)
-    shared = launch["shared_memory_bytes"]
-    if type(shared) is int and not 0 <= shared <= 160 * 1024:
-        raise ArtifactError("invalid shared memory size")
+        _require(isinstance(dims, list) and len(dims) == 3, f"launch {field} needs three dimensions")
+        for dim in dims:
+            _extent(dim, symbols, f"launch {field} (positive int32)", high=1 << 31)
+    block = launch["block"]
+    if all(type(v) is int for v in block):
+        _require(block[0] * block[1] * block[2] <= 1024, "a launch block holds at most 1024 threads")
+    _extent(launch["shared_memory_bytes"], symbols, "shared memory bytes", low=0, high=160 * 1024 + 1)
+
+
+def _argument_table(manifest: dict, symbols: dict) -> dict:
+    """name -> descriptor of every frontend argument, buffers checked for dtype, shape and a
+    power-of-two alignment, scalars for a dtype matching their symbol."""
     arguments = manifest.get("arguments")
-    if not isinstance(arguments, list) or not arguments or len(arguments) > 256:
-        raise ArtifactError("invalid artifact argument count")
-    names, buffers = [], set()
+    _require(isinstance(arguments, list) and 0 < len(arguments) <= 256, "arguments: 1 to 256 descriptors")
+    table = {}
     for argument in arguments:
-        if not isinstance(argument, dict):
-            raise ArtifactError("invalid argument")
+        _require(isinstance(argument, dict), "an argument descriptor must be an object")
         kind = argument.get("kind", "buffer")
-        fields = {"kind", "name", "dtype", "shape", "alignment"} if kind == "buffer" else {"kind", "name", "dtype"}
-        if set(argument) != fields or kind not in ("buffer", "scalar"):
-            raise ArtifactError("invalid argument descriptor")
+        expected = {"kind", "name", "dtype"} | ({"shape", "alignment"} if kind == "buffer" else set())
+        _require(kind in ("buffer", "scalar") and set(argument) == expected,
+                 f"argument descriptor fields must be {sorted(expected)}")
         name, dtype = argument["name"], argument["dtype"]
-        if not isinstance(name, str) or not NAME.fullmatch(name):
-            raise ArtifactError("invalid argument name")
+        _require(_is_name(name), f"argument name {name!r} is not an identifier")
+        _require(name not in table, f"duplicate argument {name}")
         if kind == "scalar":
-            if dtype not in SCALAR_TYPES or (name in symbols and symbols[name] != dtype):
-                raise ArtifactError("invalid scalar argument dtype")
+            _require(dtype in SCALAR_TYPES and symbols.get(name, dtype) == dtype, f"scalar {name}: bad dtype {dtype!r}")
         else:
-            if dtype not in BUFFER_DTYPES:
-                raise ArtifactError(f"unsupported argument dtype {dtype}")
-            if name in symbols:
-                raise ArtifactError("buffer and dimension names must be distinct")
-            buffers.add(name)
+            _require(dtype in BUFFER_DTYPES, f"buffer {name}: unsupported dtype {dtype!r}")
+            _require(name not in symbols, f"buffer {name} shadows a dimension symbol")
             shape = argument["shape"]
-            if not isinstance(shape, list) or not shape or len(shape) > 64:
-                raise ArtifactError("invalid buffer shape")
-            for extent in shape:
-                _expression(extent, symbols)
-                if type(extent) is int and extent < 1:
-                    raise ArtifactError("invalid buffer shape")
+            _require(isinstance(shape, list) and 0 < len(shape) <= 64, f"buffer {name}: shape of rank 1 to 64")
+            for dim in shape:
+                _extent(dim, symbols, f"buffer {name} shape")
             alignment = argument["alignment"]
-            if type(alignment) is not int or not 1 <= alignment <= 4096 or alignment & (alignment - 1):
-                raise ArtifactError("invalid buffer alignment")
-        names.append(name)
-    if len(names) != len(set(names)):
-        raise ArtifactError("duplicate argument")
-    if not buffers:
-        raise ArtifactError("artifact has no buffer arguments")
+            _require(type(alignment) is int and 0 < alignment <= 4096 and not alignment & (alignment - 1),
+                     f"buffer {name}: alignment must be a power of two up to 4096")
+        table[name] = argument
+    _require(any(a.get("kind", "buffer") == "buffer" for a in table.values()), "no buffer arguments")
+    return table
+
+
+def _outputs(manifest: dict, table: dict) -> None:
     outputs = manifest.get("outputs", [])
-    if not isinstance(outputs, list) or any(n not in buffers for n in outputs) or len(outputs) != len(set(outputs)):
-        raise ArtifactError("invalid output names")
+    buffers = {n for n, a in table.items() if a.get("kind", "buffer") == "buffer"}
+    _require(isinstance(outputs, list) and len(outputs) == len(set(outputs)) and set(outputs) <= buffers,
+             "each output must name a distinct buffer argument")
+
+
+def _kernel_abi(manifest: dict, table: dict, symbols: dict) -> None:
+    """The kernel's own argument list: every frontend buffer once, scalars either frontend
+    arguments or dimension symbols, each with the frontend's kind and dtype."""
     abi = manifest.get("abi")
-    if not isinstance(abi, list) or not abi or len(abi) > 256:
-        raise ArtifactError("missing or invalid kernel ABI")
-    frontend = {item["name"]: item for item in arguments}
-    abi_names = []
+    _require(isinstance(abi, list) and 0 < len(abi) <= 256, "kernel ABI: 1 to 256 entries")
+    seen = set()
     for item in abi:
-        if not isinstance(item, dict) or set(item) != {"kind", "name", "dtype"}:
-            raise ArtifactError("invalid kernel ABI argument")
-        name, kind, dtype = item["name"], item["kind"], item["dtype"]
-        original = frontend.get(name)
-        if original is not None:
-            if kind != original.get("kind", "buffer") or dtype != original["dtype"]:
-                raise ArtifactError("kernel ABI does not match frontend argument")
-        elif kind != "scalar" or symbols.get(name) != dtype:
-            raise ArtifactError(f"unmapped kernel ABI argument {name}")
-        abi_names.append(name)
-    if len(abi_names) != len(set(abi_names)) or buffers - set(abi_names):
-        raise ArtifactError("duplicate or missing kernel buffer ABI argument")
-    value = manifest.get("source_sha256")
-    if not isinstance(value, str) or not HASH.fullmatch(value):
-        raise ArtifactError("invalid source_sha256")
-    if not isinstance(manifest.get("op_set", []), list):
-        raise ArtifactError("invalid frontend operator set")
+        _require(isinstance(item, dict) and set(item) == {"kind", "name", "dtype"},
+                 "a kernel ABI entry has exactly kind, name and dtype")
+        name = item["name"]
+        frontend = table.get(name)
+        if frontend is not None:
+            _require((item["kind"], item["dtype"]) == (frontend.get("kind", "buffer"), frontend["dtype"]),
+                     f"kernel ABI entry {name} does not match frontend argument")
+        else:
+            _require(item["kind"] == "scalar" and symbols.get(name) == item["dtype"],
+                     f"unmapped kernel ABI argument {name}")
+        _require(name not in seen, f"duplicate kernel ABI entry {name}")
+        seen.add(name)
+    missing = sorted(n for n, a in table.items() if a.get("kind", "buffer") == "buffer" and n not in seen)
+    _require(not missing, f"missing kernel buffer ABI argument(s) {missing}")
+
+
+def _provenance_and_payloads(manifest: dict) -> None:
+    digest = manifest.get("source_sha256")
+    _require(isinstance(digest, str) and HASH.fullmatch(digest) is not None, "source_sha256 must be 64 hex digits")
+    _require(isinstance(manifest.get("op_set", []), list), "op_set must be a list")
     files = manifest.get("files")
-    if not isinstance(files, dict) or IMAGE not in files:
-        raise ArtifactError("missing executable payload")
-    for name, digest in files.items():
-        if not isinstance(name, str) or not (name == IMAGE or re.fullmatch(r"licenses/[A-Za-z0-9_.-]+", name)):
-            raise ArtifactError(f"invalid payload name: {name}")
-        if not isinstance(digest, str) or not HASH.fullmatch(digest):
-            raise ArtifactError(f"invalid payload hash: {name}")
+    _require(isinstance(files, dict) and IMAGE in files, f"files must list the payload {IMAGE}")
+    for name, value in files.items():
+        _require(isinstance(name, str) and (name == IMAGE or re.fullmatch(r"licenses/[A-Za-z0-9_.-]+", name)),
+                 f"invalid payload name {name!r}")
+        _require(isinstance(value, str) and HASH.fullmatch(value) is not None, f"invalid payload hash for {name}")
+
+
+def validate_manifest(manifest: object) -> dict:
+    """Schema of a `hip` bundle manifest: the reference's manifest fields (format.py:35-266)
+    restricted to this provider, checked section by section."""
+    _require(isinstance(manifest, dict), "manifest must be an object")
+    _identity(manifest)
+    symbols = _symbols(manifest)
+    _launch(manifest, symbols)
+    table = _argument_table(manifest, symbols)
+    _outputs(manifest, table)
+    _kernel_abi(manifest, table, symbols)
+    _provenance_and_payloads(manifest)
     return manifest
 
 

@@ -126,6 +126,37 @@ __device__ __forceinline__ float sum16(const uint4& a, const uint4& b) {
   return dot2(b.w, one, s);
 }
 
+// Sum of the 8 fp16 values held in one uint4.
+__device__ __forceinline__ float sum8(const uint4& a) {
+  const uint32_t one = 0x3C003C00u;
+  return dot2(a.w, one, dot2(a.z, one, dot2(a.y, one, dot2(a.x, one, 0.0f))));
+}
+
+// v plus the value of the lane a DPP control selects (CONTROL: a dpp_ctrl encoding).
+template <int CONTROL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CONTROL, 0xF, 0xF, true));
+}
+
+// v[lane] + v[lane ^ 1] + ... over the lane's quad, added as (a + b) + (c + d) in every lane of
+// it (DPP quad permutes: no LDS traffic, no lane arithmetic).
+__device__ __forceinline__ float quad_sum(float v) {
+  v = dpp_add<0xB1>(v);     // quad_perm [1, 0, 3, 2]: lane ^ 1
+  return dpp_add<0x4E>(v);  // quad_perm [2, 3, 0, 1]: lane ^ 2
+}
+
+// Total over the wave when every lane of each 16-lane row already holds its row's sum:
+// (row 0 + row 1) + (row 2 + row 3), the order of a xor-16 then xor-32 butterfly, read into
+// scalar registers with v_readlane.
+__device__ __forceinline__ float rows_total(float v) {
+  const int bits = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);

@@ -60,12 +60,8 @@ __device__ __forceinline__ float dpp_row_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v = dpp_row_sum(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
-}
+// Every lane gets the wave total (row sums by DPP, then the four rows through v_readlane).
+__device__ __forceinline__ float wave_sum_dpp(float v) { return rows_total(dpp_row_sum(v)); }
 
 // ------------------------------------------------------- M = 1, LDS x ---
 
@@ -146,10 +142,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __rest
     const int c = threadIdx.x + i * T;
     if (c < K / 8) {
       const uint4 v = xr[i];
-      // sum of the 32 x of sub-block c / 4 over the four chunks c = 4 s' .. 4 s' + 3
-      float p = sum16(v, make_uint4(0, 0, 0, 0));
-      p += __shfl_xor(p, 1, 64);
-      p += __shfl_xor(p, 2, 64);
+      // sum of the 32 x of sub-block c / 4 over the four chunks c = 4 s' .. 4 s' + 3 (one quad
+      // of lanes; K / 8 is a multiple of 4, so a quad is wholly inside or outside the range)
+      const float p = quad_sum(sum8(v));
       if ((c & 3) == 0) sxl[c >> 2] = p;
       // chunk c (16 B) -> LDS byte 16 c + 16 (c / 8): padding keeps the b128 reads conflict-free
       *reinterpret_cast<uint4*>(xlds + 16 * c + 16 * (c >> 3)) =
@@ -402,7 +397,7 @@ __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict_
       *reinterpret_cast<uint4*>(xl + m * xrow + 16 * cc) = xr[i];
       const uint32_t one = 0x3C003C00u;
       float s = dot2(xr[i].w, one, dot2(xr[i].z, one, dot2(xr[i].y, one, dot2(xr[i].x, one, 0.f))));
-      s += __shfl_xor(s, 1, 64);
+      s = dpp_add<0xB1>(s);  // + the neighbouring chunk (lane ^ 1)
       if ((lane & 1) == 0) s16[m * srow + sum_slot(cc >> 1)] = s;
     }
   }

@@ -16,6 +16,10 @@
 
 namespace tensor_gguf {
 
+// Slot of run r = e / 16 of a row (e = 256 b + 128 hh + 32 c + 16 p) in the table of run sums:
+// 16 b + 8 hh + 4 p + c, so the runs c = 0..3 that one lane reads (fixed b, hh, p) are adjacent.
+__device__ __forceinline__ int run_slot(int r) { return (r & ~15) | (r & 8) | ((r & 1) << 2) | ((r >> 1) & 3); }
+
 // Wave total in every lane: row sums by DPP (xor 1, xor 2, half mirror, mirror), then the four
 // rows through v_readlane.
 __device__ __forceinline__ float q6_wave_sum(float v) {
@@ -34,6 +38,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __res
   constexpr int ROW_BYTES = STEPS * 16 * 210;
   constexpr int T = WAVES * 64, XC = (K / 8 + T - 1) / T;  // 16-byte x chunks per thread
   __shared__ __attribute__((aligned(16))) uint8_t xlds[K * 2 + K / 4];
+  // sums of the K / 16 runs of 16 x, super-block by super-block in the order the lanes read
+  // them (see run_slot), staged with x so that no wave sums x itself
+  __shared__ __attribute__((aligned(16))) float sxl[K / 16];
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * WAVES + (threadIdx.x >> 6)) * R;
   const int slot = lane >> 2, part = lane & 3, hh = part >> 1, l0 = 16 * (part & 1);
@@ -66,7 +73,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __res
 #pragma unroll
   for (int i = 0; i < XC; ++i) {
     const int c = threadIdx.x + i * T;
-    if (c < K / 8) *reinterpret_cast<uint4*>(xlds + 16 * c + 16 * (c >> 3)) = xr[i];
+    if (c < K / 8) {
+      *reinterpret_cast<uint4*>(xlds + 16 * c + 16 * (c >> 3)) = xr[i];
+      // chunks c and c ^ 1 make one run (K / 8 is even: both lanes are in range)
+      const float s = dpp_add<0xB1>(sum8(xr[i]));
+      if ((c & 1) == 0) sxl[run_slot(c >> 1)] = s;
+    }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
@@ -77,15 +89,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __res
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
-    // the four 16-element runs 128 hh + 32 c + l0 (c = 0..3), one scale group each
+    // the four 16-element runs 128 hh + 32 c + l0 (c = 0..3), one scale group each; their
+    // sums of x are four consecutive slots
     uint4 xs[4][2];
-    float sx[4];
+    const float4 s4 = *reinterpret_cast<const float4*>(&sxl[(s * 16 + slot) * 16 + 8 * hh + 4 * (part & 1)]);
+    const float sx[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int ch = ((s * 16 + slot) * 256 + 128 * hh + 32 * c + l0) >> 3;
       xs[c][0] = *reinterpret_cast<const uint4*>(xlds + 16 * ch + 16 * (ch >> 3));
       xs[c][1] = *reinterpret_cast<const uint4*>(xlds + 16 * (ch + 1) + 16 * ((ch + 1) >> 3));
-      sx[c] = sum16(xs[c][0], xs[c][1]);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {

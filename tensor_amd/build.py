@@ -36,6 +36,12 @@ DEVICE_FLAGS = [
     f"-I{CSRC}",
 ]
 
+# The library's kernels take their leading scalar arguments preloaded into SGPRs by the
+# dispatcher (gfx950 kernel-argument preloading), so a wave's first loads do not wait on
+# scalar loads of the argument block; on firmware without the feature the compiler's
+# entry sequence loads the same registers itself.
+LIBRARY_FLAGS = [*DEVICE_FLAGS, "-mllvm", "-amdgpu-kernarg-preload-count=16"]
+
 
 def hipcc() -> str:
     for candidate in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
@@ -46,7 +52,7 @@ def hipcc() -> str:
 
 def _compile(source: Path, verbose: bool) -> Path:
     obj = BUILD / (source.stem + ".o")
-    cmd = [hipcc(), *DEVICE_FLAGS, "-c", str(source), "-o", str(obj)]
+    cmd = [hipcc(), *LIBRARY_FLAGS, "-c", str(source), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode:
         raise RuntimeError(f"hipcc failed for {source.name}:\n{result.stdout}\n{result.stderr}")
@@ -133,13 +139,14 @@ def build_executor(verbose: bool = False) -> Path | None:
 
 
 def source_hash() -> str:
-    """SHA-256 over every file the library is compiled from (csrc/ and include/, by relative
-    path and content).  build() embeds it in the library and the loader refuses a library
-    whose embedded hash differs from the sources beside it, so a stale binary is never
-    tested or benchmarked silently."""
+    """SHA-256 over the compiler flags (include paths aside) and every file the library is
+    compiled from (csrc/ and include/, by relative path and content).  build() embeds it in
+    the library and the loader refuses a library whose embedded hash differs from the sources
+    beside it, so a stale binary is never tested or benchmarked silently."""
     import hashlib
 
     digest = hashlib.sha256()
+    digest.update(" ".join(f for f in LIBRARY_FLAGS if not f.startswith("-I")).encode() + b"\0")
     files = sorted(p for d in (CSRC, ROOT / "include") for p in d.rglob("*") if p.is_file())
     for path in files:
         digest.update(str(path.relative_to(ROOT)).encode() + b"\0")

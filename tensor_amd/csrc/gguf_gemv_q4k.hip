@@ -90,31 +90,27 @@ constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
 // Byte l of a lane's quant chunks pairs with byte l of the qh run, so the fifth bit of each
 // code is OR-ed into its fp16 subnormal (bit 4 for the low nibble, bit 8 for the high nibble's
 // 16 q): every code stays below 1024 and exact.
+//
+// The arguments are plain scalars, x, the weights and the row counts first: the library is
+// built with kernel-argument preloading, so the dispatcher places them in SGPRs and the first
+// loads of a wave leave without waiting on scalar loads of the argument block (the selection
+// of the matrix is scalar arithmetic on them; only the output pointers, needed at the store,
+// are read from memory).  Matrix i takes ceil(n_i / rows-per-workgroup) consecutive
+// workgroups.
 template <int STEPS, int WAVES, int MATS, typename OutT, bool SWIGLU = false, int TYPE = kQ4_K>
-__global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __restrict__ x, GemvGroup<OutT> g) {
+__global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __restrict__ x, const uint8_t* w0,
+                                                          const uint8_t* w1, const uint8_t* w2, int n0, int n1, int n2,
+                                                          OutT* out0, OutT* out1, OutT* out2) {
   constexpr bool Q5 = TYPE == kQ5_K;
   constexpr int BLOCK = Q5 ? 176 : 144, QOFF = Q5 ? 48 : 16, SB = 16 * BLOCK;  // SB: one 4096-column step
   constexpr int K = STEPS * 4096, ROW_BYTES = STEPS * SB, T = WAVES * 64;
   constexpr int XC = (K / 8 + T - 1) / T;  // 16-byte x chunks per thread
   constexpr int PAIRS = WAVES / 2;
   static_assert(!SWIGLU || MATS == 2, "the SwiGLU pairing takes a gate and an up matrix");
+  static_assert(MATS >= 1 && MATS <= kGemvGroupMax, "one to three matrices per launch");
   __shared__ __attribute__((aligned(16))) uint8_t xlds[K * 2 + K / 4];
   __shared__ __attribute__((aligned(16))) float sxl[K / 32];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  int mat = 0, block = blockIdx.x;
-  if constexpr (SWIGLU) {
-    mat = wv >= PAIRS ? 1 : 0;
-  } else {
-#pragma unroll
-    for (int i = 1; i < MATS; ++i) {
-      if (block < g.blocks[i - 1]) break;
-      block -= g.blocks[i - 1];
-      mat = i;
-    }
-  }
-  const int n_rows = g.n[mat];
-  const int row = SWIGLU ? block * PAIRS + wv - mat * PAIRS : block * WAVES + wv;
-  const int slot = lane >> 2, j = lane & 3;
 
   uint4 xr[XC];
 #pragma unroll
@@ -122,7 +118,25 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __rest
     const int c = threadIdx.x + i * T;
     if (c < K / 8) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * c);
   }
-  const uint8_t* wl = g.w[mat] + (size_t)min(row, n_rows - 1) * ROW_BYTES + slot * BLOCK;
+  int mat = 0, block = blockIdx.x;
+  if constexpr (SWIGLU) {
+    mat = wv >= PAIRS ? 1 : 0;
+  } else {
+    const int b0 = (n0 + WAVES - 1) / WAVES, b1 = (n1 + WAVES - 1) / WAVES;
+    if (MATS > 1 && block >= b0) {
+      block -= b0;
+      mat = 1;
+      if (MATS > 2 && block >= b1) {
+        block -= b1;
+        mat = 2;
+      }
+    }
+  }
+  const uint8_t* const wm = mat == 0 ? w0 : mat == 1 ? w1 : w2;
+  const int n_rows = mat == 0 ? n0 : mat == 1 ? n1 : n2;
+  const int row = SWIGLU ? block * PAIRS + wv - mat * PAIRS : block * WAVES + wv;
+  const int slot = lane >> 2, j = lane & 3;
+  const uint8_t* wl = wm + (size_t)min(row, n_rows - 1) * ROW_BYTES + slot * BLOCK;
   const uint8_t* wq = wl + 32 * j;
   uint4 hd[STEPS], q0[STEPS], q1[STEPS];
   uint4 h0[Q5 ? STEPS : 1], h1[Q5 ? STEPS : 1];  // Q5_K: the 32 fifth-bit bytes of the super-block
@@ -207,9 +221,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __rest
     const int pair = wv - mat * PAIRS;
     if (mat == 1 && lane == 0) up_sum[pair] = v;
     __syncthreads();
-    if (mat == 0 && lane == 0 && row < n_rows) store_out<OutT>(g.out[0], (size_t)row, swiglu(v, up_sum[pair]));
+    if (mat == 0 && lane == 0 && row < n_rows) store_out<OutT>(out0, (size_t)row, swiglu(v, up_sum[pair]));
   } else {
-    if (lane == 0) store_out<OutT>(g.out[mat], (size_t)row, v);
+    if (lane == 0) store_out<OutT>(mat == 0 ? out0 : mat == 1 ? out1 : out2, (size_t)row, v);
   }
 }
 
@@ -632,14 +646,29 @@ __global__ __launch_bounds__(1024) void gemv_q4k_mt(const _Float16* __restrict__
 
 // ---------------------------------------------------------------- launch ---
 
-template <int WAVES, int MATS, typename OutT, int TYPE = kQ4_K>
-static hipError_t launch_m1(const _Float16* x, const GemvGroup<OutT>& g, int k, hipStream_t stream) {
-  const dim3 grid(g.blocks[0] + (MATS > 1 ? g.blocks[1] : 0) + (MATS > 2 ? g.blocks[2] : 0)), block(WAVES * 64);
+// Arguments of one M = 1 launch: up to three matrices sharing x (unused slots repeat matrix 0,
+// which the kernel never selects).
+template <typename OutT>
+struct M1Launch {
+  const _Float16* x;
+  const uint8_t* w[kGemvGroupMax];
+  int n[kGemvGroupMax];
+  OutT* out[kGemvGroupMax];
+};
+
+template <int STEPS, int WAVES, int MATS, typename OutT, bool SWIGLU, int TYPE>
+static void launch_m1_kernel(const M1Launch<OutT>& l, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((gemv_q4k_m1<STEPS, WAVES, MATS, OutT, SWIGLU, TYPE>), grid, dim3(WAVES * 64), 0, stream, l.x,
+                     l.w[0], l.w[1], l.w[2], l.n[0], l.n[1], l.n[2], l.out[0], l.out[1], l.out[2]);
+}
+
+template <int WAVES, int MATS, typename OutT, bool SWIGLU, int TYPE>
+static hipError_t launch_m1(const M1Launch<OutT>& l, int k, dim3 grid, hipStream_t stream) {
   switch (k / 4096) {
-    case 1: hipLaunchKernelGGL((gemv_q4k_m1<1, WAVES, MATS, OutT, false, TYPE>), grid, block, 0, stream, x, g); break;
-    case 2: hipLaunchKernelGGL((gemv_q4k_m1<2, WAVES, MATS, OutT, false, TYPE>), grid, block, 0, stream, x, g); break;
-    case 3: hipLaunchKernelGGL((gemv_q4k_m1<3, WAVES, MATS, OutT, false, TYPE>), grid, block, 0, stream, x, g); break;
-    case 4: hipLaunchKernelGGL((gemv_q4k_m1<4, WAVES, MATS, OutT, false, TYPE>), grid, block, 0, stream, x, g); break;
+    case 1: launch_m1_kernel<1, WAVES, MATS, OutT, SWIGLU, TYPE>(l, grid, stream); break;
+    case 2: launch_m1_kernel<2, WAVES, MATS, OutT, SWIGLU, TYPE>(l, grid, stream); break;
+    case 3: launch_m1_kernel<3, WAVES, MATS, OutT, SWIGLU, TYPE>(l, grid, stream); break;
+    case 4: launch_m1_kernel<4, WAVES, MATS, OutT, SWIGLU, TYPE>(l, grid, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -647,19 +676,22 @@ static hipError_t launch_m1(const _Float16* x, const GemvGroup<OutT>& g, int k, 
 
 template <int WAVES, typename OutT, int TYPE = kQ4_K>
 static hipError_t launch_m1_waves(const GemvArgs* a, int count, hipStream_t stream) {
-  GemvGroup<OutT> g{};
-  for (int i = 0; i < count; ++i) {
-    g.w[i] = static_cast<const uint8_t*>(a[i].w);
-    g.out[i] = static_cast<OutT*>(a[i].out);
-    g.n[i] = a[i].n;
-    g.blocks[i] = (a[i].n + WAVES - 1) / WAVES;
+  if (count < 1 || count > kGemvGroupMax) return hipErrorInvalidValue;
+  M1Launch<OutT> l{};
+  l.x = static_cast<const _Float16*>(a[0].x);
+  unsigned blocks = 0;
+  for (int i = 0; i < kGemvGroupMax; ++i) {
+    const GemvArgs& m = a[i < count ? i : 0];
+    l.w[i] = static_cast<const uint8_t*>(m.w);
+    l.out[i] = static_cast<OutT*>(m.out);
+    l.n[i] = m.n;
+    if (i < count) blocks += (unsigned)((m.n + WAVES - 1) / WAVES);
   }
-  const _Float16* x = static_cast<const _Float16*>(a[0].x);
+  const dim3 grid(blocks);
   switch (count) {
-    case 1: return launch_m1<WAVES, 1, OutT, TYPE>(x, g, a[0].k, stream);
-    case 2: return launch_m1<WAVES, 2, OutT, TYPE>(x, g, a[0].k, stream);
-    case 3: return launch_m1<WAVES, 3, OutT, TYPE>(x, g, a[0].k, stream);
-    default: return hipErrorInvalidValue;
+    case 1: return launch_m1<WAVES, 1, OutT, false, TYPE>(l, a[0].k, grid, stream);
+    case 2: return launch_m1<WAVES, 2, OutT, false, TYPE>(l, a[0].k, grid, stream);
+    default: return launch_m1<WAVES, 3, OutT, false, TYPE>(l, a[0].k, grid, stream);
   }
 }
 
@@ -850,22 +882,14 @@ hipError_t launch_gemv_q4k_group(const GemvArgs* a, int count, hipStream_t strea
 // M = 1 SwiGLU pairs: WAVES / 2 gate rows and the same up rows per workgroup.
 template <int WAVES, typename OutT, int TYPE>
 static hipError_t launch_m1_swiglu(const GemvArgs& a, const void* w_up, hipStream_t stream) {
-  GemvGroup<OutT> g{};
-  g.w[0] = static_cast<const uint8_t*>(a.w);
-  g.w[1] = static_cast<const uint8_t*>(w_up);
-  g.out[0] = g.out[1] = static_cast<OutT*>(a.out);
-  g.n[0] = g.n[1] = a.n;
-  g.blocks[0] = (a.n + WAVES / 2 - 1) / (WAVES / 2);
-  const _Float16* x = static_cast<const _Float16*>(a.x);
-  const dim3 grid(g.blocks[0]), block(WAVES * 64);
-  switch (a.k / 4096) {
-    case 1: hipLaunchKernelGGL((gemv_q4k_m1<1, WAVES, 2, OutT, true, TYPE>), grid, block, 0, stream, x, g); break;
-    case 2: hipLaunchKernelGGL((gemv_q4k_m1<2, WAVES, 2, OutT, true, TYPE>), grid, block, 0, stream, x, g); break;
-    case 3: hipLaunchKernelGGL((gemv_q4k_m1<3, WAVES, 2, OutT, true, TYPE>), grid, block, 0, stream, x, g); break;
-    case 4: hipLaunchKernelGGL((gemv_q4k_m1<4, WAVES, 2, OutT, true, TYPE>), grid, block, 0, stream, x, g); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  M1Launch<OutT> l{};
+  l.x = static_cast<const _Float16*>(a.x);
+  l.w[0] = static_cast<const uint8_t*>(a.w);
+  l.w[1] = l.w[2] = static_cast<const uint8_t*>(w_up);
+  l.out[0] = l.out[1] = l.out[2] = static_cast<OutT*>(a.out);
+  l.n[0] = l.n[1] = l.n[2] = a.n;
+  const dim3 grid((unsigned)((a.n + WAVES / 2 - 1) / (WAVES / 2)));
+  return launch_m1<WAVES, 2, OutT, true, TYPE>(l, a.k, grid, stream);
 }
 
 template <typename OutT, int TYPE>

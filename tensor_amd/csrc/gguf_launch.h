@@ -32,15 +32,6 @@ constexpr int kGemvMaxM = 8;
 
 // Largest number of matrices one grouped decode GEMV launch covers.
 constexpr int kGemvGroupMax = 3;
-// Matrices of one grouped launch: they share x and K; blocks[i] workgroups
-// cover matrix i.
-template <typename OutT>
-struct GemvGroup {
-  const uint8_t* w[kGemvGroupMax];
-  OutT* out[kGemvGroupMax];
-  int n[kGemvGroupMax];
-  int blocks[kGemvGroupMax];
-};
 
 hipError_t launch_gemv(const GemvArgs& args, hipStream_t stream);
 // Decode GEMV of fp32 activations at M = 1, every encoding (args.x_f32).

@@ -695,13 +695,15 @@ static hipError_t launch_m1_waves(const GemvArgs* a, int count, hipStream_t stre
   }
 }
 
-// Rows per workgroup (measured on MI355X, M = 1): 16 for K = 4096 groups of up to 16384 rows
-// (a single 12288-row gate: 7.4 us at 16, 7.8 us at 8), 8 for longer groups and longer rows
-// (gate + up 24576 rows: 13.0 us at 8, 13.8 us at 16; down 4096 x 12288: 7.6 us at 8, 8.4 us at 16).
+// Rows per workgroup (measured on MI355X, M = 1, back-to-back launches on rotated weights):
+// 4 for K = 4096 groups of 8193..16384 rows (12288 rows: 6.21 us at 4, 6.38 at 8 and 16;
+// 16384: 7.64 at 4, 7.70 at 8, 8.37 at 16), else 8 (4096 rows: 3.30 at 8, 3.29 at 16, 3.63
+// at 4; 6144: 4.09 at 8, 4.20 at 16; gate + up 24576: 10.33 at 8, 10.41 at 4, 11.6 at 16;
+// down 4096 x 12288: 6.63 at 8, 7.00 at 4, 7.37 at 16).
 static int m1_waves(const GemvArgs* a, int count) {
   long rows = 0;
   for (int i = 0; i < count; ++i) rows += a[i].n;
-  return a[0].k == 4096 && rows <= 16384 ? 16 : 8;
+  return a[0].k == 4096 && rows > 8192 && rows <= 16384 ? 4 : 8;
 }
 
 template <typename OutT, int TYPE = kQ4_K>

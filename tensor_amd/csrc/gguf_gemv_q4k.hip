@@ -2,8 +2,8 @@
 //
 // Two kernels replace the generic VALU GEMV for Q4_K:
 //
-//  * M = 1, K a multiple of 4096: gemv_q4k_m1.  A 1024-thread workgroup owns
-//    16 rows, one per wave, of one matrix of a group of up to three matrices
+//  * M = 1, K a multiple of 4096: gemv_q4k_m1.  A workgroup of 4 or 8 waves owns
+//    as many rows, one per wave, of one matrix of a group of up to three matrices
 //    that share x (gate + up, q + k + v).  It loads x first, then all of its
 //    weight bytes, and stages x once in LDS together with the per-sub-block
 //    sums of x.  Lane = (super-block slot 0..15, quant pair j 0..3): each lane
@@ -83,7 +83,7 @@ constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
 // SWIGLU = true (MATS = 2: gate, up): waves 0 .. WAVES/2-1 take rows r .. of
 // the gate matrix and the other half the same rows of the up matrix; the up
 // waves hand their sums over in LDS and the gate waves store silu(gate) * up
-// to g.out[0], so the pair's products never leave the workgroup.
+// to out0, so the pair's products never leave the workgroup.
 //
 // TYPE = kQ5_K runs Q5_K rows through the same kernel: its super-block is Q4_K's header and
 // nibbles (at byte 48) plus 32 bytes of fifth bits, bit sub of byte l for element 32 sub + l.

@@ -40,7 +40,8 @@ hipError_t launch_gemv_f32x(const GemvArgs& args, hipStream_t stream);
 // *handled to false when the shape is not covered by them.
 hipError_t launch_gemv_q4k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 // Grouped M = 1 Q4_K (or Q5_K) GEMV: `count` (<= kGemvGroupMax) matrices sharing x and K in one launch.
-bool gemv_q4k_group_supported(int m, int k);
+// n: the largest row count of the group (the kernel addresses a matrix with 32-bit offsets).
+bool gemv_q4k_group_supported(int m, int k, int n);
 // waves: rows (one per wave) per workgroup; 0 takes the default, 4 / 8 / 16 fix it (for sweeps)
 hipError_t launch_gemv_q4k_group(const GemvArgs* args, int count, hipStream_t stream, int waves = 0);
 // Two Q4_K matrices of one shape sharing x at 2 <= M <= 4 (K a multiple of 1024, at most 8192):

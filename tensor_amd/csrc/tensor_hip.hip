@@ -3,6 +3,7 @@
 // Declarations and their reference counterparts: include/tensor_hip.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -233,8 +234,10 @@ int32_t group_call(const TensorCallV1* call, TensorErrorV1* error) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
   hipError_t status = hipSuccess;
   bool paired = false;
+  int widest = 0;
+  for (int i = 0; i < count; ++i) widest = std::max(widest, args[i].n);
   if ((args[0].type == (int)TENSOR_GGML_Q4_K || args[0].type == (int)TENSOR_GGML_Q5_K) &&
-      tensor_gguf::gemv_q4k_group_supported((int)m, (int)k)) {
+      tensor_gguf::gemv_q4k_group_supported((int)m, (int)k, widest)) {
     status = tensor_gguf::launch_gemv_q4k_group(args, count, stream);
   } else if (tensor_gguf::gemv_q4k_pair_supported(args, count) &&
              (status = tensor_gguf::launch_gemv_q4k_pair(args, stream, &paired), paired)) {

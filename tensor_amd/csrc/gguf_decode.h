@@ -17,11 +17,12 @@ namespace tensor_gguf {
 template <int TYPE>
 __device__ __forceinline__ void decode8(const uint8_t* __restrict__ block, int e0, float v[8]) {
   if (TYPE == kQ4_K) {
-    const float d = half_bits_to_float(block[0] | (block[1] << 8));
-    const float dmin = half_bits_to_float(block[2] | (block[3] << 8));
+    const uint4 hd = load16(block);  // fp16 d, fp16 dmin, 12 scale bytes in one load
+    const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
     const int sub = e0 >> 5;
-    int sc, mn;
-    q4k_scale_min(block + 4, sub, sc, mn);
+    int sc_lo, mn_lo, sc_hi, mn_hi;
+    q4k_scale_pair(hd.y, hd.z, hd.w, sub >> 1, sc_lo, mn_lo, sc_hi, mn_hi);
+    const int sc = (sub & 1) ? sc_hi : sc_lo, mn = (sub & 1) ? mn_hi : mn_lo;
     const float ds = d * (float)sc, dm = dmin * (float)mn;
     const int shift = 4 * ((e0 & 63) >> 5);
     const uint2 q = load8(block + 16 + (e0 >> 6) * 32 + (e0 & 31));

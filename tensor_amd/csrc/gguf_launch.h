@@ -104,4 +104,11 @@ hipError_t launch_gemm_pipe(const GemvArgs& args, hipStream_t stream, bool* hand
 // One tile configuration of the pipelined GEMM by index (tile sweeps and tests).
 hipError_t launch_gemm_pipe_config(const GemvArgs& args, hipStream_t stream, int config);
 
+// Small-M dequant-GEMM, every encoding (M <= kSkinnyMaxM, K a multiple of 32): weights
+// dequantized into MFMA operands in registers, K split over the 8 waves of a workgroup of
+// 16 nt rows (nt 1, 2 or 4; 0 chooses by N).
+constexpr int kSkinnyMaxM = 64;
+bool gemm_skinny_supported(const GemvArgs& args);
+hipError_t launch_gemm_skinny(const GemvArgs& args, hipStream_t stream, int nt = 0);
+
 }  // namespace tensor_gguf

@@ -505,8 +505,8 @@ def test_c5_layer_chained_in_one_graph(hip_device, c_oracle, m):
     (520, 4096, 512),    # 128x128, K split 2, ragged M
     (384, 7168, 768),    # 128x128 unsplit (12 K steps do not split evenly)
     (256, 9984, 768),    # 128x64 unsplit
-    (40, 1000, 768),     # 64x64 unsplit, ragged N
-    (40, 1000, 512),     # 64x64, K split 2
+    (80, 1000, 768),     # 64x64 unsplit, ragged N (M <= 64 at N <= 4096 takes the small-M kernel)
+    (80, 1000, 512),     # 64x64, K split 2
     (256, 9984, 1024),   # 64x64, K split 4
 ])
 def test_gemm_tile_configurations(hip_device, c_oracle, encoding, m, n, k):
@@ -541,6 +541,43 @@ def test_gemm_one_hot_rows_give_dequantized_weights(hip_device, c_oracle, encodi
     got = run_linear(hip_device, "gguf_gemm", encoding, x, raw, "float32")
     # the fp32 sum of one exact product and zeros is that product (a -0.0 weight reads +0.0)
     assert np.array_equal(got, deq[:, perm].T), encoding
+
+
+@pytest.mark.parametrize("encoding,m,n,k,x_dtype", [
+    ("q4_0", 2, 1000, 1056, "float32"),    # ragged N, a last half chunk of K (K % 64 == 32)
+    ("q8_0", 33, 8200, 1056, "float32"),   # three M tiles, two 16-row tiles per workgroup
+    ("q4_k", 64, 4096, 2048, "float16"),   # four M tiles, the widest N of the K-quants
+    ("q6_k", 48, 1000, 4096, "float32"),
+    ("q5_k", 16, 3000, 1024, "float16"),
+    ("q2_k", 40, 9000, 768, "float32"),
+    ("q3_k", 7, 2000, 768, "float16"),
+    ("q4_1", 64, 8192, 1024, "float16"),
+    ("q5_0", 20, 500, 1056, "float32"),
+    ("q5_1", 3, 700, 1024, "float16"),
+])
+def test_gemm_small_m_kernel(hip_device, c_oracle, encoding, m, n, k, x_dtype):
+    """M <= 64 (every encoding; the Q4_K / Q5_K / Q6_K tiles keep N > 4096): weights decoded
+    into MFMA operands, K over the waves of a workgroup, activations through a wave-private LDS
+    tile.  Every output row against the prefill oracle (fp16 x and W, fp32 sums)."""
+    code = Q.ggml_type(encoding)
+    note("gemm-small-m", encoding, m, n, k, x_dtype)
+    x, raw = showcase_inputs(encoding, m, n, k, 600 + m)
+    x = x.astype(x_dtype)
+    expected = packed_reference(c_oracle, x, raw, code, m, n, k).reshape(m, n)
+    for out_dtype in ("float32", "float16"):
+        exe = hip_device.load("gguf_packed", encoding=encoding, m=m, n=n, k=k, x_dtype=x_dtype,
+                              out_dtype=out_dtype)
+        xb, wb = hip_device.from_numpy(x), hip_device.from_numpy(raw.reshape(-1))
+        out = hip_device.empty((m * n,), out_dtype)
+        hip_device.fill_bytes(out, 0xFF)
+        exe.launch(xb, wb, out)
+        got = out.to_numpy().reshape(m, n).astype(np.float32)
+        for b in (xb, wb, out):
+            b.release()
+        assert not np.isnan(got).any(), out_dtype
+        rows = np.linalg.norm(got - expected, axis=1) / np.linalg.norm(expected, axis=1)
+        # fp32 out: the operands are the oracle's, only the order of the fp32 sums differs
+        assert rows.max() <= (1e-5 if out_dtype == "float32" else 4 * TOLERANCE), (out_dtype, int(rows.argmax()))
 
 
 def test_gemm_zero_input_gives_exact_zero(hip_device):

@@ -12,9 +12,9 @@
 //     fp16) straight into the B operand of v_mfma_f32_16x16x32_f16, and
 //   * takes the same 8 elements of activation row 16 i + l % 16 as the A operand of tile i
 //     (fp32 activations rounded to fp16 on the way through a wave-private LDS tile),
-// so each dequantized weight feeds MT MFMAs.  The waves' fp32 tiles meet in LDS and wave 0
-// stores.  The operands are the ones the tiled GEMM stages (fp16(x), fp16(dequant(W))); only
-// the order of the fp32 additions differs.
+// so each dequantized weight feeds MT MFMAs.  The waves' fp32 tiles meet in LDS, summed in
+// wave order by all threads.  The operands are the ones the tiled GEMM stages (fp16(x),
+// fp16(dequant(W))); only the order of the fp32 additions differs.
 #include "gguf_common.h"
 #include "gguf_decode.h"
 #include "gguf_launch.h"
@@ -27,7 +27,7 @@ template <int TYPE, int MT, int NT, int SPLIT, typename OutT, typename XT>
 __global__ __launch_bounds__(SPLIT * 64) void gemm_skinny(const XT* __restrict__ x, const uint8_t* __restrict__ w,
                                                           OutT* __restrict__ out, int M, int N, int K) {
   constexpr int QK = Block<TYPE>::QK, BYTES = Block<TYPE>::BYTES;
-  __shared__ float4_t red[SPLIT > 1 ? SPLIT - 1 : 1][MT * NT][64];
+  __shared__ float red[SPLIT][MT * NT][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16 * NT;
@@ -126,35 +126,25 @@ __global__ __launch_bounds__(SPLIT * 64) void gemm_skinny(const XT* __restrict__
     __builtin_amdgcn_wave_barrier();  // the next pass rewrites the wave's tiles
   }
 
-  if constexpr (SPLIT > 1) {
-    if (wave > 0) {
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < NT; ++j) red[wave - 1][i * NT + j][lane] = acc[i][j];
-    }
-    __syncthreads();
-    if (wave > 0) return;
-    // waves 1 .. SPLIT-1 in order: the sum does not depend on which wave finished first
-#pragma unroll
-    for (int p = 0; p < SPLIT - 1; ++p)
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < NT; ++j) acc[i][j] += red[p][i * NT + j][lane];
-  }
-  // result tile (i, j): lane holds rows 16 i + 4 g + e of column n0 + 16 j + r
+  // Every wave's fp32 tiles go to LDS, row-major per 16 x 16 tile; then each thread sums
+  // outputs over the SPLIT partials in wave order (so the result does not depend on which wave
+  // finished first) and stores them: a wave instruction covers 4 rows x 16 columns.  (Wave 0
+  // alone summing all partials in the MFMA layout took ~0.5 us at M = 32.)
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int col = n0 + 16 * j + r;
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = 16 * i + 4 * g + e;
-        if (row < M && col < N) store_out<OutT>(out, (size_t)row * N + col, acc[i][j][e]);
-      }
-    }
+      for (int e = 0; e < 4; ++e) red[wave][i * NT + j][(4 * g + e) * 16 + r] = acc[i][j][e];
+  __syncthreads();
+  for (int f = threadIdx.x; f < MT * NT * 256; f += SPLIT * 64) {
+    const int tile = f >> 8, pos = f & 255;
+    float v = red[0][tile][pos];
+#pragma unroll
+    for (int p = 1; p < SPLIT; ++p) v += red[p][tile][pos];
+    const int row = 16 * (tile / NT) + (pos >> 4), col = n0 + 16 * (tile % NT) + (pos & 15);
+    if (row < M && col < N) store_out<OutT>(out, (size_t)row * N + col, v);
+  }
 }
 
 namespace {

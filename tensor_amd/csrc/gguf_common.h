@@ -157,10 +157,14 @@ __device__ __forceinline__ float rows_total(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// The wave total in every lane: row sums by DPP (xor 1, xor 2, half mirror, mirror: no LDS
+// traffic, unlike a shuffle butterfly), then the four rows through v_readlane.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
-  return v;
+  v = dpp_add<0xB1>(v);
+  v = dpp_add<0x4E>(v);
+  v = dpp_add<0x141>(v);
+  v = dpp_add<0x140>(v);
+  return rows_total(v);
 }
 
 // Q4_K: the (scale, min) 6-bit pairs of sub-blocks 2j and 2j+1 from the three

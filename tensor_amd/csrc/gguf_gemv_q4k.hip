@@ -51,18 +51,6 @@ struct PairSelect {
   }
 };
 
-__device__ __forceinline__ float dpp_row_sum(float v) {
-  // within each 16-lane row: xor 1, xor 2, half mirror, mirror
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true));
-  return v;
-}
-
-// Every lane gets the wave total (row sums by DPP, then the four rows through v_readlane).
-__device__ __forceinline__ float wave_sum_dpp(float v) { return rows_total(dpp_row_sum(v)); }
-
 // ------------------------------------------------------- M = 1, LDS x ---
 
 // Widening by bit masks alone: q & 0x000F000F is the fp16 pair (q0 * 2^-24,
@@ -239,7 +227,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __rest
     total = fmaf(-dmin * (float)(mns & 0xFF), sx.x, total);
     total = fmaf(-dmin * (float)(mns >> 8), sx.y, total);
   }
-  const float v = wave_sum_dpp(total);
+  const float v = wave_sum(total);
   if constexpr (SWIGLU) {
     __shared__ float up_sum[PAIRS];
     const int pair = wv - mat * PAIRS;

@@ -20,16 +20,6 @@ namespace tensor_gguf {
 // 16 b + 8 hh + 4 p + c, so the runs c = 0..3 that one lane reads (fixed b, hh, p) are adjacent.
 __device__ __forceinline__ int run_slot(int r) { return (r & ~15) | (r & 8) | ((r & 1) << 2) | ((r >> 1) & 3); }
 
-// Wave total in every lane: row sums by DPP (xor 1, xor 2, half mirror, mirror), then the four
-// rows through v_readlane.
-__device__ __forceinline__ float q6_wave_sum(float v) {
-  v = dpp_add<0xB1>(v);
-  v = dpp_add<0x4E>(v);
-  v = dpp_add<0x141>(v);
-  v = dpp_add<0x140>(v);
-  return rows_total(v);
-}
-
 template <int R, int STEPS, int WAVES, typename OutT>
 __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __restrict__ x,
                                                            const uint8_t* __restrict__ w,
@@ -134,7 +124,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __res
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float v = q6_wave_sum(acc[r]);
+    const float v = wave_sum(acc[r]);
     if (lane == 0 && row0 + r < n_rows) store_out<OutT>(out, (size_t)(row0 + r), v);
   }
 }

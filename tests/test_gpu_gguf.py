@@ -554,6 +554,8 @@ def test_gemm_one_hot_rows_give_dequantized_weights(hip_device, c_oracle, encodi
     ("q4_1", 64, 8192, 1024, "float16"),
     ("q5_0", 20, 500, 1056, "float32"),
     ("q5_1", 3, 700, 1024, "float16"),
+    ("q8_0", 3, 50, 32, "float32"),        # K = 32: one half chunk, only wave 0 has work
+    ("q4_0", 9, 5, 96, "float16"),         # N < 16: every row index clamped, a half chunk
 ])
 def test_gemm_small_m_kernel(hip_device, c_oracle, encoding, m, n, k, x_dtype):
     """M <= 64 (every encoding; the Q4_K / Q5_K / Q6_K tiles keep N > 4096): weights decoded

@@ -30,7 +30,7 @@ __global__ __launch_bounds__(SPLIT * 64) void gemm_skinny(const XT* __restrict__
   __shared__ float red[SPLIT][MT * NT][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16 * NT;
+  const int n0 = blockIdx.x * 16 * NT, m0 = blockIdx.y * 16 * MT;  // this workgroup's rows of W and x
   const size_t row_bytes = (size_t)(K / QK) * BYTES;
   const uint8_t* wr[NT];
 #pragma unroll
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(SPLIT * 64) void gemm_skinny(const XT* __restrict__
 #pragma unroll
         for (int h = 0; h < 16 / RPL; ++h)
           xw[u][i][h] = load16(reinterpret_cast<const uint8_t*>(
-              x + (size_t)min(16 * i + RPL * h + xrow, M - 1) * K + kc + (xcol & (second ? 63 : 31))));
+              x + (size_t)min(m0 + 16 * i + RPL * h + xrow, M - 1) * K + kc + (xcol & (second ? 63 : 31))));
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int k = kc + (t ? second : 0) + 8 * g;  // this lane's first element of step t
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(SPLIT * 64) void gemm_skinny(const XT* __restrict__
     float v = red[0][tile][pos];
 #pragma unroll
     for (int p = 1; p < SPLIT; ++p) v += red[p][tile][pos];
-    const int row = 16 * (tile / NT) + (pos >> 4), col = n0 + 16 * (tile % NT) + (pos & 15);
+    const int row = m0 + 16 * (tile / NT) + (pos >> 4), col = n0 + 16 * (tile % NT) + (pos & 15);
     if (row < M && col < N) store_out<OutT>(out, (size_t)row * N + col, v);
   }
 }
@@ -151,7 +151,7 @@ namespace {
 
 template <int TYPE, int MT, int NT, int SPLIT, typename OutT, typename XT>
 hipError_t launch_shape(const GemvArgs& a, hipStream_t stream) {
-  const dim3 grid((a.n + 16 * NT - 1) / (16 * NT)), block(SPLIT * 64);
+  const dim3 grid((a.n + 16 * NT - 1) / (16 * NT), (a.m + 16 * MT - 1) / (16 * MT)), block(SPLIT * 64);
   hipLaunchKernelGGL((gemm_skinny<TYPE, MT, NT, SPLIT, OutT, XT>), grid, block, 0, stream,
                      static_cast<const XT*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out), a.m,
                      a.n, a.k);
@@ -170,41 +170,52 @@ hipError_t launch_nt(const GemvArgs& a, int nt, hipStream_t stream) {
   }
 }
 
+// mt: 16-row M tiles per workgroup (1, 2 or 4); the M tiles beyond it go to further rows of
+// workgroups (grid y)
 template <int TYPE, typename OutT, typename XT>
-hipError_t launch_mt(const GemvArgs& a, int nt, hipStream_t stream) {
-  if (a.m <= 16) return launch_nt<TYPE, 1, OutT, XT>(a, nt, stream);
-  if (a.m <= 32) return launch_nt<TYPE, 2, OutT, XT>(a, nt, stream);
-  return launch_nt<TYPE, 4, OutT, XT>(a, nt, stream);
+hipError_t launch_mt(const GemvArgs& a, int nt, int mt, hipStream_t stream) {
+  switch (mt) {
+    case 1: return launch_nt<TYPE, 1, OutT, XT>(a, nt, stream);
+    case 2: return launch_nt<TYPE, 2, OutT, XT>(a, nt, stream);
+    case 4: return launch_nt<TYPE, 4, OutT, XT>(a, nt, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int TYPE>
-hipError_t launch_io(const GemvArgs& a, int nt, hipStream_t stream) {
+hipError_t launch_io(const GemvArgs& a, int nt, int mt, hipStream_t stream) {
   if (a.x_f32)
-    return a.out_half ? launch_mt<TYPE, _Float16, float>(a, nt, stream) : launch_mt<TYPE, float, float>(a, nt, stream);
-  return a.out_half ? launch_mt<TYPE, _Float16, _Float16>(a, nt, stream)
-                    : launch_mt<TYPE, float, _Float16>(a, nt, stream);
+    return a.out_half ? launch_mt<TYPE, _Float16, float>(a, nt, mt, stream)
+                      : launch_mt<TYPE, float, float>(a, nt, mt, stream);
+  return a.out_half ? launch_mt<TYPE, _Float16, _Float16>(a, nt, mt, stream)
+                    : launch_mt<TYPE, float, _Float16>(a, nt, mt, stream);
 }
 
 }  // namespace
 
 bool gemm_skinny_supported(const GemvArgs& a) { return a.m >= 1 && a.m <= kSkinnyMaxM && a.k % 32 == 0; }
 
-hipError_t launch_gemm_skinny(const GemvArgs& a, hipStream_t stream, int nt) {
+hipError_t launch_gemm_skinny(const GemvArgs& a, hipStream_t stream, int nt, int mt) {
   if (!gemm_skinny_supported(a)) return hipErrorInvalidValue;
-  // one 16-row tile per workgroup unless N is wide enough to fill the CUs with pairs (M = 64,
-  // N = 12288: 58 against 64 us; at M <= 16 the single tiles stay ahead)
+  // one 16-row tile of W per workgroup unless N is wide enough to fill the CUs with pairs (M =
+  // 64, N = 12288: 58 against 64 us; at M <= 16 the single tiles stay ahead)
   if (nt == 0) nt = a.n >= 8192 && a.m > 16 ? 2 : 1;
+  // one 16-row tile of x per workgroup while that keeps the grid within one round of 256
+  // workgroups (each then reads a quarter or half of x and decodes its weights again from L2:
+  // N = K = 1024, M = 64: Q4_0 6.4 -> 4.2 us, M = 32: 4.6 -> 4.0 us), else all of them
+  const int mtiles = (a.m + 15) / 16, ntiles = (a.n + 16 * nt - 1) / (16 * nt);
+  if (mt == 0) mt = (long)ntiles * mtiles <= 256 ? 1 : mtiles <= 1 ? 1 : mtiles <= 2 ? 2 : 4;
   switch (a.type) {
-    case kQ4_0: return launch_io<kQ4_0>(a, nt, stream);
-    case kQ4_1: return launch_io<kQ4_1>(a, nt, stream);
-    case kQ5_0: return launch_io<kQ5_0>(a, nt, stream);
-    case kQ5_1: return launch_io<kQ5_1>(a, nt, stream);
-    case kQ8_0: return launch_io<kQ8_0>(a, nt, stream);
-    case kQ2_K: return launch_io<kQ2_K>(a, nt, stream);
-    case kQ3_K: return launch_io<kQ3_K>(a, nt, stream);
-    case kQ4_K: return launch_io<kQ4_K>(a, nt, stream);
-    case kQ5_K: return launch_io<kQ5_K>(a, nt, stream);
-    case kQ6_K: return launch_io<kQ6_K>(a, nt, stream);
+    case kQ4_0: return launch_io<kQ4_0>(a, nt, mt, stream);
+    case kQ4_1: return launch_io<kQ4_1>(a, nt, mt, stream);
+    case kQ5_0: return launch_io<kQ5_0>(a, nt, mt, stream);
+    case kQ5_1: return launch_io<kQ5_1>(a, nt, mt, stream);
+    case kQ8_0: return launch_io<kQ8_0>(a, nt, mt, stream);
+    case kQ2_K: return launch_io<kQ2_K>(a, nt, mt, stream);
+    case kQ3_K: return launch_io<kQ3_K>(a, nt, mt, stream);
+    case kQ4_K: return launch_io<kQ4_K>(a, nt, mt, stream);
+    case kQ5_K: return launch_io<kQ5_K>(a, nt, mt, stream);
+    case kQ6_K: return launch_io<kQ6_K>(a, nt, mt, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -106,9 +106,9 @@ hipError_t launch_gemm_pipe_config(const GemvArgs& args, hipStream_t stream, int
 
 // Small-M dequant-GEMM, every encoding (M <= kSkinnyMaxM, K a multiple of 32): weights
 // dequantized into MFMA operands in registers, K split over the 8 waves of a workgroup of
-// 16 nt rows (nt 1, 2 or 4; 0 chooses by N).
+// 16 nt rows of W (nt 1, 2 or 4) and 16 mt rows of x (mt 1, 2 or 4); 0 chooses by shape.
 constexpr int kSkinnyMaxM = 64;
 bool gemm_skinny_supported(const GemvArgs& args);
-hipError_t launch_gemm_skinny(const GemvArgs& args, hipStream_t stream, int nt = 0);
+hipError_t launch_gemm_skinny(const GemvArgs& args, hipStream_t stream, int nt = 0, int mt = 0);
 
 }  // namespace tensor_gguf

@@ -1,12 +1,13 @@
 // Small-M prefill dequant-GEMM (gfx950), every encoding: out[m, n] = sum_k fp16(x[m, k]) *
-// fp16(W[n, k]) with fp32 accumulation, for 2 <= M <= 64 (the showcase's M = 32 prefill at
+// fp16(W[n, k]) with fp32 accumulation, for M <= 64 (the showcase's M = 32 prefill at
 // N = K = 1024 among them: benchmarks/kernels/showcase/benchmark.py:122-126, :460-464).
 //
 // At these shapes the tiled GEMM has few output tiles (8-16 workgroups of 128 or 64 columns for
 // N = 1024) and each walks the whole of K, so its time is the latency of one long K loop.  Here
-// a workgroup owns 16 NT weight rows, and its SPLIT waves take interleaved 32-element K steps
-// (wave v: steps v, v + SPLIT, ..), so the K loop is SPLIT times shorter and N / 16 / NT
-// workgroups run at once.  No LDS tiles: in each step lane l
+// a workgroup owns 16 NT weight rows and 16 MT activation rows, and its SPLIT waves take
+// interleaved 64-element chunks of K (wave v: chunks v, v + SPLIT, ..), so the K loop is SPLIT
+// times shorter and N / (16 NT) x M / (16 MT) workgroups run at once.  No LDS tile of weights:
+// in each 32-element step lane l
 //   * dequantizes the 8 elements 8 (l / 16) .. + 7 of weight row l % 16 of every 16-row tile
 //     with the shared per-element decoder (the reference's fp32 arithmetic, then one cast to
 //     fp16) straight into the B operand of v_mfma_f32_16x16x32_f16, and

@@ -37,12 +37,15 @@ __device__ __forceinline__ void decode8(const uint8_t* __restrict__ block, int e
     const float sc = (float)(int8_t)block[192 + (e0 >> 4)];
     const uint2 lo = load8(block + 64 * half + 32 * (quarter & 1) + l);
     const uint2 hi = load8(block + 128 + 32 * half + l);
+    // the four 6-bit codes of a dword assembled with byte masks; (q - 32) * (sc * d) is the
+    // reference's (q - 32) * sc * d bit for bit: every product is exact, sign of zero included
+    const float scd = sc * d;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t lb = ((i < 4 ? lo.x : lo.y) >> (8 * (i & 3))) & 0xFFu;
-      const uint32_t hb = ((i < 4 ? hi.x : hi.y) >> (8 * (i & 3))) & 0xFFu;
-      const int q = (int)(((lb >> (4 * (quarter >> 1))) & 15u) | (((hb >> (2 * quarter)) & 3u) << 4));
-      v[i] = (float)(q - 32) * sc * d;
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t codes = (((w ? lo.y : lo.x) >> (4 * (quarter >> 1))) & 0x0F0F0F0Fu) |
+                             ((((w ? hi.y : hi.x) >> (2 * quarter)) & 0x03030303u) << 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[4 * w + i] = ((float)((codes >> (8 * i)) & 0xFFu) - 32.0f) * scd;
     }
   } else if (TYPE == kQ8_0) {
     const float d = half_bits_to_float(block[0] | (block[1] << 8));

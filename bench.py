@@ -554,6 +554,13 @@ def detail_cases(device):
         gemv_case(f"C2_q4k_gemv_m{m}_12288x4096", "q4_k", m, 12288, 4096, "float16")
         gemv_case(f"C2_q4k_gemv_m{m}_4096x12288", "q4_k", m, 4096, 12288, "float16")
     gemv_case("C3_q6k_lm_head_m1_151936x4096_fp32", "q6_k", 1, 151936, 4096, "float32")
+    # one GPU's share of an 8-way tensor-parallel decode step: column-parallel gate (and up)
+    # rows, the row-parallel down's K slice (its partial sums would then be all-reduced), the
+    # vocab-parallel LM head
+    gemv_case("shard8_q4k_gate_m1_1536x4096", "q4_k", 1, 1536, 4096, "float16")
+    gemv_case("shard8_q4k_down_m1_4096x1536", "q4_k", 1, 4096, 1536, "float16")
+    gemv_case("shard8_q6k_down_m1_4096x1536", "q6_k", 1, 4096, 1536, "float16")
+    gemv_case("shard8_q6k_lm_head_m1_18992x4096_fp32", "q6_k", 1, 18992, 4096, "float32")
     for encoding in ("q6_k", "q8_0", "q4_0", "q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q5_k"):
         gemv_case(f"enc_{encoding}_gemv_m1_12288x4096", encoding, 1, 12288, 4096, "float16")
 

@@ -110,9 +110,13 @@ def test_gemv_parity_small(hip_device, encoding, m, k):
     ("q6_k", 4096, 12288, 1, "float16"),   # C5 down (Q6_K)
     ("q6_k", 1001, 12288, 1, "float32"),   # three steps per row, ragged last workgroup
     ("q8_0", 4096, 4096, 1, "float16"),    # C1 shape
-    ("q5_k", 12288, 4096, 1, "float16"),   # Q5_K through the M = 1 kernel (16 rows per workgroup)
+    ("q5_k", 12288, 4096, 1, "float16"),   # Q5_K through the M = 1 kernel (4 rows per workgroup)
     ("q5_k", 4096, 12288, 1, "float32"),   # three 4096-column steps, 8 rows per workgroup
     ("q5_k", 1003, 16384, 1, "float16"),   # four steps, ragged last workgroup
+    ("q4_k", 1536, 4096, 1, "float16"),    # one GPU's rows of an 8-way gate
+    ("q4_k", 4096, 1536, 1, "float16"),    # one GPU's K slice of an 8-way down (generic kernel)
+    ("q6_k", 4096, 1536, 1, "float16"),
+    ("q6_k", 18992, 4096, 1, "float32"),   # one GPU's rows of an 8-way LM head
 ])
 def test_gemv_parity_baseline_shapes(hip_device, c_oracle, encoding, n, k, m, out_dtype):
     code = Q.ggml_type(encoding)

@@ -218,14 +218,14 @@ static hipError_t launch_tile(const GemvArgs& a, hipStream_t stream) {
 // on the generic tiles, and for Q4_K / Q5_K / Q6_K also N <= 4096 (at N = 12288 their
 // pipelined tiles are faster from M = 16: Q4_K M = 32, K = 4096: 33.6 against 38.4 us; at
 // N = K = 1024, M = 32 the small-M kernel takes 5.3 against 10.4 us, Q4_0 4.9 against 30.6).
-static bool small_m(const GemvArgs& a) {
+bool gemm_small_m(const GemvArgs& a) {
   const bool pipelined = a.type == kQ4_K || a.type == kQ5_K || a.type == kQ6_K;
   return gemm_skinny_supported(a) && (!pipelined || a.n <= 4096);
 }
 
 template <int TYPE, typename OutT>
 static hipError_t launch_type(const GemvArgs& a, hipStream_t stream) {
-  if (small_m(a)) return launch_gemm_skinny(a, stream);
+  if (gemm_small_m(a)) return launch_gemm_skinny(a, stream);
   bool handled = false;
   const hipError_t status = launch_gemm_pipe(a, stream, &handled);
   if (handled) return status;

@@ -110,5 +110,7 @@ hipError_t launch_gemm_pipe_config(const GemvArgs& args, hipStream_t stream, int
 constexpr int kSkinnyMaxM = 64;
 bool gemm_skinny_supported(const GemvArgs& args);
 hipError_t launch_gemm_skinny(const GemvArgs& args, hipStream_t stream, int nt = 0, int mt = 0);
+// Whether launch_gemm takes the small-M kernel for this shape.
+bool gemm_small_m(const GemvArgs& args);
 
 }  // namespace tensor_gguf

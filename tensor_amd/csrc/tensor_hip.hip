@@ -441,23 +441,26 @@ int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has
   }
   hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
   hipError_t status = hipSuccess;
-  if (format.qk == 256 && (group.type == (int)TENSOR_GGML_Q4_K || group.type == (int)TENSOR_GGML_Q5_K ||
-                           group.type == (int)TENSOR_GGML_Q6_K)) {
+  tensor_gguf::GemvArgs one[tensor_gguf::kGemmGroupMax];
+  bool small = true;  // every matrix on the small-M kernel, as tensor_gguf_gemm_v1 would run it
+  for (int i = 0; i < count; ++i) {
+    one[i].x = group.x;
+    one[i].w = group.w[i];
+    one[i].out = group.out[i];
+    one[i].type = group.type;
+    one[i].m = group.m;
+    one[i].n = group.n[i];
+    one[i].k = group.k;
+    one[i].out_half = group.out_half;
+    small = small && tensor_gguf::gemm_small_m(one[i]);
+  }
+  if (!small && format.qk == 256 && (group.type == (int)TENSOR_GGML_Q4_K || group.type == (int)TENSOR_GGML_Q5_K ||
+                                     group.type == (int)TENSOR_GGML_Q6_K)) {
     status = tensor_gguf::launch_gemm_group_plan(group, plan, workspace, workspace_bytes, stream);
   } else {
-    // the other encodings take the generic GEMM, one launch per matrix in order
-    for (int i = 0; i < count && status == hipSuccess; ++i) {
-      tensor_gguf::GemvArgs one;
-      one.x = group.x;
-      one.w = group.w[i];
-      one.out = group.out[i];
-      one.type = group.type;
-      one.m = group.m;
-      one.n = group.n[i];
-      one.k = group.k;
-      one.out_half = group.out_half;
-      status = tensor_gguf::launch_gemm(one, stream);
-    }
+    // the other encodings, and small M, one launch per matrix in order (no workspace: such
+    // plans never split K)
+    for (int i = 0; i < count && status == hipSuccess; ++i) status = tensor_gguf::launch_gemm(one[i], stream);
   }
   if (status != hipSuccess) return hip_fail(error, status, "GGUF grouped GEMM launch");
   return TENSOR_OK;

@@ -807,6 +807,8 @@ def run_gemm_group(device, encoding, x, raws, out_dtype, workspace_bytes=None):
     ("q5_k", 300, 8192, (1000, 77), True),           # ragged M and N, Q5_K
     ("q6_k", 200, 8192, (300, 500, 64), True),       # three ragged matrices, K >= 8192
     ("q8_0", 64, 1024, (300, 100), False),           # other encodings: one generic launch per matrix
+    ("q4_k", 32, 4096, (4096, 1024, 1024), False),   # q + k + v at M=32: the small-M kernel per matrix
+    ("q6_k", 48, 2048, (3000, 100), False),          # small M, ragged rows, Q6_K
 ])
 def test_gemm_group_parity(hip_device, c_oracle, encoding, m, k, rows, split):
     code = Q.ggml_type(encoding)

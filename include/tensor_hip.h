@@ -126,7 +126,8 @@ int32_t tensor_gguf_gemv_group_v1(const TensorCallV1 *call, TensorErrorV1 *error
  * leaves most CUs idle, K is split across workgroups: each writes fp32 partial sums into the
  * workspace and a second kernel adds them in split order (deterministic) and converts; the
  * split is chosen to fit the workspace given (any size; a short one only limits the split).
- * Q4_K, Q5_K and Q6_K use the pipelined kernel; the other encodings, and M <= 64 where every
+ * Q4_K, Q5_K, Q6_K, Q8_0 and Q4_0 use the pipelined kernel (Q8_0 / Q4_0 where K is an even
+ * number of 64-element steps); the other encodings and shapes, and M <= 64 where every
  * N_i <= 4096, take one launch per matrix as tensor_gguf_gemm_v1 runs it.  Arguments, in order:
  *   0        x         buffer fp16  [M, K]
  *   2i+1     w_i       buffer uint8 [N_i, K/QK*BLOCK]

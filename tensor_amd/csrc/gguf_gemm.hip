@@ -214,13 +214,14 @@ static hipError_t launch_tile(const GemvArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// The small-M kernel where the tiled kernels leave most CUs idle: M <= 64 for the encodings
-// on the generic tiles, and for Q4_K / Q5_K / Q6_K also N <= 4096 (at N = 12288 their
-// pipelined tiles are faster from M = 16: Q4_K M = 32, K = 4096: 33.6 against 38.4 us; at
-// N = K = 1024, M = 32 the small-M kernel takes 5.3 against 10.4 us, Q4_0 4.9 against 30.6).
+// The small-M kernel where the tiled kernels leave most CUs idle: M <= 64 for shapes on the
+// generic tiles, and for shapes the pipelined tiles take also N <= 4096 (at N = 12288 those are
+// faster from M = 16: Q4_K M = 32, K = 4096: 33.6 against 38.4 us, Q4_0 with fp16 x 23.4
+// against 40.9; at N = K = 1024, M = 32 the small-M kernel takes 5.3 against 10.4 us, Q4_0
+// 4.9 against 30.6).  Q8_0 with fp32 x keeps it to M = 16 (33.7 against 42.8 us at N = 12288).
 bool gemm_small_m(const GemvArgs& a) {
-  const bool pipelined = a.type == kQ4_K || a.type == kQ5_K || a.type == kQ6_K;
-  return gemm_skinny_supported(a) && (!pipelined || a.n <= 4096);
+  if (!gemm_skinny_supported(a)) return false;
+  return !gemm_pipe_supported(a) || a.n <= 4096 || (a.type == kQ8_0 && a.x_f32 && a.m <= 16);
 }
 
 template <int TYPE, typename OutT>

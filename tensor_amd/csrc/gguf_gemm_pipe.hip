@@ -1,4 +1,4 @@
-// Pipelined fused dequant-GEMM for the K-quants (Q4_K, Q6_K) on gfx950:
+// Pipelined fused dequant-GEMM for Q4_K, Q5_K, Q6_K, Q8_0 and Q4_0 on gfx950:
 // out[m, n] = sum_k fp16(x[m, k]) * fp16(W[n, k]), fp32 accumulation
 // (reference kernel: AKAS _packed, benchmarks/kernels/showcase/kernels.py:114-119;
 //  Triton restatement triton_kernels.py:185-211).
@@ -24,6 +24,8 @@
 //   Q6_K (triton_kernels.py:163-180): a step covers quarters 2(s%2), 2(s%2)+1
 //     of half h = (s%4)/2: the 64 low-nibble bytes of ql for that half (nibble
 //     s%2), the 32 qh bytes of the half (2 bits per quarter) and 4 scales.
+//   Q8_0 / Q4_0 (triton_kernels.py:135-142 for Q4_0): a step is two whole
+//     32-element blocks, d * q and (q - 8) * d.
 #include <algorithm>
 
 #include "gguf_common.h"
@@ -76,6 +78,20 @@ struct Geometry<kQ6_K, TPR> {
   static constexpr int W0 = EPT / 4, W1 = EPT / 4 + 2;  // ql dwords; qh dwords + scales + d
 };
 
+// Q8_0 / Q4_0: a step is two 32-element blocks (68 / 36 bytes).  TPR threads per weight row
+// share the step's quant bytes (64 / 32): thread p takes QB of them, all in block
+// QB p / QPB at byte QB p % QPB (QPB = quant bytes per block), and that block's fp16 d.
+template <int TPR>
+struct Geometry<kQ8_0, TPR> {
+  static constexpr int QPB = 32, QB = 2 * QPB / TPR;
+  static constexpr int W0 = QB / 4, W1 = 2;  // dwords: quants; d (low half), unused
+};
+template <int TPR>
+struct Geometry<kQ4_0, TPR> {
+  static constexpr int QPB = 16, QB = 2 * QPB / TPR;
+  static constexpr int W0 = QB / 4, W1 = 2;
+};
+
 // Raw bytes of one step in vector registers (vector values stay in VGPRs; arrays of
 // several sets were demoted to the stack). x: XL 16-byte activation chunks.
 template <int XL, int W0, int W1>
@@ -112,8 +128,9 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
   static_assert(XL * THREADS == BM * 8 && TPR * BN == THREADS && (TPR == 1 || TPR == 2 || TPR == 4), "tile shape");
   using G = Geometry<TYPE, TPR>;
   using RawT = Raw<XL, G::W0, G::W1>;
-  constexpr int BYTES = Block<TYPE>::BYTES;
+  constexpr int QK = Block<TYPE>::QK, BYTES = Block<TYPE>::BYTES;
   constexpr bool KQ = TYPE == kQ4_K || TYPE == kQ5_K;  // Q4_K's header and nibble layout
+  constexpr bool B32 = TYPE == kQ8_0 || TYPE == kQ4_0;  // 32-element blocks, two per step
   constexpr int STAGE = 2 * (BM + BN) * ROW;  // halves of one group's double-buffered tiles
   __shared__ __attribute__((aligned(16))) _Float16 stage[KS * STAGE];
   // wave-uniform (THREADS is a multiple of 64): keeps the step counter and the
@@ -132,9 +149,9 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
   const int N = job.n[mi];
   const int m0 = blockIdx.y * BM, n0 = (tile - (mi ? job.tile_end[mi - 1] : 0)) * BN;
   const int wrow = tid / TPR, wpart = tid % TPR;
-  const uint8_t* wbase = job.w[mi] + (size_t)min(n0 + wrow, N - 1) * (size_t)(K >> 8) * BYTES;
-  // this group's steps of this split; the host guarantees steps % (4 KS splits) == 0, so every
-  // group starts on a super-block
+  const uint8_t* wbase = job.w[mi] + (size_t)min(n0 + wrow, N - 1) * (size_t)(K / QK) * BYTES;
+  // this group's steps of this split; the host guarantees that every group takes an even number
+  // of steps and (for the 256-element encodings) starts on a super-block
   const int split_steps = K / BK / job.splits;
   const int steps = split_steps / KS, first = blockIdx.z * split_steps + group * steps;
 
@@ -157,8 +174,24 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
         r.x[4 * i] = v.x; r.x[4 * i + 1] = v.y; r.x[4 * i + 2] = v.z; r.x[4 * i + 3] = v.w;
       }
     }
-    const uint8_t* blk = wbase + (size_t)(k0 >> 8) * BYTES;
-    if constexpr (KQ) {
+    const uint8_t* blk = wbase + (size_t)(k0 / QK) * BYTES;
+    if constexpr (B32) {
+      constexpr int QPB = G::QPB, QB = G::QB;
+      const uint8_t* b = blk + (QB * wpart / QPB) * BYTES;  // this thread's block: fp16 d, quants
+      const uint8_t* q = b + 2 + QB * wpart % QPB;
+      if constexpr (G::W0 % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < G::W0; i += 4) {
+          const uint4 v = load16(q + 4 * i);
+          r.a[i] = v.x; r.a[i + 1] = v.y; r.a[i + 2] = v.z; r.a[i + 3] = v.w;
+        }
+      } else {
+        const uint2 v = load8(q);
+        r.a[0] = v.x; r.a[1] = v.y;
+      }
+      r.b[0] = load4(b);
+      r.b[1] = 0;
+    } else if constexpr (KQ) {
       const uint4 hd = load16(blk);
       r.b[0] = hd.x; r.b[1] = hd.y; r.b[2] = hd.z; r.b[3] = hd.w;
       const uint8_t* q = blk + (TYPE == kQ5_K ? 48 : 16) + 32 * (step & 3) + G::QB * wpart;
@@ -189,7 +222,32 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
       const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
       *reinterpret_cast<uint4*>(&xs[row * ROW + c8]) = make_uint4(r.x[4 * i], r.x[4 * i + 1], r.x[4 * i + 2], r.x[4 * i + 3]);
     }
-    if constexpr (KQ) {
+    if constexpr (B32) {
+      constexpr int QPB = G::QPB, QB = G::QB;
+      const float d = half_bits_to_float(r.b[0]);
+      // element e of block b (32 b + e in the step) sits at ws[wrow][32 b + e]
+      _Float16* dst = &ws[wrow * ROW + 32 * (QB * wpart / QPB) + QB * wpart % QPB];
+      if constexpr (TYPE == kQ8_0) {
+        // d * q for the int8 code q, as the fp16 subnormal code q + 128 (byte ^ 0x80) times
+        // d 2^24 plus -128 d: the product and the sum (q d) are exact, so is the fp32 value
+        const float d24 = d * kTwo24, bias = -128.0f * d;
+#pragma unroll
+        for (int i = 0; i < G::W0; ++i) {
+          const uint32_t u = r.a[i] ^ 0x80808080u;
+          *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(u & 0x00FF00FFu, (u >> 8) & 0x00FF00FFu, d24, bias);
+        }
+      } else {
+        // (q - 8) * d: byte j's low nibble is element j, its high nibble element j + 16
+        const float d24 = d * kTwo24, bias = -8.0f * d;
+#pragma unroll
+        for (int i = 0; i < G::W0; ++i) {
+          const uint32_t q = r.a[i];
+          *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(q & 0x000F000Fu, (q >> 8) & 0x000F000Fu, d24, bias);
+          *reinterpret_cast<uint2*>(dst + 16 + 4 * i) =
+              affine4((q >> 4) & 0x000F000Fu, (q >> 12) & 0x000F000Fu, d24, bias);
+        }
+      }
+    } else if constexpr (KQ) {
       int sc_lo, mn_lo, sc_hi, mn_hi;
       q4k_scale_pair(r.b[1], r.b[2], r.b[3], step & 3, sc_lo, mn_lo, sc_hi, mn_hi);
       const float d = half_bits_to_float(r.b[0]), dmin = half_bits_to_float(r.b[0] >> 16);
@@ -468,13 +526,18 @@ hipError_t launch_typed(const GemmGroupArgs& a, int tile, int splits, void* work
                     : launch_tile<TYPE, float, _Float16>(a, tile, splits, workspace, stream);
 }
 
-bool pipe_type(int type) { return type == kQ4_K || type == kQ5_K || type == kQ6_K; }
+bool pipe_type(int type) {
+  return type == kQ4_K || type == kQ5_K || type == kQ6_K || type == kQ8_0 || type == kQ4_0;
+}
 
-// A tile and split count that fit the shape: the steps of a split divide evenly into the
-// workgroup's wave groups, each starting on a super-block.
+// A tile and split count that fit the shape: K is whole 64-element steps, and the steps of a
+// split divide evenly into the workgroup's wave groups, each taking an even number of them (the
+// main loop runs two steps per pass) that starts on a super-block (4 steps) for the 256-element
+// encodings.
 bool valid_plan(const GemmGroupArgs& a, int tile, int splits) {
-  const int steps = a.k / pipe::BK;
-  return tile >= 0 && tile < 8 && splits >= 1 && steps % (4 * kTiles[tile].ks * splits) == 0;
+  const int steps = a.k / pipe::BK, unit = a.type == kQ8_0 || a.type == kQ4_0 ? 2 : 4;
+  return tile >= 0 && tile < 8 && splits >= 1 && a.k % pipe::BK == 0 &&
+         steps % (unit * kTiles[tile].ks * splits) == 0;
 }
 
 // Largest tile that still gives the 256 CUs work: the workgroup count of a tile must reach
@@ -484,7 +547,7 @@ bool valid_plan(const GemmGroupArgs& a, int tile, int splits) {
 constexpr long kMinBlocks = 160;
 
 int base_tile(const GemmGroupArgs& a) {
-  const int steps = a.k / pipe::BK;  // a multiple of 4 (K is whole super-blocks)
+  const int steps = a.k / pipe::BK;  // even (whole 32-element block pairs or super-blocks)
   if (tile_count(a, kTiles[0]) >= kMinBlocks) return 0;
   if (tile_count(a, kTiles[1]) >= kMinBlocks) return steps % 8 == 0 ? 4 : 1;
   if (steps % 16 == 0) return 7;
@@ -522,12 +585,20 @@ size_t gemm_group_workspace(const GemmGroupArgs& a, const GemmPlan& plan) {
 
 hipError_t launch_gemm_group_plan(const GemmGroupArgs& a, const GemmPlan& plan, void* workspace,
                                   size_t workspace_bytes, hipStream_t stream) {
-  if (!pipe_type(a.type) || a.count < 1 || a.count > kGemmGroupMax || !valid_plan(a, plan.tile, plan.splits) ||
+  if (!gemm_group_pipelined(a, plan) || a.count < 1 || a.count > kGemmGroupMax ||
       gemm_group_workspace(a, plan) > workspace_bytes || (plan.splits > 1 && !workspace))
     return hipErrorInvalidValue;
-  if (a.type == kQ4_K) return launch_typed<kQ4_K>(a, plan.tile, plan.splits, workspace, stream);
-  if (a.type == kQ5_K) return launch_typed<kQ5_K>(a, plan.tile, plan.splits, workspace, stream);
-  return launch_typed<kQ6_K>(a, plan.tile, plan.splits, workspace, stream);
+  switch (a.type) {
+    case kQ4_K: return launch_typed<kQ4_K>(a, plan.tile, plan.splits, workspace, stream);
+    case kQ5_K: return launch_typed<kQ5_K>(a, plan.tile, plan.splits, workspace, stream);
+    case kQ6_K: return launch_typed<kQ6_K>(a, plan.tile, plan.splits, workspace, stream);
+    case kQ8_0: return launch_typed<kQ8_0>(a, plan.tile, plan.splits, workspace, stream);
+    default: return launch_typed<kQ4_0>(a, plan.tile, plan.splits, workspace, stream);
+  }
+}
+
+bool gemm_group_pipelined(const GemmGroupArgs& a, const GemmPlan& plan) {
+  return pipe_type(a.type) && valid_plan(a, plan.tile, plan.splits);
 }
 
 static GemmGroupArgs single(const GemvArgs& a) {
@@ -550,11 +621,17 @@ hipError_t launch_gemm_pipe_config(const GemvArgs& a, hipStream_t stream, int co
   return launch_gemm_group_plan(single(a), GemmPlan{config, 1}, nullptr, 0, stream);
 }
 
-hipError_t launch_gemm_pipe(const GemvArgs& a, hipStream_t stream, bool* handled) {
-  *handled = pipe_type(a.type);
-  if (!*handled) return hipSuccess;
+bool gemm_pipe_supported(const GemvArgs& a) {
   const GemmGroupArgs g = single(a);
-  return launch_gemm_group_plan(g, plan_gemm_group(g, 0), nullptr, 0, stream);
+  return gemm_group_pipelined(g, plan_gemm_group(g, 0));
+}
+
+hipError_t launch_gemm_pipe(const GemvArgs& a, hipStream_t stream, bool* handled) {
+  const GemmGroupArgs g = single(a);
+  const GemmPlan plan = plan_gemm_group(g, 0);
+  *handled = gemm_group_pipelined(g, plan);
+  if (!*handled) return hipSuccess;
+  return launch_gemm_group_plan(g, plan, nullptr, 0, stream);
 }
 
 }  // namespace tensor_gguf

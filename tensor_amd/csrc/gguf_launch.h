@@ -94,12 +94,17 @@ struct GemmPlan {
 GemmPlan plan_gemm_group(const GemmGroupArgs& args, size_t workspace_bytes);
 // Bytes of fp32 partial sums a plan needs (0 when it does not split K).
 size_t gemm_group_workspace(const GemmGroupArgs& args, const GemmPlan& plan);
-// Q4_K / Q5_K / Q6_K only; hipErrorInvalidValue for other encodings, invalid plans or a short
-// workspace.  A split plan also launches the in-order reduction of the partial sums.
+// Whether the pipelined kernel runs this group under this plan: Q4_K, Q5_K, Q6_K, Q8_0 and
+// Q4_0, with K whole 64-element steps that the plan's wave groups and splits share evenly.
+bool gemm_group_pipelined(const GemmGroupArgs& args, const GemmPlan& plan);
+// The pipelined kernel; hipErrorInvalidValue where gemm_group_pipelined is false or the
+// workspace is short.  A split plan also launches the in-order reduction of the partial sums.
 hipError_t launch_gemm_group_plan(const GemmGroupArgs& args, const GemmPlan& plan, void* workspace,
                                   size_t workspace_bytes, hipStream_t stream);
-// Pipelined dequant-GEMM for Q4_K, Q5_K and Q6_K (K a multiple of 256); sets
-// *handled to false for the encodings it does not cover.
+// Whether the pipelined kernel covers this single-matrix shape (as launch_gemm_pipe runs it).
+bool gemm_pipe_supported(const GemvArgs& args);
+// Pipelined dequant-GEMM of one matrix; sets *handled to false for the encodings and shapes it
+// does not cover.
 hipError_t launch_gemm_pipe(const GemvArgs& args, hipStream_t stream, bool* handled);
 // One tile configuration of the pipelined GEMM by index (tile sweeps and tests).
 hipError_t launch_gemm_pipe_config(const GemvArgs& args, hipStream_t stream, int config);

@@ -438,7 +438,9 @@ def test_gemm_workspace_query_follows_the_split_plan():
     assert query(12, 256, 4096, [4096]) == 0                                # o: small tiles fill the CUs
     assert query(12, 2048, 4096, [12288]) == 0                              # C4: 256 x 128 tiles fill them
     assert query(12, 256, 4096, [12288, 12288]) == 0                        # gate + up
-    assert query(8, 256, 12288, [4096]) == 0                                # generic encodings never split
+    assert query(8, 256, 12288, [4096]) == 8 * 256 * 4096 * 4             # Q8_0 down: pipelined too
+    assert query(8, 256, 12320, [4096]) == 0                                # K % 64 == 32: generic tiles
+    assert query(3, 256, 12288, [4096]) == 0                                # generic encodings never split
 
 
 def _query_workspace(type_, m, k, rows):

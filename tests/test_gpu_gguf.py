@@ -385,6 +385,8 @@ def test_gemm_parity_small(hip_device, encoding, m):
     ("q4_k", 512, 12288, 4096),   # C4
     ("q4_k", 2048, 12288, 4096),  # C4 at its larger M
     ("q6_k", 256, 4096, 12288),   # C5 down at M=256
+    ("q8_0", 512, 12288, 4096),   # C4's shape in the showcase's other encodings
+    ("q4_0", 512, 12288, 4096),
 ])
 def test_gemm_parity_baseline_shapes(hip_device, c_oracle, encoding, m, n, k):
     """Full-size prefill shapes, every output row against the C oracle (16 threads)."""
@@ -503,7 +505,7 @@ def test_c5_layer_chained_in_one_graph(hip_device, c_oracle, m):
             b.release()
 
 
-@pytest.mark.parametrize("encoding", ["q4_k", "q5_k", "q6_k"])
+@pytest.mark.parametrize("encoding", ["q4_k", "q5_k", "q6_k", "q8_0", "q4_0"])
 @pytest.mark.parametrize("m,n,k", [
     (384, 7168, 512),    # 128x128 tile, K split over 2 wave groups
     (520, 4096, 512),    # 128x128, K split 2, ragged M
@@ -525,7 +527,7 @@ def test_gemm_tile_configurations(hip_device, c_oracle, encoding, m, n, k):
     assert R.relative_l2(got, expected) <= 1e-5
 
 
-@pytest.mark.parametrize("encoding", ["q4_k", "q5_k", "q6_k"])
+@pytest.mark.parametrize("encoding", ["q4_k", "q5_k", "q6_k", "q8_0", "q4_0"])
 @pytest.mark.parametrize("k,n", [
     (512, 10240),   # 256x128 tile
     (1024, 2560),   # 128x128, K split 2
@@ -562,12 +564,30 @@ def test_gemm_one_hot_rows_give_dequantized_weights(hip_device, c_oracle, encodi
     ("q4_0", 9, 5, 96, "float16"),         # N < 16: every row index clamped, a half chunk
 ])
 def test_gemm_small_m_kernel(hip_device, c_oracle, encoding, m, n, k, x_dtype):
-    """M <= 64 (every encoding; the Q4_K / Q5_K / Q6_K tiles keep N > 4096): weights decoded
+    """M <= 64 (every encoding; the pipelined tiles keep N > 4096): weights decoded
     into MFMA operands, K over the waves of a workgroup, activations through a wave-private LDS
     tile.  Every output row against the prefill oracle (fp16 x and W, fp32 sums)."""
-    code = Q.ggml_type(encoding)
     note("gemm-small-m", encoding, m, n, k, x_dtype)
-    x, raw = showcase_inputs(encoding, m, n, k, 600 + m)
+    check_packed_rows(hip_device, c_oracle, encoding, m, n, k, x_dtype, 600 + m)
+
+
+@pytest.mark.parametrize("encoding,m,n,k,x_dtype", [
+    ("q4_0", 32, 8192, 2048, "float16"),   # N > 4096: the pipelined tiles
+    ("q8_0", 48, 6000, 1024, "float32"),   # pipelined, ragged M and N, fp32 x rounded as staged
+    ("q8_0", 16, 6000, 1024, "float32"),   # Q8_0 with fp32 x at M <= 16: the small-M kernel
+    ("q4_0", 20, 5000, 1056, "float16"),   # K % 64 == 32: the small-M kernel at any N
+])
+def test_gemm_small_m_at_wide_n(hip_device, c_oracle, encoding, m, n, k, x_dtype):
+    """M <= 64 with N > 4096, on either side of the boundary between the small-M kernel and the
+    pipelined tiles: every output row against the prefill oracle."""
+    note("gemm-small-m-wide", encoding, m, n, k, x_dtype)
+    check_packed_rows(hip_device, c_oracle, encoding, m, n, k, x_dtype, 650 + m)
+
+
+def check_packed_rows(hip_device, c_oracle, encoding, m, n, k, x_dtype, seed):
+    """The packed entry at (m, n, k), fp32 and fp16 out, every output row within tolerance."""
+    code = Q.ggml_type(encoding)
+    x, raw = showcase_inputs(encoding, m, n, k, seed)
     x = x.astype(x_dtype)
     expected = packed_reference(c_oracle, x, raw, code, m, n, k).reshape(m, n)
     for out_dtype in ("float32", "float16"):
@@ -652,13 +672,17 @@ def test_fp16_weights_are_the_cast_of_the_fp32_dequantization(hip_device, c_orac
     assert np.all(got == TIE_HALF), np.unique(got)
 
 
-@pytest.mark.parametrize("encoding", MORE)
-def test_generic_gemm_one_hot_rows_give_dequantized_weights(hip_device, c_oracle, encoding):
-    """The generic GEMM stages every weight of the other encodings as fp16(dequant): one-hot
-    rows read them back bit for bit."""
+@pytest.mark.parametrize("encoding,k", [(e, 512) for e in MORE] + [
+    ("q8_0", 544),    # 17 K steps: odd, so the pipelined kernel passes the shape on
+    ("q4_0", 1056),   # K % 64 == 32
+])
+def test_generic_gemm_one_hot_rows_give_dequantized_weights(hip_device, c_oracle, encoding, k):
+    """The generic GEMM stages every weight of the other encodings, and of Q8_0 / Q4_0 where K
+    is not an even number of 64-element steps, as fp16(dequant): one-hot rows read them back
+    bit for bit."""
     code = Q.ggml_type(encoding)
-    k, n = 512, 384
-    note("gemm-one-hot-generic", encoding)
+    n = 384
+    note("gemm-one-hot-generic", encoding, k)
     raw = cases.random_blocks(encoding, n, k, 98)
     deq = c_oracle.dequantize(raw, code, n, k).astype(np.float16).astype(np.float32)
     perm = np.random.default_rng(99).permutation(k)
@@ -806,7 +830,10 @@ def run_gemm_group(device, encoding, x, raws, out_dtype, workspace_bytes=None):
     ("q4_k", 256, 4096, (4096,), False),             # o: 64 x 64 tiles with the K range inside the workgroup
     ("q5_k", 300, 8192, (1000, 77), True),           # ragged M and N, Q5_K
     ("q6_k", 200, 8192, (300, 500, 64), True),       # three ragged matrices, K >= 8192
-    ("q8_0", 64, 1024, (300, 100), False),           # other encodings: one generic launch per matrix
+    ("q8_0", 64, 1024, (300, 100), False),           # small M: one small-M launch per matrix
+    ("q8_0", 256, 12288, (4096,), True),             # Q8_0 down at M=256: K split across workgroups
+    ("q4_0", 256, 4096, (4096, 1024, 1024), True),   # Q4_0 q + k + v in one split launch
+    ("q4_0", 200, 1056, (300, 500), False),          # K % 64 == 32: one generic launch per matrix
     ("q4_k", 32, 4096, (4096, 1024, 1024), False),   # q + k + v at M=32: the small-M kernel per matrix
     ("q6_k", 48, 2048, (3000, 100), False),          # small M, ragged rows, Q6_K
 ])

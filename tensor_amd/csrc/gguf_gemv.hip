@@ -354,6 +354,112 @@ __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
   store_rows<SWIGLU>(acc, out, n_rows, row0, rows, lane);
 }
 
+// M = 1, K a multiple of 2048 (STEPS = K / 2048 blocks per lane, all of them held in registers):
+// the form of the Q4_K M = 1 kernel.  Each thread loads its x chunks into registers first, then
+// the lane issues every weight load of its row, and only then is x written to LDS and the
+// workgroup met at an LDS-only barrier, so the weight latency runs under the x staging instead
+// of after it.  x sits in LDS with 16 bytes of padding per 64-byte block (a lane's four b128
+// reads of its block then spread over the banks).  The arithmetic and its order per lane are
+// gemv_q32's, so the two kernels give identical results.  Timing harness, weights rotated
+// through 10 copies: Q8_0 4096x4096 4.65 -> 4.12 us, 12288x4096 14.1 -> 13.0 us, 4096x12288
+// 14.9 -> 13.2 us; Q4_0 3.68 -> 3.24, 8.59 -> 7.40, 8.39 -> 8.03 us (WAVES 8 for one or two
+// blocks per lane, else 4).
+template <int TYPE, int WAVES, int STEPS, typename OutT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q32_m1(const _Float16* __restrict__ x,
+                                                          const uint8_t* __restrict__ w,
+                                                          OutT* __restrict__ out, int n_rows) {
+  constexpr int kBytes = TYPE == kQ8_0 ? 34 : 18;
+  constexpr float kBias = TYPE == kQ8_0 ? 1152.0f : 1032.0f;  // as in gemv_q32
+  constexpr int T = WAVES * 64, K = 2048 * STEPS, BLOCKS = K / 32, CHUNKS = K / 8;
+  constexpr int XC = (CHUNKS + T - 1) / T;  // 16-byte x chunks per thread
+  __shared__ __attribute__((aligned(16))) uint8_t xl[CHUNKS * 20];  // 64 + 16 bytes per block
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  // rows past the last reload it (every wave meets the barrier), then return before the sum
+  const uint8_t* const wr = w + (size_t)min(row, n_rows - 1) * (size_t)(BLOCKS * kBytes);
+  uint4 xr[XC];
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    if (CHUNKS % T == 0 || c < CHUNKS) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * c);
+  }
+  uint32_t head[STEPS];
+  uint4 q0[STEPS], q1[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const uint8_t* block = wr + (lane + 64 * s) * kBytes;
+    head[s] = load4(block);  // fp16 d in the low half
+    q0[s] = load16(block + 2);
+    if constexpr (TYPE == kQ8_0) q1[s] = load16(block + 18);
+  }
+  asm volatile("" ::: "memory");  // every load above is issued before the x stores below
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    if (CHUNKS % T == 0 || c < CHUNKS) *reinterpret_cast<uint4*>(xl + 16 * c + 16 * (c >> 2)) = xr[i];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  if (row >= n_rows) return;
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const uint4* xp = reinterpret_cast<const uint4*>(xl + 80 * (lane + 64 * s));
+    uint4 xs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xs[i] = xp[i];
+    const float sx = sum16(xs[0], xs[1]) + sum16(xs[2], xs[3]);
+    float a = 0.0f;
+    if constexpr (TYPE == kQ8_0) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t q = word(u < 4 ? q0[s] : q1[s], u & 3) ^ 0x80808080u;
+        a = dot2(magic01(q), word(xs[u >> 1], 2 * (u & 1)), a);
+        a = dot2(magic23(q), word(xs[u >> 1], 2 * (u & 1) + 1), a);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t q = word(q0[s], u);
+        const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+        a = dot2(magic01(lo), word(xs[u >> 1], 2 * (u & 1)), a);
+        a = dot2(magic23(lo), word(xs[u >> 1], 2 * (u & 1) + 1), a);
+        a = dot2(magic01(hi), word(xs[2 + (u >> 1)], 2 * (u & 1)), a);
+        a = dot2(magic23(hi), word(xs[2 + (u >> 1)], 2 * (u & 1) + 1), a);
+      }
+    }
+    acc = fmaf(half_bits_to_float(head[s]), a - kBias * sx, acc);
+  }
+  const float v = wave_sum(acc);
+  if (lane == 0) store_out<OutT>(out, (size_t)row, v);
+}
+
+template <int TYPE, int STEPS, typename OutT>
+static void launch_q32_m1_steps(const GemvArgs& a, hipStream_t stream) {
+  constexpr int WAVES = STEPS <= 2 ? 8 : 4;
+  hipLaunchKernelGGL((gemv_q32_m1<TYPE, WAVES, STEPS, OutT>), dim3((a.n + WAVES - 1) / WAVES), dim3(WAVES * 64), 0,
+                     stream, static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w),
+                     static_cast<OutT*>(a.out), a.n);
+}
+
+// gemv_q32_m1 for K = 2048 .. 16384 in steps of 2048; false for the other shapes.
+template <int TYPE, typename OutT>
+static bool launch_q32_m1(const GemvArgs& a, hipStream_t stream) {
+  if (a.m != 1 || a.k % 2048) return false;
+  switch (a.k / 2048) {
+    case 1: launch_q32_m1_steps<TYPE, 1, OutT>(a, stream); return true;
+    case 2: launch_q32_m1_steps<TYPE, 2, OutT>(a, stream); return true;
+    case 3: launch_q32_m1_steps<TYPE, 3, OutT>(a, stream); return true;
+    case 4: launch_q32_m1_steps<TYPE, 4, OutT>(a, stream); return true;
+    case 5: launch_q32_m1_steps<TYPE, 5, OutT>(a, stream); return true;
+    case 6: launch_q32_m1_steps<TYPE, 6, OutT>(a, stream); return true;
+    case 7: launch_q32_m1_steps<TYPE, 7, OutT>(a, stream); return true;
+    case 8: launch_q32_m1_steps<TYPE, 8, OutT>(a, stream); return true;
+    default: return false;
+  }
+}
+
 // ------------------------------------------------------ other encodings ---
 // Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K: each lane decodes 16-element groups with the
 // dequantizer's arithmetic (decode8, twice) and accumulates their products with the
@@ -516,10 +622,12 @@ static hipError_t launch_m(const GemvArgs& a, hipStream_t stream) {
       hipLaunchKernelGGL((gemv_q6k<M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
       break;
     case kQ8_0:
+      if (launch_q32_m1<kQ8_0, OutT>(a, stream)) break;
       if (xlds) hipLaunchKernelGGL((gemv_q32<kQ8_0, M, 1, OutT, false, true>), grid1, block, xbytes, stream, x, w, out, a.n, a.k);
       else hipLaunchKernelGGL((gemv_q32<kQ8_0, M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
       break;
     case kQ4_0:
+      if (launch_q32_m1<kQ4_0, OutT>(a, stream)) break;
       if (xlds) hipLaunchKernelGGL((gemv_q32<kQ4_0, M, 1, OutT, false, true>), grid1, block, xbytes, stream, x, w, out, a.n, a.k);
       else hipLaunchKernelGGL((gemv_q32<kQ4_0, M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
       break;

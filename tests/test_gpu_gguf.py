@@ -110,6 +110,8 @@ def test_gemv_parity_small(hip_device, encoding, m, k):
     ("q6_k", 4096, 12288, 1, "float16"),   # C5 down (Q6_K)
     ("q6_k", 1001, 12288, 1, "float32"),   # three steps per row, ragged last workgroup
     ("q8_0", 4096, 4096, 1, "float16"),    # C1 shape
+    ("q8_0", 4096, 12288, 1, "float16"),   # six blocks per lane, 4-wave workgroups
+    ("q4_0", 12288, 4096, 1, "float32"),
     ("q5_k", 12288, 4096, 1, "float16"),   # Q5_K through the M = 1 kernel (4 rows per workgroup)
     ("q5_k", 4096, 12288, 1, "float32"),   # three 4096-column steps, 8 rows per workgroup
     ("q5_k", 1003, 16384, 1, "float16"),   # four steps, ragged last workgroup
@@ -127,6 +129,24 @@ def test_gemv_parity_baseline_shapes(hip_device, c_oracle, encoding, n, k, m, ou
     expected = c_oracle.linear(x, raw, code, n, k)
     got = run_linear(hip_device, "gguf_gemv", encoding, x, raw, out_dtype)
     assert R.relative_l2(got, expected) <= TOLERANCE
+
+
+@pytest.mark.parametrize("encoding", ["q8_0", "q4_0"])
+def test_gemv_q32_m1_every_row_length(hip_device, c_oracle, encoding):
+    """M = 1 Q8_0 / Q4_0 rows of 2048 .. 16384 columns: one to eight blocks per lane, all held
+    in registers, 8- and 4-wave workgroups, a ragged last workgroup (203 rows)."""
+    code = Q.ggml_type(encoding)
+    n = 203
+    for k in range(2048, 16384 + 1, 2048):
+        note("gemv-q32-m1", encoding, n, k)
+        raw = cases.weight(n, k, encoding, 45 + k // 2048)
+        x = cases.activation(1, k, 46)
+        expected = c_oracle.linear(x, raw, code, n, k)
+        for out_dtype in ("float32", "float16"):
+            got = run_linear(hip_device, "gguf_gemv", encoding, x, raw, out_dtype)
+            assert not np.isnan(got).any(), (k, out_dtype)
+            err = R.relative_l2(got, expected)
+            assert err <= (2e-4 if out_dtype == "float32" else TOLERANCE), (k, out_dtype, err)
 
 
 @pytest.mark.parametrize("n", [65536 + 1007, 70000])

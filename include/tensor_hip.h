@@ -127,8 +127,9 @@ int32_t tensor_gguf_gemv_group_v1(const TensorCallV1 *call, TensorErrorV1 *error
  * workspace and a second kernel adds them in split order (deterministic) and converts; the
  * split is chosen to fit the workspace given (any size; a short one only limits the split).
  * Q4_K, Q5_K, Q6_K, Q8_0 and Q4_0 use the pipelined kernel (Q8_0 / Q4_0 where K is an even
- * number of 64-element steps); the other encodings and shapes, and M <= 64 where every
- * N_i <= 4096, take one launch per matrix as tensor_gguf_gemm_v1 runs it.  Arguments, in order:
+ * number of 64-element steps), at M <= 64 with every N_i <= 4096 on 64 x 64 tiles with K split
+ * across workgroups where that fills at least 128 workgroups; the other encodings and shapes
+ * take one launch per matrix as tensor_gguf_gemm_v1 runs it.  Arguments, in order:
  *   0        x         buffer fp16  [M, K]
  *   2i+1     w_i       buffer uint8 [N_i, K/QK*BLOCK]
  *   2i+2     out_i     buffer [M, N_i], one dtype (fp16 or fp32) for all i

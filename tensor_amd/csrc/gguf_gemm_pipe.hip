@@ -561,6 +561,23 @@ int base_tile(const GemmGroupArgs& a) {
 GemmPlan plan_gemm_group(const GemmGroupArgs& a, size_t workspace_bytes) {
   GemmPlan plan{base_tile(a), 1};
   if (!pipe_type(a.type)) return plan;
+  // M <= 64 with every N <= 4096 (where one matrix alone takes the small-M kernel): 64 x 64
+  // tiles with K over four wave groups, split across workgroups while the grid stays within
+  // 256 workgroups and each split keeps >= 16 steps; taken when that grid reaches 128
+  // workgroups, else each matrix keeps its small-M launch.  Timing harness at M = 32: q + k + v
+  // (4096, 1024, 1024) x 4096 Q4_K 41.2 -> 16.5 us with 2 splits, down 4096 x 12288 Q4_K 40.7 ->
+  // 22.5 us with 4, Q6_K 44.3 -> 34.5, Q8_0 37.7 -> 30.9, o 4096 x 4096 15.0 -> 13.6.
+  bool narrow = a.m <= kSkinnyMaxM;
+  for (int i = 0; i < a.count; ++i) narrow = narrow && a.n[i] <= 4096;
+  if (narrow) {
+    const long tiles = tile_count(a, kTiles[7]);
+    int splits = 1;
+    while (tiles * splits * 2 <= 256 && valid_plan(a, 7, splits * 2) && a.k / pipe::BK / (splits * 2) >= 16 &&
+           (size_t)splits * 2 * a.m * total_columns(a) * sizeof(float) <= workspace_bytes)
+      splits *= 2;
+    if (valid_plan(a, 7, splits) && tiles * splits >= 128) return GemmPlan{7, splits, true};
+    return plan;
+  }
   // Split K across workgroups with the 256 x 128 tile when that tile alone leaves most CUs
   // idle and the small tiles are no better: when even 64 x 64 tiles need more than one round
   // of 256 workgroups, or K is long (>= 8192).  Measured at M = 256 (q + k + v grouped 68 ->

@@ -89,6 +89,7 @@ struct GemmJob {
 // A workgroup tile (index into the pipelined GEMM's tile table) and a cross-workgroup K split.
 struct GemmPlan {
   int tile, splits;
+  bool small_m = false;  // M <= 64: this plan replaces one small-M launch per matrix
 };
 // The plan for a shape given the workspace available (0: no cross-workgroup split).
 GemmPlan plan_gemm_group(const GemmGroupArgs& args, size_t workspace_bytes);

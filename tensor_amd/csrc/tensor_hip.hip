@@ -454,11 +454,11 @@ int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has
     one[i].out_half = group.out_half;
     small = small && tensor_gguf::gemm_small_m(one[i]);
   }
-  if (!small && tensor_gguf::gemm_group_pipelined(group, plan)) {
+  if ((!small || plan.small_m) && tensor_gguf::gemm_group_pipelined(group, plan)) {
     status = tensor_gguf::launch_gemm_group_plan(group, plan, workspace, workspace_bytes, stream);
   } else {
-    // the other encodings and shapes, and small M, one launch per matrix in order (no
-    // workspace: such plans never split K)
+    // the other encodings and shapes, and small M where the plan keeps the small-M kernel, one
+    // launch per matrix in order (no workspace: such plans never split K)
     for (int i = 0; i < count && status == hipSuccess; ++i) status = tensor_gguf::launch_gemm(one[i], stream);
   }
   if (status != hipSuccess) return hip_fail(error, status, "GGUF grouped GEMM launch");

@@ -441,6 +441,8 @@ def test_gemm_workspace_query_follows_the_split_plan():
     assert query(8, 256, 12288, [4096]) == 8 * 256 * 4096 * 4             # Q8_0 down: pipelined too
     assert query(8, 256, 12320, [4096]) == 0                                # K % 64 == 32: generic tiles
     assert query(3, 256, 12288, [4096]) == 0                                # generic encodings never split
+    assert query(12, 32, 4096, [4096, 1024, 1024]) == 2 * 32 * 6144 * 4    # q + k + v at M=32: 64 x 64, 2 splits
+    assert query(12, 32, 1024, [1024]) == 0                                 # showcase M=32: the small-M kernel
 
 
 def _query_workspace(type_, m, k, rows):

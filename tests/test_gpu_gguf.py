@@ -854,8 +854,11 @@ def run_gemm_group(device, encoding, x, raws, out_dtype, workspace_bytes=None):
     ("q8_0", 256, 12288, (4096,), True),             # Q8_0 down at M=256: K split across workgroups
     ("q4_0", 256, 4096, (4096, 1024, 1024), True),   # Q4_0 q + k + v in one split launch
     ("q4_0", 200, 1056, (300, 500), False),          # K % 64 == 32: one generic launch per matrix
-    ("q4_k", 32, 4096, (4096, 1024, 1024), False),   # q + k + v at M=32: the small-M kernel per matrix
-    ("q6_k", 48, 2048, (3000, 100), False),          # small M, ragged rows, Q6_K
+    ("q4_k", 32, 4096, (4096, 1024, 1024), True),    # q + k + v at M=32: 64 x 64 tiles, K split 2 ways
+    ("q6_k", 48, 12288, (4096,), True),              # down at M=48: 64 x 64 tiles, K split 4 ways
+    ("q4_0", 16, 4096, (4096, 1024, 1024), True),    # Q4_0 q + k + v at M=16
+    ("q6_k", 48, 2048, (3000, 100), False),          # small M, 98 workgroups at most: small-M kernel per matrix
+    ("q4_k", 32, 1024, (1024,), False),              # the showcase's shape: small-M kernel
 ])
 def test_gemm_group_parity(hip_device, c_oracle, encoding, m, k, rows, split):
     code = Q.ggml_type(encoding)

@@ -582,12 +582,15 @@ GemmPlan plan_gemm_group(const GemmGroupArgs& a, size_t workspace_bytes) {
   // idle and the small tiles are no better: when even 64 x 64 tiles need more than one round
   // of 256 workgroups, or K is long (>= 8192).  Measured at M = 256 (q + k + v grouped 68 ->
   // 34 us with 4 splits, the Q6_K down 4096 x 12288 90 -> 54 us with 8); the 4096 x 4096 o
-  // projection stays on 64 x 64 tiles (25 us against 30 split).  Splits double while the grid
-  // stays within 256 workgroups and each split keeps >= 8 steps (512 of K).
+  // projection stays on 64 x 64 tiles (25 us against 30 split).  From M = 65 (timing harness,
+  // M = 96 / 128 / 160): the down 4096 x 12288 Q6_K 96 / 95 / 93 -> 46 / 48 / 50 us with 8
+  // splits, Q8_0 85 / 89 / 85 -> 46 / 48 / 49, Q4_K 55 / 55 / 56 -> 40 / 41 / 43; q + k + v at
+  // M = 160 40 -> 31 with 4.  Splits double while the grid stays within 256 workgroups and each
+  // split keeps >= 8 steps (512 of K).
   const long tiles = tile_count(a, kTiles[0]);
   const bool big_tile = plan.tile == 0 || plan.tile == 1 || plan.tile == 4;  // already fills the CUs
   const bool crowded = tile_count(a, kTiles[3]) > 256 || a.k >= 8192;
-  if (a.m < 192 || big_tile || !crowded) return plan;
+  if (a.m <= kSkinnyMaxM || big_tile || !crowded) return plan;
   int splits = 1;
   while (tiles * splits * 2 <= 256 && valid_plan(a, 0, splits * 2) && a.k / pipe::BK / (splits * 2) >= 8 &&
          (size_t)splits * 2 * a.m * total_columns(a) * sizeof(float) <= workspace_bytes)

@@ -443,6 +443,8 @@ def test_gemm_workspace_query_follows_the_split_plan():
     assert query(3, 256, 12288, [4096]) == 0                                # generic encodings never split
     assert query(12, 32, 4096, [4096, 1024, 1024]) == 2 * 32 * 6144 * 4    # q + k + v at M=32: 64 x 64, 2 splits
     assert query(12, 32, 1024, [1024]) == 0                                 # showcase M=32: the small-M kernel
+    assert query(14, 128, 12288, [4096]) == 8 * 128 * 4096 * 4            # down at M=128: 256 x 128, 8 splits
+    assert query(12, 128, 4096, [4096, 1024, 1024]) == 0                    # q + k + v at M=128: 64 x 64 tiles fill them
 
 
 def _query_workspace(type_, m, k, rows):

@@ -859,6 +859,8 @@ def run_gemm_group(device, encoding, x, raws, out_dtype, workspace_bytes=None):
     ("q4_0", 16, 4096, (4096, 1024, 1024), True),    # Q4_0 q + k + v at M=16
     ("q6_k", 48, 2048, (3000, 100), False),          # small M, 98 workgroups at most: small-M kernel per matrix
     ("q4_k", 32, 1024, (1024,), False),              # the showcase's shape: small-M kernel
+    ("q8_0", 100, 12288, (4096,), True),             # down at M=100: 256 x 128 tiles, K split 8 ways
+    ("q4_k", 160, 4096, (4096, 1024, 1024), True),   # q + k + v at M=160: K split 4 ways
 ])
 def test_gemm_group_parity(hip_device, c_oracle, encoding, m, k, rows, split):
     code = Q.ggml_type(encoding)

@@ -584,29 +584,35 @@ def detail_cases(device):
               ("o", "q4_k", 4096, 4096), ("gate", "q4_k", 12288, 4096), ("up", "q4_k", 12288, 4096),
               ("down", "q6_k", 4096, 12288)]
     layer_weights = sum(weight_bytes(e, n, k) for _, e, n, k in shapes)
-    @add("C5_layer_m256")
-    def layer_prefill():
+    def layer_prefill(m):
         # the prefill step: q + k + v and gate + up as grouped GEMMs, o, then down, each on the
-        # plan the library picks (K split across workgroups for q + k + v and the Q6_K down)
-        m = 256
+        # plan the library picks (K split across workgroups for q + k + v and the Q6_K down at
+        # M=256; at M=32 and 128 the small- and mid-M plans); below M=256 the weights rotate
+        # through enough copies to stay out of the MALL, since the launches then stream them
         groups = [("qkv", "q4_k", 4096, [4096, 1024, 1024]), ("o", "q4_k", 4096, [4096]),
                   ("gate_up", "q4_k", 4096, [12288, 12288]), ("down", "q6_k", 12288, [4096])]
         need = max(device.gemm_workspace(e, m, k, rows) for _, e, k, rows in groups)
         workspace = device.empty((max(need, 256),), "uint8")
-        layers = [GroupGemm(device, e, m, k, rows, "float16", 2, 30 + 5 * i, workspace)
+        copies = 2 if m >= 256 else copies_for(layer_weights)
+        layers = [GroupGemm(device, e, m, k, rows, "float16", copies, 30 + 5 * i, workspace)
                   for i, (_, e, k, rows) in enumerate(groups)]
-        stats = time_launches(device, rotated_launches(layers, 4), per=4)
+        steps = max(4, copies)
+        stats = time_launches(device, rotated_launches(layers, steps), per=steps)
         result = dict(stats, **rate(stats, sum(layer.flops for layer in layers), "TFLOP/s"), launches=len(layers),
                       workspace_bytes=need)
         result["mfma_frac"] = round(result["TFLOP/s"] / FP16_PEAK_TFLOPS, 4)
         result["per_group_us"] = {}
         for (name, *_), layer in zip(groups, layers):
-            one = time_launches(device, [layer.calls[i % 2].launch for i in range(10)], per=10)
+            one = time_launches(device, [layer.calls[i % copies].launch for i in range(10)], per=10)
             result["per_group_us"][name] = one["median_us"]
         for layer in layers:
             layer.release()
         workspace.release()
         return result
+
+    add("C5_layer_m256")(lambda: layer_prefill(256))
+    add("C5_layer_m128_grouped")(lambda: layer_prefill(128))
+    add("C5_layer_m32_grouped")(lambda: layer_prefill(32))
 
     for m, kernel in ((1, "gguf_gemv"), (256, "gguf_gemm")):
         @add(f"C5_layer_m{m}" if m == 1 else "C5_layer_m256_seven_launches")

@@ -546,12 +546,23 @@ bool valid_plan(const GemmGroupArgs& a, int tile, int splits) {
 // M = 256: 1.4x to 4x faster than the unsplit tiles for the q/k/v/o, gate/up and down shapes).
 constexpr long kMinBlocks = 160;
 
+// A tile is taken only where M fills more than half its rows: 256-row tiles from M = 129,
+// 128-row tiles from M = 65 (timing harness, Q4_K gate + up 2 x 12288 x 4096: M = 32 69.8 ->
+// 39.8 us on 64 x 64 KS2, M = 128 72.3 -> 51.4 on 128 x 128 KS2; one 12288-row gate at M = 96 /
+// 128 on 128 x 64 KS2 33.1 / 33.9 us; the Q6_K LM head at M = 32 414 -> 320 us).  At M <= 64
+// the 64 x 64 tile splits K over 4 wave groups while its tiles stay within 256, else over 2.
 int base_tile(const GemmGroupArgs& a) {
   const int steps = a.k / pipe::BK;  // even (whole 32-element block pairs or super-blocks)
-  if (tile_count(a, kTiles[0]) >= kMinBlocks) return 0;
-  if (tile_count(a, kTiles[1]) >= kMinBlocks) return steps % 8 == 0 ? 4 : 1;
-  if (steps % 16 == 0) return 7;
-  if (steps % 8 == 0) return 6;
+  const bool ks2 = steps % 8 == 0, ks4 = steps % 16 == 0;
+  if (a.m > 128 && tile_count(a, kTiles[0]) >= kMinBlocks) return 0;
+  if (a.m > 64) {
+    const long wide = tile_count(a, kTiles[1]);
+    if (wide >= 512) return 1;
+    if (wide >= kMinBlocks) return ks2 ? 4 : 1;
+    if (a.m <= 128 && tile_count(a, kTiles[2]) >= kMinBlocks) return ks2 ? 5 : 2;
+  }
+  if (ks4 && (a.m > 64 || tile_count(a, kTiles[3]) < 256)) return 7;
+  if (ks2) return 6;
   if (tile_count(a, kTiles[2]) >= kMinBlocks) return 2;
   return 3;
 }
@@ -588,7 +599,7 @@ GemmPlan plan_gemm_group(const GemmGroupArgs& a, size_t workspace_bytes) {
   // M = 160 40 -> 31 with 4.  Splits double while the grid stays within 256 workgroups and each
   // split keeps >= 8 steps (512 of K).
   const long tiles = tile_count(a, kTiles[0]);
-  const bool big_tile = plan.tile == 0 || plan.tile == 1 || plan.tile == 4;  // already fills the CUs
+  const bool big_tile = plan.tile != 3 && plan.tile != 6 && plan.tile != 7;  // already fills the CUs
   const bool crowded = tile_count(a, kTiles[3]) > 256 || a.k >= 8192;
   if (a.m <= kSkinnyMaxM || big_tile || !crowded) return plan;
   int splits = 1;

@@ -547,6 +547,25 @@ def test_gemm_tile_configurations(hip_device, c_oracle, encoding, m, n, k):
     assert R.relative_l2(got, expected) <= 1e-5
 
 
+@pytest.mark.parametrize("encoding,m,n,k", [
+    ("q4_k", 96, 12288, 4096),    # 128 x 64 tiles, K over 2 wave groups (M <= 128)
+    ("q6_k", 40, 20480, 1024),    # 64 x 64 tiles, K over 2 (M <= 64 and >= 256 tiles)
+    ("q8_0", 100, 70000, 512),    # 128 x 128 unsplit (>= 512 tiles at M <= 128), ragged M and N
+    ("q4_0", 130, 20480, 2048),   # 256 x 128 again from M = 129 (160 tiles)
+])
+def test_gemm_tiles_at_small_m(hip_device, c_oracle, encoding, m, n, k):
+    """Tiles no more than twice as tall as M: shapes that select each of them below M = 129."""
+    code = Q.ggml_type(encoding)
+    note("gemm-small-m-tiles", encoding, m, n, k)
+    raw = cases.weight(n, k, encoding, 95)
+    x = cases.activation(m, k, 96)
+    c_oracle.set_threads(16)
+    expected = c_oracle.linear(x, raw, code, n, k, prefill=True)
+    got = run_linear(hip_device, "gguf_gemm", encoding, x, raw, "float32")
+    rows = np.linalg.norm(got - expected, axis=1) / np.linalg.norm(expected, axis=1)
+    assert rows.max() <= 1e-5, int(rows.argmax())
+
+
 @pytest.mark.parametrize("encoding", ["q4_k", "q5_k", "q6_k", "q8_0", "q4_0"])
 @pytest.mark.parametrize("k,n", [
     (512, 10240),   # 256x128 tile
@@ -860,6 +879,8 @@ def run_gemm_group(device, encoding, x, raws, out_dtype, workspace_bytes=None):
     ("q6_k", 48, 2048, (3000, 100), False),          # small M, 98 workgroups at most: small-M kernel per matrix
     ("q4_k", 32, 1024, (1024,), False),              # the showcase's shape: small-M kernel
     ("q8_0", 100, 12288, (4096,), True),             # down at M=100: 256 x 128 tiles, K split 8 ways
+    ("q4_k", 32, 4096, (12288, 12288), False),       # gate + up at M=32: 64 x 64 tiles, K over 2 wave groups
+    ("q4_k", 128, 4096, (12288, 12288), False),      # gate + up at M=128: 128 x 128 tiles, K over 2
     ("q4_k", 160, 4096, (4096, 1024, 1024), True),   # q + k + v at M=160: K split 4 ways
 ])
 def test_gemm_group_parity(hip_device, c_oracle, encoding, m, k, rows, split):

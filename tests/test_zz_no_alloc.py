@@ -19,6 +19,7 @@ SCRATCH_BYTES = 32 << 20  # TENSOR_GGUF_NOALLOC_SCRATCH_BYTES
 CALLS = (
     ("q4_k", 256, 4096, (4096, 1024, 1024)),  # C5 q + k + v: 4-way K split, 24 MiB of partial sums
     ("q6_k", 200, 8192, (300, 500, 64)),      # smaller and ragged, a different split
+    ("q4_0", 32, 4096, (4096, 1024, 1024)),   # M <= 64: 64 x 64 tiles, 2-way K split, 1.5 MiB
 )
 
 

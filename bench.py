@@ -23,12 +23,14 @@ launch over the first 100 launches, 93 us from the fourth hundred on).
 Also reported:
 
 * ``roofline`` for the dominant kernel (the grouped gate + up GEMV, 2 x
-  12288 x 4096): ``achieved`` from the live event-timed graph of 200 launches,
-  ``profiled`` the per-dispatch average and HBM ``traffic`` that the committed
-  rocprofv3 summary (profiles/gemv_q4k_m1_qwen3_mlp.md) records for it;
+  12288 x 4096): ``avg_us``, ``achieved``, ``frac`` and HBM ``traffic`` from
+  the committed rocprofv3 summary (profiles/gemv_q4k_m1_qwen3_mlp.md), and this
+  run's own HIP-event timings under ``live``: per dispatch (eager launches, as
+  the trace records them) and per launch of a captured graph;
 * ``cpu_baseline``: the C restatement in oracle/, invoked through its
-  TensorKernelV1 entry exactly as the reference CPU provider invokes images,
-  on the headline step and on every other configuration (``per_config``);
+  TensorKernelV1 entries exactly as the reference CPU provider invokes images,
+  on the headline step and on every other configuration (``per_config``:
+  decode numerics for the GEMV configs, prefill numerics for the GEMM ones);
 * ``details`` for the other BASELINE configurations (C1's shape, C2 M = 4/8,
   C3 LM head, C4 prefill GEMM, C5 decoder-layer chain at M = 1 and M = 256),
   the showcase's packed call at its own shapes, and the resident-dequantized
@@ -132,6 +134,26 @@ def time_launches(device, launches, per=1, replays=REPLAYS):
         return summarize(timed(graph.replay), per)
     finally:
         graph.close()
+
+
+def time_each(device, launches):
+    """Per-dispatch durations of eager launches, the way a kernel trace records them: each launch
+    bracketed by its own pair of HIP events on the launch stream and synchronized before the
+    next, so every kernel starts on an idle queue.  Returns per-launch statistics and the mean."""
+    warm(device, lambda: [launch() for launch in launches])
+    samples = []
+    for launch in launches:
+        start = device.record_event(timing=True)
+        launch()
+        stop = device.record_event(timing=True)
+        stop.synchronize()
+        samples.append(device.elapsed_ms(start, stop) * 1e-3)
+        start.release()
+        stop.release()
+    stats = summarize(samples, 1)
+    stats["mean_us"] = round(statistics.fmean(samples) * 1e6, 3)
+    del stats["samples_us"]
+    return stats
 
 
 def rate(stats, work, unit):
@@ -278,10 +300,40 @@ def cpu_threads():
     return (min(available, int(share)) if share and share.isdigit() and int(share) > 0 else available), available
 
 
+CPU_DTYPE_IDS = {np.dtype(np.float16): 10, np.dtype(np.float32): 11, np.dtype(np.uint8): 3}
+
+
+def cpu_call(x, raw, out, code):
+    """A TensorCallV1 for the oracle's CPU entries over host arrays [x, w, out, type], built as
+    the reference CPU provider builds one for a native image (src/tensor/providers/cpu.py:153-197).
+    Returns (call, keep): ``keep`` holds the shape / stride arrays the descriptor points at."""
+    import ctypes as c
+
+    from tensor_amd.runtime import abi
+
+    keep, args = [], (abi.Argument * 4)()
+    for j, arr in enumerate((x, raw, out)):
+        shape = (c.c_int64 * 2)(*arr.shape)
+        strides = (c.c_int64 * 2)(arr.strides[0], arr.strides[1])
+        keep += [shape, strides, arr]
+        dtype = CPU_DTYPE_IDS[arr.dtype]
+        args[j].kind, args[j].dtype = 1, dtype
+        args[j].buffer = abi.BufferDescriptor(arr.ctypes.data, arr.nbytes, shape, strides, 2, dtype, 1, 0)
+    args[3].kind, args[3].dtype, args[3].scalar = 2, 7, code
+    call = abi.CallDescriptor(1, 72, args, 4, 0, (c.c_uint32 * 3)(1, 1, 1), (c.c_uint32 * 3)(1, 1, 1), 0,
+                              abi.StreamDescriptor(1, 0, 0))
+    keep.append(args)
+    return call, keep
+
+
 def cpu_baseline(budget_s=20.0):
-    """Time the oracle's TensorKernelV1 CPU entry (tensor_gguf_gemv_cpu_v1) on the headline
-    step and on every other configuration, invoked as the reference CPU provider invokes a
-    native image (ctypes, synchronous call; src/tensor/providers/cpu.py:153-197)."""
+    """Time the oracle's TensorKernelV1 CPU entries, invoked as the reference CPU provider
+    invokes a native image (ctypes, synchronous call; src/tensor/providers/cpu.py:153-197):
+    tensor_gguf_gemv_cpu_v1 (decode numerics) on the headline step, C1, C2 at M = 4 / 8, C3 and
+    C5 at M = 1, and tensor_gguf_gemm_cpu_v1 (prefill numerics: fp16 operands, fp32
+    accumulation) on C4 at M = 512 / 2048 and C5 at M = 256.  Every config reports all-core and
+    single-thread figures; where a full call would take minutes the timed call covers a
+    stated slice of the weight rows (rows are independent, so the rate is the config's)."""
     import ctypes as c
 
     from oracle import gguf_ref
@@ -291,26 +343,11 @@ def cpu_baseline(budget_s=20.0):
     if not gguf_ref.LIBRARY.exists():
         gguf_ref.build()
     oracle = gguf_ref.c_oracle()
-    entry = oracle.entry
-    entry.argtypes = [c.POINTER(abi.CallDescriptor), c.POINTER(abi.ErrorDescriptor)]
-    entry.restype = c.c_int32
+    for entry in (oracle.entry, oracle.gemm_entry):
+        entry.argtypes = [c.POINTER(abi.CallDescriptor), c.POINTER(abi.ErrorDescriptor)]
+        entry.restype = c.c_int32
     threads, available = cpu_threads()
     codes = {"q8_0": 8, "q4_k": 12, "q6_k": 14}
-    dtype_ids = {np.dtype(np.float16): 10, np.dtype(np.float32): 11, np.dtype(np.uint8): 3}
-
-    def call_for(x, raw, out, code):
-        keep, args = [], (abi.Argument * 4)()
-        for j, arr in enumerate((x, raw, out)):
-            shape = (c.c_int64 * 2)(*arr.shape)
-            strides = (c.c_int64 * 2)(arr.strides[0], arr.strides[1])
-            keep += [shape, strides, arr]
-            dtype = dtype_ids[arr.dtype]
-            args[j].kind, args[j].dtype = 1, dtype
-            args[j].buffer = abi.BufferDescriptor(arr.ctypes.data, arr.nbytes, shape, strides, 2, dtype, 1, 0)
-        args[3].kind, args[3].dtype, args[3].scalar = 2, 7, code
-        call = abi.CallDescriptor(1, 72, args, 4, 0, (c.c_uint32 * 3)(1, 1, 1), (c.c_uint32 * 3)(1, 1, 1), 0,
-                                  abi.StreamDescriptor(1, 0, 0))
-        return call, keep, args
 
     def layers_for(shapes, m, out_dtype, seed, rotate=True):
         """Bound CPU calls for each (encoding, n, k), weights rotated past the host LLC."""
@@ -321,14 +358,14 @@ def cpu_baseline(budget_s=20.0):
             first = cases.weight(n, k, encoding, seed + i)
             x = cases.activation(m, k, seed + 100 + i)
             o = np.empty((m, n), out_dtype)
-            out.append([call_for(x, first if r == 0 else first.copy(), o, codes[encoding]) for r in range(copies)])
+            out.append([cpu_call(x, first if r == 0 else first.copy(), o, codes[encoding]) for r in range(copies)])
         return out, copies
 
-    def measure(calls, threads_, seconds):
+    def measure(entry, calls, threads_, seconds, at_least=3):
         oracle.set_threads(threads_)
         error = abi.ErrorDescriptor()
         samples, step, begin = [], 0, time.perf_counter()
-        while time.perf_counter() - begin < seconds or len(samples) < 3:
+        while time.perf_counter() - begin < seconds or len(samples) < at_least:
             t0 = time.perf_counter()
             for layer in calls:
                 if entry(c.byref(layer[step % len(layer)][0]), c.byref(error)):
@@ -337,35 +374,51 @@ def cpu_baseline(budget_s=20.0):
             step += 1
         return statistics.median(samples), len(samples)
 
-    def config(name, shapes, m, out_dtype, seconds, seed, single=True):
-        calls, copies = layers_for(shapes, m, out_dtype, seed)
-        nbytes = sum(gemv_bytes(e, m, n, k, np.dtype(out_dtype).itemsize) for e, n, k in shapes)
-        multi, count = measure(calls, threads, seconds)
-        result = {"GB/s": round(nbytes / multi / 1e9, 3), "ms": round(multi * 1e3, 3), "calls": count,
-                  "threads": threads, "weight_copies": copies, "bytes": nbytes}
-        if single:
-            one, count1 = measure(calls, 1, seconds / 2)
-            result.update({"single_thread_GB/s": round(nbytes / one / 1e9, 3),
-                           "single_thread_ms": round(one * 1e3, 3), "single_thread_calls": count1})
+    def config(name, shapes, m, out_dtype, seconds, seed, gemm=False, slices=(1, 1)):
+        """``slices`` = (all-core, single-thread) divisors of each matrix's rows for the timed calls."""
+        entry = oracle.gemm_entry if gemm else oracle.entry
+        itemsize = np.dtype(out_dtype).itemsize
+        result = {"numerics": "prefill: fp16 x . fp16(dequant W), fp32 accumulate" if gemm else
+                  "decode: fp32 x . fp32 dequant W, fp32 accumulate"}
+        for label, threads_, divisor, budget in (("", threads, slices[0], seconds), ("single_thread_", 1, slices[1],
+                                                                                     seconds / 2)):
+            sample = [(e, n // divisor, k) for e, n, k in shapes]
+            calls, copies = layers_for(sample, m, out_dtype, seed, rotate=not gemm)
+            nbytes = sum(gemv_bytes(e, m, n, k, itemsize) for e, n, k in sample)
+            flops = sum(2 * m * n * k for _, n, k in sample)
+            seconds_per_call, count = measure(entry, calls, threads_, budget, at_least=1 if label else 3)
+            full = seconds_per_call * divisor
+            result.update({f"{label}ms": round(full * 1e3, 3), f"{label}calls": count,
+                           f"{label}GB/s": round(nbytes / seconds_per_call / 1e9, 3),
+                           f"{label}GFLOP/s": round(flops / seconds_per_call / 1e9, 3)})
+            if divisor > 1:
+                result[f"{label}sample"] = f"1/{divisor} of each matrix's rows per call; ms scaled to the full call"
+            if not label:
+                result.update(threads=threads, weight_copies=copies)
         log("cpu", name, result)
         return result
 
     share = budget_s / 10.0
+    layer_shapes = [("q4_k", 4096, 4096), ("q4_k", 1024, 4096), ("q4_k", 1024, 4096), ("q4_k", 4096, 4096),
+                    ("q4_k", 12288, 4096), ("q4_k", 12288, 4096), ("q6_k", 4096, 12288)]
     per_config = {
         "C1_q8_0_gemv_m1_4096x4096": config("C1", [("q8_0", 4096, 4096)], 1, np.float16, share, 3000),
         "C2_q4k_gemv_m4_12288x4096": config("C2 M=4", [("q4_k", 12288, 4096)], 4, np.float16, share, 3100),
         "C2_q4k_gemv_m8_12288x4096": config("C2 M=8", [("q4_k", 12288, 4096)], 8, np.float16, share, 3200),
-        "C3_q6k_lm_head_m1_151936x4096_fp32": config("C3", [("q6_k", 151936, 4096)], 1, np.float32, share, 3300,
-                                                     single=False),
-        "C5_layer_m1": config("C5 M=1", [("q4_k", 4096, 4096), ("q4_k", 1024, 4096), ("q4_k", 1024, 4096),
-                                         ("q4_k", 4096, 4096), ("q4_k", 12288, 4096), ("q4_k", 12288, 4096),
-                                         ("q6_k", 4096, 12288)], 1, np.float16, share, 3400),
+        "C3_q6k_lm_head_m1_151936x4096_fp32": config("C3", [("q6_k", 151936, 4096)], 1, np.float32, share, 3300),
+        "C4_q4k_gemm_m512_12288x4096": config("C4 M=512", [("q4_k", 12288, 4096)], 512, np.float16, share, 3500,
+                                              gemm=True, slices=(1, 16)),
+        "C4_q4k_gemm_m2048_12288x4096": config("C4 M=2048", [("q4_k", 12288, 4096)], 2048, np.float16, share,
+                                               3600, gemm=True, slices=(4, 64)),
+        "C5_layer_m1": config("C5 M=1", layer_shapes, 1, np.float16, share, 3400),
+        "C5_layer_m256": config("C5 M=256", layer_shapes, 256, np.float16, share, 3700, gemm=True,
+                                slices=(2, 32)),
     }
     headline_shapes = [("q4_k", 12288, 4096), ("q4_k", 12288, 4096), ("q4_k", 4096, 12288)]
     calls, copies = layers_for(headline_shapes, 1, np.float16, 1000)
     step_bytes = sum(gemv_bytes(e, 1, n, k, 2) for e, n, k in headline_shapes)
-    multi, n_multi = measure(calls, threads, budget_s * 0.3)
-    single, n_single = measure(calls, 1, budget_s * 0.2)
+    multi, n_multi = measure(oracle.entry, calls, threads, budget_s * 0.3)
+    single, n_single = measure(oracle.entry, calls, 1, budget_s * 0.2)
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -759,34 +812,45 @@ def main():
         log(f"headline {value:.1f} GB/s, {headline['median_us']:.2f} us/step "
             f"(min {headline['min_us']}, max {headline['max_us']})")
 
-        # ---- roofline of the dominant kernel: the grouped gate + up GEMV, 2 x 12288 x 4096, M=1
+        # ---- roofline of the dominant kernel: the grouped gate + up GEMV, 2 x 12288 x 4096, M=1.
+        # achieved / frac / avg_us are the committed rocprofv3 per-dispatch average of this kernel
+        # (profiles/gemv_q4k_m1_qwen3_mlp.md); this run's own event timings sit beside them under
+        # "live": per dispatch (each eager launch bracketed by HIP events, as the trace records a
+        # dispatch) and per launch of a graph of 200 launches (consecutive launches overlap ramp-up
+        # and drain).
         launches = 200
-        kernel = time_launches(device, [gate_up.calls[i % copies].launch for i in range(launches)], per=launches)
-        achieved = gate_up.bytes / kernel["median_us"] / 1e3
+        graph = time_launches(device, [gate_up.calls[i % copies].launch for i in range(launches)], per=launches)
+        eager = time_each(device, [gate_up.calls[i % copies].launch for i in range(launches)])
         figures = profile_figures()
-        profiled = None
-        if "avg_us_per_launch" in figures:
-            avg = figures["avg_us_per_launch"]
-            profiled = {"avg_us": avg, "achieved": round(gate_up.bytes / avg / 1e3, 1),
-                        "frac": round(gate_up.bytes / avg / 1e3 / HBM_PEAK_GBS, 4),
-                        "source": "profiles/gemv_q4k_m1_qwen3_mlp.md (rocprofv3 --kernel-trace --stats, "
-                                  "per-dispatch average of eager launches)"}
+        live = {
+            "per_dispatch": dict(eager, achieved=round(gate_up.bytes / eager["mean_us"] / 1e3, 1),
+                                 frac=round(gate_up.bytes / eager["mean_us"] / 1e3 / HBM_PEAK_GBS, 4),
+                                 timing=f"{launches} eager launches, each bracketed by HIP events on the launch "
+                                        "stream; mean and median of the per-dispatch durations"),
+            "graph": {"avg_us": graph["median_us"], "avg_us_min": graph["min_us"], "avg_us_max": graph["max_us"],
+                      "achieved": round(gate_up.bytes / graph["median_us"] / 1e3, 1),
+                      "frac": round(gate_up.bytes / graph["median_us"] / 1e3 / HBM_PEAK_GBS, 4),
+                      "timing": f"HIP events around a graph of {launches} launches, median of {REPLAYS} replays"},
+        }
+        avg = figures.get("avg_us_per_launch", eager["mean_us"])
         roofline = {
             "bound": "hbm",
-            "achieved": round(achieved, 1),
+            "achieved": round(gate_up.bytes / avg / 1e3, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "frac": round(gate_up.bytes / avg / 1e3 / HBM_PEAK_GBS, 4),
             "traffic": int(figures["traffic_bytes_per_launch"]) if "traffic_bytes_per_launch" in figures else None,
             "kernel": "gemv_q4k_m1<STEPS=1, WAVES=8, MATS=2> gate+up 2 x 12288x4096, M=1, fp16 out",
-            "timing": f"live: HIP events around a graph of {launches} launches, median of {REPLAYS} replays",
-            "avg_us": kernel["median_us"],
-            "avg_us_min": kernel["min_us"],
-            "avg_us_max": kernel["max_us"],
+            "avg_us": avg,
+            "timing": ("rocprofv3 --kernel-trace --stats per-dispatch average, profiles/gemv_q4k_m1_qwen3_mlp.md"
+                       if "avg_us_per_launch" in figures else "live per-dispatch mean (no committed profile)"),
             "algorithmic_bytes": gate_up.bytes,
-            "profiled": profiled,
+            "live": live,
+            "live_per_dispatch_vs_profiled": round(eager["mean_us"] / avg, 4),
         }
-        log(f"roofline kernel {kernel['median_us']:.2f} us -> {achieved:.1f} GB/s; profiled {profiled}")
+        achieved = roofline["achieved"]
+        log(f"roofline kernel: profiled {avg:.3f} us -> {achieved:.1f} GB/s; live per dispatch "
+            f"{eager['mean_us']:.3f} us (median {eager['median_us']:.3f}), graph {graph['median_us']:.3f} us")
         for layer in mlp:
             layer.release()
 

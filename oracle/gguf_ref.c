@@ -432,14 +432,16 @@ static int check_buffer(const TensorArgumentV1 *arg, uint32_t rank,
 }
 
 /*
- * CPU baseline of the decode path, invoked exactly as the reference CPU
- * provider invokes a native image.  Arguments, in order:
+ * CPU baselines of the decode path (mode 0: fp32 operands, benchmark.py:466-472)
+ * and of the prefill path (mode 1: fp16-rounded operands, benchmark.py:473-477),
+ * invoked exactly as the reference CPU provider invokes a native image.
+ * Arguments, in order:
  *   x    fp16 [M, K]
  *   w    uint8 [N, K/QK*BLOCK]  (raw GGUF rows)
  *   out  fp16 or fp32 [M, N]
- *   type uint32 scalar GGML type id (2, 8, 12, 14)
+ *   type uint32 scalar GGML type id (2, 8, 12, 14, ...)
  */
-int32_t tensor_gguf_gemv_cpu_v1(const TensorCallV1 *call, TensorErrorV1 *error) {
+static int32_t linear_cpu(const TensorCallV1 *call, TensorErrorV1 *error, int mode) {
   if (error) {
     error->code = 0;
     error->message[0] = 0;
@@ -474,9 +476,17 @@ int32_t tensor_gguf_gemv_cpu_v1(const TensorCallV1 *call, TensorErrorV1 *error) 
     return fail(error, TENSOR_ERROR_ARGUMENT, "w: shape, stride or size mismatch");
   if (a[2].buffer.shape[0] != m || a[2].buffer.shape[1] != n)
     return fail(error, TENSOR_ERROR_ARGUMENT, "out: shape, stride or size mismatch");
-  if (oracle_linear(type, 0, (const void *)a[0].buffer.address, 1,
+  if (oracle_linear(type, mode, (const void *)a[0].buffer.address, 1,
                     (const uint8_t *)a[1].buffer.address,
                     (void *)a[2].buffer.address, out_half, m, n, k))
     return fail(error, TENSOR_ERROR_PROVIDER, "CPU kernel failed");
   return TENSOR_OK;
+}
+
+int32_t tensor_gguf_gemv_cpu_v1(const TensorCallV1 *call, TensorErrorV1 *error) {
+  return linear_cpu(call, error, 0);
+}
+
+int32_t tensor_gguf_gemm_cpu_v1(const TensorCallV1 *call, TensorErrorV1 *error) {
+  return linear_cpu(call, error, 1);
 }

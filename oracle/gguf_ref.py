@@ -214,7 +214,8 @@ class COracle:
         lib.oracle_set_threads.argtypes = [ctypes.c_int]
         lib.oracle_max_threads.restype = ctypes.c_int
         self.lib = lib
-        self.entry = lib.tensor_gguf_gemv_cpu_v1
+        self.entry = lib.tensor_gguf_gemv_cpu_v1       # decode numerics (fp32 operands)
+        self.gemm_entry = lib.tensor_gguf_gemm_cpu_v1  # prefill numerics (fp16 operands)
 
     def set_threads(self, threads: int) -> None:
         self.lib.oracle_set_threads(int(threads))

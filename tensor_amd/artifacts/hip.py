@@ -199,9 +199,9 @@ def validate_manifest(manifest: object) -> dict:
 
 # ---------------------------------------------------------- code objects --
 
-def code_object_kernels(image: bytes) -> tuple[str, dict]:
-    """(target, {kernel name: [explicit arguments]}) from a gfx950 ELF code object's
-    AMDGPU metadata note; each argument is (value_kind, size)."""
+def code_object_metadata(image: bytes) -> dict:
+    """The AMDGPU metadata note of a 64-bit ELF code object, decoded (its ``amdhsa.target``
+    and one record per kernel in ``amdhsa.kernels``: arguments, LDS, scratch, registers)."""
     import msgpack
 
     if image[:4] != b"\x7fELF" or len(image) < 64 or image[4] != 2 or image[5] != 1:
@@ -223,15 +223,58 @@ def code_object_kernels(image: bytes) -> tuple[str, dict]:
                 position += (descsz + 3) & ~3
                 if name.rstrip(b"\0") == b"AMDGPU" and note_type == 32:  # NT_AMDGPU_METADATA
                     metadata = msgpack.unpackb(desc, raw=False)
-                    target = metadata.get("amdhsa.target", "")
-                    kernels = {}
-                    for kernel in metadata.get("amdhsa.kernels", []):
-                        kernels[kernel[".name"]] = [(a.get(".value_kind"), a.get(".size")) for a in kernel.get(".args", [])
-                                                    if not str(a.get(".value_kind", "")).startswith("hidden_")]
-                    return target, kernels
+                    if not isinstance(metadata, dict):
+                        raise ValueError("metadata is not a map")
+                    return metadata
     except (struct.error, KeyError, TypeError, ValueError) as exc:
         raise ArtifactError(f"unreadable code object metadata: {exc}") from exc
     raise ArtifactError(f"{IMAGE} carries no AMDGPU kernel metadata")
+
+
+def code_object_kernels(image: bytes) -> tuple[str, dict]:
+    """(target, {kernel name: [explicit arguments]}) from a gfx950 ELF code object's
+    AMDGPU metadata note; each argument is (value_kind, size)."""
+    metadata = code_object_metadata(image)
+    try:
+        kernels = {}
+        for kernel in metadata.get("amdhsa.kernels", []):
+            kernels[kernel[".name"]] = [(a.get(".value_kind"), a.get(".size")) for a in kernel.get(".args", [])
+                                        if not str(a.get(".value_kind", "")).startswith("hidden_")]
+    except (KeyError, TypeError, AttributeError) as exc:
+        raise ArtifactError(f"unreadable code object metadata: {exc}") from exc
+    return metadata.get("amdhsa.target", ""), kernels
+
+
+def offload_code_objects(image: bytes, target: str = "gfx950") -> list:
+    """The device code objects for ``target`` inside a host shared library built by hipcc:
+    its ``.hip_fatbin`` section holds one clang offload bundle per translation unit (a
+    24-byte magic, an entry count, then offset, size and triple of each entry)."""
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    if image[:4] != b"\x7fELF" or len(image) < 64:
+        raise ArtifactError("not an ELF shared library")
+    shoff, = struct.unpack_from("<Q", image, 0x28)
+    shentsize, shnum, shstrndx = struct.unpack_from("<HHH", image, 0x3A)
+    sections = [struct.unpack_from("<IIQQQQ", image, shoff + i * shentsize) for i in range(shnum)]
+    names = sections[shstrndx][4]
+    fatbin = None
+    for name_offset, _, _, _, offset, size in sections:
+        name = image[names + name_offset:image.index(b"\0", names + name_offset)]
+        if name == b".hip_fatbin":
+            fatbin = image[offset:offset + size]
+    if fatbin is None:
+        raise ArtifactError("no .hip_fatbin section")
+    objects, position = [], 0
+    while (start := fatbin.find(magic, position)) >= 0:
+        count, = struct.unpack_from("<Q", fatbin, start + len(magic))
+        entry = start + len(magic) + 8
+        for _ in range(count):
+            offset, size, triple_size = struct.unpack_from("<QQQ", fatbin, entry)
+            triple = fatbin[entry + 24:entry + 24 + triple_size].decode()
+            entry += 24 + triple_size
+            if triple.endswith("--" + target) and size:
+                objects.append(fatbin[start + offset:start + offset + size])
+        position = start + len(magic)
+    return objects
 
 
 def check_kernel(manifest: dict, image: bytes) -> None:

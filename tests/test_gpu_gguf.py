@@ -105,6 +105,8 @@ def test_gemv_parity_small(hip_device, encoding, m, k):
     ("q4_k", 12288, 4096, 1, "float16"),   # C2 gate/up
     ("q4_k", 4096, 12288, 1, "float16"),   # C2 down
     ("q4_k", 12288, 4096, 4, "float16"),
+    ("q4_k", 4096, 12288, 4, "float16"),   # C2 down at M = 4: one 16-row tile x 12 K ranges per workgroup
+    ("q4_k", 12288, 4096, 8, "float16"),   # C2 gate at M = 8
     ("q4_k", 4096, 12288, 8, "float16"),
     ("q6_k", 151936, 4096, 1, "float32"),  # C3 LM head, fp32 logits
     ("q6_k", 4096, 12288, 1, "float16"),   # C5 down (Q6_K)
@@ -173,6 +175,7 @@ def test_gemv_q6k_tall_rows_each_within_tolerance(hip_device, c_oracle, n):
     (6, 12296, 4096),   # sector-aligned, three tiles per workgroup, last workgroup one tile
     (3, 8200, 8192),    # sector-aligned, two tiles x eight K ranges (1024 threads)
     (4, 4101, 12288),   # sector-aligned for a long row, twelve K ranges, ragged rows
+    (4, 4096, 12288),   # C2 down at M = 4: 256 workgroups, so x is staged before the weights
     (2, 100, 16384),    # sector-aligned, sixteen K ranges of one 16-row tile
     (5, 4100, 12288),   # x too large for the sector kernel: three super-blocks per wave, x in LDS
     (8, 4100, 4096),    # narrow matrix: the LDS multi-tile kernel

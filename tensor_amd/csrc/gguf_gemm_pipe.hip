@@ -93,15 +93,16 @@ struct Geometry<kQ4_0, TPR> {
 };
 
 // Raw bytes of one step in vector registers (vector values stay in VGPRs; arrays of
-// several sets were demoted to the stack). x: XL 16-byte activation chunks.
-template <int XL, int W0, int W1>
+// several sets were demoted to the stack). x: XL 16-byte activation chunks; a / b: the
+// quant and header dwords of each of the thread's P weight parts.
+template <int XL, int W0, int W1, int P>
 struct Raw {
   typedef uint32_t XV __attribute__((ext_vector_type(4 * XL)));
   typedef uint32_t AV __attribute__((ext_vector_type(W0)));
   typedef uint32_t BV __attribute__((ext_vector_type(W1)));
   XV x;
-  AV a;
-  BV b;
+  AV a[P];
+  BV b[P];
 };
 
 }  // namespace pipe
@@ -124,10 +125,16 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
   constexpr int THREADS = WM * WN * 64;  // per K group
   constexpr int MT = BM / WM / 16, NT = BN / WN / 16;
   constexpr int XL = BM * 8 / THREADS;  // 16-byte activation chunks per thread per step
-  constexpr int TPR = THREADS / BN;     // threads per weight row
-  static_assert(XL * THREADS == BM * 8 && TPR * BN == THREADS && (TPR == 1 || TPR == 2 || TPR == 4), "tile shape");
+  // TPR parts per weight row (a part: the row's step bytes one thread decodes).  Where BN
+  // divides the threads, every thread takes one part of one row; otherwise (BN = 96, 192)
+  // rows take 4 parts and thread t the parts t, t + THREADS, ... below BN * 4, so a wave
+  // either has a part at a given index or has none (the test is wave-uniform).
+  constexpr int TPR = THREADS % BN == 0 ? THREADS / BN : 4;
+  constexpr int PARTS = (BN * TPR + THREADS - 1) / THREADS;
+  static_assert(XL * THREADS == BM * 8 && (TPR == 1 || TPR == 2 || TPR == 4) && PARTS <= 2 &&
+                    (BN * TPR) % 64 == 0, "tile shape");
   using G = Geometry<TYPE, TPR>;
-  using RawT = Raw<XL, G::W0, G::W1>;
+  using RawT = Raw<XL, G::W0, G::W1, PARTS>;
   constexpr int QK = Block<TYPE>::QK, BYTES = Block<TYPE>::BYTES;
   constexpr bool KQ = TYPE == kQ4_K || TYPE == kQ5_K;  // Q4_K's header and nibble layout
   constexpr bool B32 = TYPE == kQ8_0 || TYPE == kQ4_0;  // 32-element blocks, two per step
@@ -148,8 +155,17 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
   const int mi = tile < job.tile_end[0] ? 0 : tile < job.tile_end[1] ? 1 : 2;
   const int N = job.n[mi];
   const int m0 = blockIdx.y * BM, n0 = (tile - (mi ? job.tile_end[mi - 1] : 0)) * BN;
-  const int wrow = tid / TPR, wpart = tid % TPR;
-  const uint8_t* wbase = job.w[mi] + (size_t)min(n0 + wrow, N - 1) * (size_t)(K / QK) * BYTES;
+  int wrow[PARTS], wpart[PARTS];
+  bool has[PARTS];
+  const uint8_t* wbase[PARTS];
+#pragma unroll
+  for (int p = 0; p < PARTS; ++p) {
+    const int part = tid + p * THREADS;
+    has[p] = part < BN * TPR;
+    wrow[p] = has[p] ? part / TPR : 0;
+    wpart[p] = part % TPR;
+    wbase[p] = job.w[mi] + (size_t)min(n0 + wrow[p], N - 1) * (size_t)(K / QK) * BYTES;
+  }
   // this group's steps of this split; the host guarantees that every group takes an even number
   // of steps and (for the 256-element encodings) starts on a super-block
   const int split_steps = K / BK / job.splits;
@@ -174,45 +190,51 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
         r.x[4 * i] = v.x; r.x[4 * i + 1] = v.y; r.x[4 * i + 2] = v.z; r.x[4 * i + 3] = v.w;
       }
     }
-    const uint8_t* blk = wbase + (size_t)(k0 / QK) * BYTES;
-    if constexpr (B32) {
-      constexpr int QPB = G::QPB, QB = G::QB;
-      const uint8_t* b = blk + (QB * wpart / QPB) * BYTES;  // this thread's block: fp16 d, quants
-      const uint8_t* q = b + 2 + QB * wpart % QPB;
-      if constexpr (G::W0 % 4 == 0) {
 #pragma unroll
-        for (int i = 0; i < G::W0; i += 4) {
-          const uint4 v = load16(q + 4 * i);
-          r.a[i] = v.x; r.a[i + 1] = v.y; r.a[i + 2] = v.z; r.a[i + 3] = v.w;
+    for (int p = 0; p < PARTS; ++p) {
+      if (!has[p]) continue;
+      const uint8_t* blk = wbase[p] + (size_t)(k0 / QK) * BYTES;
+      typename RawT::AV& ra = r.a[p];
+      typename RawT::BV& rb = r.b[p];
+      if constexpr (B32) {
+        constexpr int QPB = G::QPB, QB = G::QB;
+        const uint8_t* b = blk + (QB * wpart[p] / QPB) * BYTES;  // this part's block: fp16 d, quants
+        const uint8_t* q = b + 2 + QB * wpart[p] % QPB;
+        if constexpr (G::W0 % 4 == 0) {
+#pragma unroll
+          for (int i = 0; i < G::W0; i += 4) {
+            const uint4 v = load16(q + 4 * i);
+            ra[i] = v.x; ra[i + 1] = v.y; ra[i + 2] = v.z; ra[i + 3] = v.w;
+          }
+        } else {
+          const uint2 v = load8(q);
+          ra[0] = v.x; ra[1] = v.y;
+        }
+        rb[0] = load4(b);
+        rb[1] = 0;
+      } else if constexpr (KQ) {
+        const uint4 hd = load16(blk);
+        rb[0] = hd.x; rb[1] = hd.y; rb[2] = hd.z; rb[3] = hd.w;
+        const uint8_t* q = blk + (TYPE == kQ5_K ? 48 : 16) + 32 * (step & 3) + G::QB * wpart[p];
+#pragma unroll
+        for (int i = 0; i < G::W0; ++i) ra[i] = load4(q + 4 * i);
+        if constexpr (TYPE == kQ5_K) {
+#pragma unroll
+          for (int i = 0; i < G::W0; ++i) rb[4 + i] = load4(blk + 16 + G::QB * wpart[p] + 4 * i);
         }
       } else {
-        const uint2 v = load8(q);
-        r.a[0] = v.x; r.a[1] = v.y;
-      }
-      r.b[0] = load4(b);
-      r.b[1] = 0;
-    } else if constexpr (KQ) {
-      const uint4 hd = load16(blk);
-      r.b[0] = hd.x; r.b[1] = hd.y; r.b[2] = hd.z; r.b[3] = hd.w;
-      const uint8_t* q = blk + (TYPE == kQ5_K ? 48 : 16) + 32 * (step & 3) + G::QB * wpart;
+        const int h = (step & 3) >> 1, e0 = G::EPT * wpart[p];  // element offset inside the step
+        const int quarter = 2 * (step & 1) + (e0 >> 5), l0 = e0 & 31;
+        const uint8_t* ql = blk + 64 * h + e0;
+        const uint8_t* qh = blk + 128 + 32 * h + l0;
 #pragma unroll
-      for (int i = 0; i < G::W0; ++i) r.a[i] = load4(q + 4 * i);
-      if constexpr (TYPE == kQ5_K) {
-#pragma unroll
-        for (int i = 0; i < G::W0; ++i) r.b[4 + i] = load4(blk + 16 + G::QB * wpart + 4 * i);
+        for (int i = 0; i < G::W0; ++i) {
+          ra[i] = load4(ql + 4 * i);
+          rb[i] = load4(qh + 4 * i);
+        }
+        rb[G::W0] = load4(blk + 192 + 8 * h + 2 * quarter);  // scales 2q .. 2q+3 of this half
+        rb[G::W0 + 1] = load4(blk + 206);                    // high half: d
       }
-    } else {
-      const int h = (step & 3) >> 1, e0 = G::EPT * wpart;  // element offset inside the step
-      const int quarter = 2 * (step & 1) + (e0 >> 5), l0 = e0 & 31;
-      const uint8_t* ql = blk + 64 * h + e0;
-      const uint8_t* qh = blk + 128 + 32 * h + l0;
-#pragma unroll
-      for (int i = 0; i < G::W0; ++i) {
-        r.a[i] = load4(ql + 4 * i);
-        r.b[i] = load4(qh + 4 * i);
-      }
-      r.b[G::W0] = load4(blk + 192 + 8 * h + 2 * quarter);  // scales 2q .. 2q+3 of this half
-      r.b[G::W0 + 1] = load4(blk + 206);                    // high half: d
     }
   };
 
@@ -222,72 +244,78 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
       const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
       *reinterpret_cast<uint4*>(&xs[row * ROW + c8]) = make_uint4(r.x[4 * i], r.x[4 * i + 1], r.x[4 * i + 2], r.x[4 * i + 3]);
     }
-    if constexpr (B32) {
-      constexpr int QPB = G::QPB, QB = G::QB;
-      const float d = half_bits_to_float(r.b[0]);
-      // element e of block b (32 b + e in the step) sits at ws[wrow][32 b + e]
-      _Float16* dst = &ws[wrow * ROW + 32 * (QB * wpart / QPB) + QB * wpart % QPB];
-      if constexpr (TYPE == kQ8_0) {
-        // d * q for the int8 code q, as the fp16 subnormal code q + 128 (byte ^ 0x80) times
-        // d 2^24 plus -128 d: the product and the sum (q d) are exact, so is the fp32 value
-        const float d24 = d * kTwo24, bias = -128.0f * d;
+#pragma unroll
+    for (int p = 0; p < PARTS; ++p) {
+      if (!has[p]) continue;
+      const typename RawT::AV& ra = r.a[p];
+      const typename RawT::BV& rb = r.b[p];
+      if constexpr (B32) {
+        constexpr int QPB = G::QPB, QB = G::QB;
+        const float d = half_bits_to_float(rb[0]);
+        // element e of block b (32 b + e in the step) sits at ws[wrow[p]][32 b + e]
+        _Float16* dst = &ws[wrow[p] * ROW + 32 * (QB * wpart[p] / QPB) + QB * wpart[p] % QPB];
+        if constexpr (TYPE == kQ8_0) {
+          // d * q for the int8 code q, as the fp16 subnormal code q + 128 (byte ^ 0x80) times
+          // d 2^24 plus -128 d: the product and the sum (q d) are exact, so is the fp32 value
+          const float d24 = d * kTwo24, bias = -128.0f * d;
+#pragma unroll
+          for (int i = 0; i < G::W0; ++i) {
+            const uint32_t u = ra[i] ^ 0x80808080u;
+            *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(u & 0x00FF00FFu, (u >> 8) & 0x00FF00FFu, d24, bias);
+          }
+        } else {
+          // (q - 8) * d: byte j's low nibble is element j, its high nibble element j + 16
+          const float d24 = d * kTwo24, bias = -8.0f * d;
+#pragma unroll
+          for (int i = 0; i < G::W0; ++i) {
+            const uint32_t q = ra[i];
+            *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(q & 0x000F000Fu, (q >> 8) & 0x000F000Fu, d24, bias);
+            *reinterpret_cast<uint2*>(dst + 16 + 4 * i) =
+                affine4((q >> 4) & 0x000F000Fu, (q >> 12) & 0x000F000Fu, d24, bias);
+          }
+        }
+      } else if constexpr (KQ) {
+        int sc_lo, mn_lo, sc_hi, mn_hi;
+        q4k_scale_pair(rb[1], rb[2], rb[3], step & 3, sc_lo, mn_lo, sc_hi, mn_hi);
+        const float d = half_bits_to_float(rb[0]), dmin = half_bits_to_float(rb[0] >> 16);
+        // d*sc*q - dmin*m: the product is exact, the subtraction rounds once
+        const float ds_lo = d * (float)sc_lo * kTwo24, dm_lo = -(dmin * (float)mn_lo);
+        const float ds_hi = d * (float)sc_hi * kTwo24, dm_hi = -(dmin * (float)mn_hi);
+        _Float16* dst = &ws[wrow[p] * ROW + G::QB * wpart[p]];
 #pragma unroll
         for (int i = 0; i < G::W0; ++i) {
-          const uint32_t u = r.a[i] ^ 0x80808080u;
-          *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(u & 0x00FF00FFu, (u >> 8) & 0x00FF00FFu, d24, bias);
+          const uint32_t q = ra[i];  // low nibbles: sub-block 2j, high nibbles: 2j+1
+          uint32_t lo02 = q & 0x000F000Fu, lo13 = (q >> 8) & 0x000F000Fu;
+          uint32_t hi02 = (q >> 4) & 0x000F000Fu, hi13 = (q >> 12) & 0x000F000Fu;
+          if constexpr (TYPE == kQ5_K) {
+            // fifth bits: bit 2j (sub-block 2j) and 2j+1 of the qh byte at the quant byte's position
+            const uint32_t h = rb[4 + i] >> (2 * (step & 3));
+            lo02 |= (h & 0x00010001u) << 4;
+            lo13 |= ((h >> 8) & 0x00010001u) << 4;
+            hi02 |= ((h >> 1) & 0x00010001u) << 4;
+            hi13 |= ((h >> 9) & 0x00010001u) << 4;
+          }
+          *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(lo02, lo13, ds_lo, dm_lo);
+          *reinterpret_cast<uint2*>(dst + 32 + 4 * i) = affine4(hi02, hi13, ds_hi, dm_hi);
         }
       } else {
-        // (q - 8) * d: byte j's low nibble is element j, its high nibble element j + 16
-        const float d24 = d * kTwo24, bias = -8.0f * d;
+        const int e0 = G::EPT * wpart[p];
+        const int quarter = 2 * (step & 1) + (e0 >> 5), l0 = e0 & 31;
+        const float d = half_bits_to_float(rb[G::W0 + 1] >> 16);
+        _Float16* dst = &ws[wrow[p] * ROW + e0];
 #pragma unroll
         for (int i = 0; i < G::W0; ++i) {
-          const uint32_t q = r.a[i];
-          *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(q & 0x000F000Fu, (q >> 8) & 0x000F000Fu, d24, bias);
-          *reinterpret_cast<uint2*>(dst + 16 + 4 * i) =
-              affine4((q >> 4) & 0x000F000Fu, (q >> 12) & 0x000F000Fu, d24, bias);
+          // 6-bit codes of elements l0 + 4i .. + 3 of this quarter
+          const uint32_t lo = (ra[i] >> (4 * (step & 1))) & 0x0F0F0F0Fu;
+          const uint32_t hi = ((rb[i] >> (2 * quarter)) & 0x03030303u) << 4;
+          const uint32_t q = lo | hi;
+          // scale index 8h + 2 quarter + l / 16: byte l / 16 of the dword loaded at 2 quarter
+          const float sc = (float)(int8_t)(rb[G::W0] >> (8 * ((l0 + 4 * i) >> 4)));
+          // (q - 32) * sc * d == q * (sc d) - 32 (sc d): exact, one fused rounding
+          const float scd = sc * d;
+          *reinterpret_cast<uint2*>(dst + 4 * i) =
+              affine4(q & 0x003F003Fu, (q >> 8) & 0x003F003Fu, scd * kTwo24, -32.0f * scd);
         }
-      }
-    } else if constexpr (KQ) {
-      int sc_lo, mn_lo, sc_hi, mn_hi;
-      q4k_scale_pair(r.b[1], r.b[2], r.b[3], step & 3, sc_lo, mn_lo, sc_hi, mn_hi);
-      const float d = half_bits_to_float(r.b[0]), dmin = half_bits_to_float(r.b[0] >> 16);
-      // d*sc*q - dmin*m: the product is exact, the subtraction rounds once
-      const float ds_lo = d * (float)sc_lo * kTwo24, dm_lo = -(dmin * (float)mn_lo);
-      const float ds_hi = d * (float)sc_hi * kTwo24, dm_hi = -(dmin * (float)mn_hi);
-      _Float16* dst = &ws[wrow * ROW + G::QB * wpart];
-#pragma unroll
-      for (int i = 0; i < G::W0; ++i) {
-        const uint32_t q = r.a[i];  // low nibbles: sub-block 2j, high nibbles: 2j+1
-        uint32_t lo02 = q & 0x000F000Fu, lo13 = (q >> 8) & 0x000F000Fu;
-        uint32_t hi02 = (q >> 4) & 0x000F000Fu, hi13 = (q >> 12) & 0x000F000Fu;
-        if constexpr (TYPE == kQ5_K) {
-          // fifth bits: bit 2j (sub-block 2j) and 2j+1 of the qh byte at the quant byte's position
-          const uint32_t h = r.b[4 + i] >> (2 * (step & 3));
-          lo02 |= (h & 0x00010001u) << 4;
-          lo13 |= ((h >> 8) & 0x00010001u) << 4;
-          hi02 |= ((h >> 1) & 0x00010001u) << 4;
-          hi13 |= ((h >> 9) & 0x00010001u) << 4;
-        }
-        *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(lo02, lo13, ds_lo, dm_lo);
-        *reinterpret_cast<uint2*>(dst + 32 + 4 * i) = affine4(hi02, hi13, ds_hi, dm_hi);
-      }
-    } else {
-      const int e0 = G::EPT * wpart;
-      const int quarter = 2 * (step & 1) + (e0 >> 5), l0 = e0 & 31;
-      const float d = half_bits_to_float(r.b[G::W0 + 1] >> 16);
-      _Float16* dst = &ws[wrow * ROW + e0];
-#pragma unroll
-      for (int i = 0; i < G::W0; ++i) {
-        // 6-bit codes of elements l0 + 4i .. + 3 of this quarter
-        const uint32_t lo = (r.a[i] >> (4 * (step & 1))) & 0x0F0F0F0Fu;
-        const uint32_t hi = ((r.b[i] >> (2 * quarter)) & 0x03030303u) << 4;
-        const uint32_t q = lo | hi;
-        // scale index 8h + 2 quarter + l / 16: byte l / 16 of the dword loaded at 2 quarter
-        const float sc = (float)(int8_t)(r.b[G::W0] >> (8 * ((l0 + 4 * i) >> 4)));
-        // (q - 32) * sc * d == q * (sc d) - 32 (sc d): exact, one fused rounding
-        const float scd = sc * d;
-        *reinterpret_cast<uint2*>(dst + 4 * i) =
-            affine4(q & 0x003F003Fu, (q >> 8) & 0x003F003Fu, scd * kTwo24, -32.0f * scd);
       }
     }
   };
@@ -445,12 +473,14 @@ namespace {
 
 // Workgroup tiles of the pipelined GEMM, by index: 0..3 without a K split inside the workgroup,
 // 4..7 with two or four wave groups per workgroup (LDS holds one double-buffered stage per
-// group, so 128 x 128 and 128 x 64 take KS <= 2 and 64 x 64 KS <= 4).
+// group, so 128 x 128 and 128 x 64 take KS <= 2 and 64 x 64 KS <= 4), 8 the 256 x 96 tile (8
+// waves of 64 x 48).
 struct Tile {
   int bm, bn, ks;
 };
-constexpr Tile kTiles[8] = {{256, 128, 1}, {128, 128, 1}, {128, 64, 1}, {64, 64, 1},
-                            {128, 128, 2}, {128, 64, 2}, {64, 64, 2}, {64, 64, 4}};
+constexpr int kTileCount = 9;
+constexpr Tile kTiles[kTileCount] = {{256, 128, 1}, {128, 128, 1}, {128, 64, 1}, {64, 64, 1}, {128, 128, 2},
+                                     {128, 64, 2},  {64, 64, 2},   {64, 64, 4},  {256, 96, 1}};
 
 long tile_count(const GemmGroupArgs& a, const Tile& t) {
   long columns = 0;
@@ -513,6 +543,7 @@ hipError_t launch_tile(const GemmGroupArgs& a, int tile, int splits, void* works
     case 5: return launch_pipe<TYPE, 128, 64, 2, 2, 2, OutT, XT>(a, splits, workspace, stream);
     case 6: return launch_pipe<TYPE, 64, 64, 1, 2, 2, OutT, XT>(a, splits, workspace, stream);
     case 7: return launch_pipe<TYPE, 64, 64, 1, 2, 4, OutT, XT>(a, splits, workspace, stream);
+    case 8: return launch_pipe<TYPE, 256, 96, 4, 2, 1, OutT, XT>(a, splits, workspace, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -536,7 +567,7 @@ bool pipe_type(int type) {
 // encodings.
 bool valid_plan(const GemmGroupArgs& a, int tile, int splits) {
   const int steps = a.k / pipe::BK, unit = a.type == kQ8_0 || a.type == kQ4_0 ? 2 : 4;
-  return tile >= 0 && tile < 8 && splits >= 1 && a.k % pipe::BK == 0 &&
+  return tile >= 0 && tile < kTileCount && splits >= 1 && a.k % pipe::BK == 0 &&
          steps % (unit * kTiles[tile].ks * splits) == 0;
 }
 
@@ -551,10 +582,22 @@ constexpr long kMinBlocks = 160;
 // 39.8 us on 64 x 64 KS2, M = 128 72.3 -> 51.4 on 128 x 128 KS2; one 12288-row gate at M = 96 /
 // 128 on 128 x 64 KS2 33.1 / 33.9 us; the Q6_K LM head at M = 32 414 -> 320 us).  At M <= 64
 // the 64 x 64 tile splits K over 4 wave groups while its tiles stay within 256, else over 2.
+//
+// 256 x 96 against 256 x 128: per workgroup a 96-column step takes 0.84 of a 128-column one
+// (timing harness, Q4_K M = 2048: 1.008 against 1.196 us per step), so the narrower tile wins
+// where its extra workgroups still fit the rounds of the wider one: C4 at M = 512 and C5's gate
+// + up at M = 256 (192 -> 256 workgroups, one round): 70.9 -> 64.9 us and 71.1 -> 64.6 us; Q6_K
+// and Q8_0 at C4 M = 512 88.4 -> 79.9 and 79.2 -> 67.0 us; at M = 2048 (three rounds against
+// four) the 128-column tile stays (229.7 against 257.4 us).
+int wide_tile(const GemmGroupArgs& a) {
+  const long rounds0 = (tile_count(a, kTiles[0]) + 255) / 256, rounds8 = (tile_count(a, kTiles[8]) + 255) / 256;
+  return rounds8 * 84 < rounds0 * 100 ? 8 : 0;
+}
+
 int base_tile(const GemmGroupArgs& a) {
   const int steps = a.k / pipe::BK;  // even (whole 32-element block pairs or super-blocks)
   const bool ks2 = steps % 8 == 0, ks4 = steps % 16 == 0;
-  if (a.m > 128 && tile_count(a, kTiles[0]) >= kMinBlocks) return 0;
+  if (a.m > 128 && tile_count(a, kTiles[0]) >= kMinBlocks) return wide_tile(a);
   if (a.m > 64) {
     const long wide = tile_count(a, kTiles[1]);
     if (wide >= 512) return 1;

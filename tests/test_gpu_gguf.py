@@ -537,6 +537,8 @@ def test_c5_layer_chained_in_one_graph(hip_device, c_oracle, m):
     (80, 1000, 768),     # 64x64 unsplit, ragged N (M <= 64 at N <= 4096 takes the small-M kernel)
     (80, 1000, 512),     # 64x64, K split 2
     (256, 9984, 1024),   # 64x64, K split 4
+    (300, 11000, 512),   # 256x96 (one round of 230 workgroups against 172 of 256x128), ragged M and N
+    (512, 14000, 512),   # 256x128 (256x96 would need a second round)
 ])
 def test_gemm_tile_configurations(hip_device, c_oracle, encoding, m, n, k):
     """Shapes that select each workgroup tile and K split of the prefill kernel."""
@@ -571,7 +573,8 @@ def test_gemm_tiles_at_small_m(hip_device, c_oracle, encoding, m, n, k):
 
 @pytest.mark.parametrize("encoding", ["q4_k", "q5_k", "q6_k", "q8_0", "q4_0"])
 @pytest.mark.parametrize("k,n", [
-    (512, 10240),   # 256x128 tile
+    (512, 10240),   # 256x96 tile (214 workgroups in one round)
+    (512, 14000),   # 256x128 tile, ragged N
     (1024, 2560),   # 128x128, K split 2
     (512, 1024),    # 64x64, K split 2
     (768, 320),     # 64x64 unsplit, ragged N

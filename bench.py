@@ -25,8 +25,8 @@ Also reported:
 * ``roofline`` for the dominant kernel (the grouped gate + up GEMV, 2 x
   12288 x 4096): ``avg_us``, ``achieved``, ``frac`` and HBM ``traffic`` from
   the committed rocprofv3 summary (profiles/gemv_q4k_m1_qwen3_mlp.md), and this
-  run's own HIP-event timings under ``live``: per dispatch (eager launches, as
-  the trace records them) and per launch of a captured graph;
+  run's own HIP-event timings under ``live``: per launch of 200 eager launches
+  and of the same launches captured in a graph;
 * ``cpu_baseline``: the C restatement in oracle/, invoked through its
   TensorKernelV1 entries exactly as the reference CPU provider invokes images,
   on the headline step and on every other configuration (``per_config``:
@@ -134,26 +134,6 @@ def time_launches(device, launches, per=1, replays=REPLAYS):
         return summarize(timed(graph.replay), per)
     finally:
         graph.close()
-
-
-def time_each(device, launches):
-    """Per-dispatch durations of eager launches, the way a kernel trace records them: each launch
-    bracketed by its own pair of HIP events on the launch stream and synchronized before the
-    next, so every kernel starts on an idle queue.  Returns per-launch statistics and the mean."""
-    warm(device, lambda: [launch() for launch in launches])
-    samples = []
-    for launch in launches:
-        start = device.record_event(timing=True)
-        launch()
-        stop = device.record_event(timing=True)
-        stop.synchronize()
-        samples.append(device.elapsed_ms(start, stop) * 1e-3)
-        start.release()
-        stop.release()
-    stats = summarize(samples, 1)
-    stats["mean_us"] = round(statistics.fmean(samples) * 1e6, 3)
-    del stats["samples_us"]
-    return stats
 
 
 def rate(stats, work, unit):
@@ -600,6 +580,22 @@ def detail_cases(device):
             group.release()
             return result
 
+    @add("C2_host_enqueue_m1_gate_up")
+    def host_enqueue():
+        # host cost of one eager launch of the headline's grouped gate + up GEMV through
+        # BoundCall.launch (tensor.runtime.bench's three figures; src/tensor/runtime/timing.py:10-43)
+        from tensor_amd.runtime.timing import bench as runtime_bench
+
+        group = GroupLinear(device, "q4_k", 1, [(12288, 4096), (12288, 4096)], "float16", 1, 80)
+        exe = device.load("gguf_gemv_group", encoding="q4_k", out_dtype="float16", count=2)
+        figures = runtime_bench(exe, (group.x, group.weights[0][0], group.outs[0], group.weights[1][0], group.outs[1]),
+                                warmup=50, iters=200)
+        group.release()
+        return {"host_enqueue_us": round(figures["median_host_enqueue_seconds"] * 1e6, 2),
+                "launch_and_sync_us": round(figures["median_launch_and_sync_seconds"] * 1e6, 2),
+                "device_us": round(figures["median_device_seconds"] * 1e6, 3),
+                "timing": "tensor_amd.runtime.timing.bench: medians of 200 eager launches, one weight copy"}
+
     # C1's shape (the reference runs it on its CPU provider) on the GPU
     gemv_case("C1_q8_0_gemv_m1_4096x4096", "q8_0", 1, 4096, 4096, "float16")
     gemv_case("C5_q6k_gemv_m1_4096x12288", "q6_k", 1, 4096, 12288, "float16")
@@ -814,25 +810,26 @@ def main():
 
         # ---- roofline of the dominant kernel: the grouped gate + up GEMV, 2 x 12288 x 4096, M=1.
         # achieved / frac / avg_us are the committed rocprofv3 per-dispatch average of this kernel
-        # (profiles/gemv_q4k_m1_qwen3_mlp.md); this run's own event timings sit beside them under
-        # "live": per dispatch (each eager launch bracketed by HIP events, as the trace records a
-        # dispatch) and per launch of a graph of 200 launches (consecutive launches overlap ramp-up
-        # and drain).
+        # (profiles/gemv_q4k_m1_qwen3_mlp.md); this run's own HIP-event timings sit beside them
+        # under "live": the same 200 launches enqueued eagerly (host enqueue ~5 us per launch,
+        # below the kernel's time, so the stream stays busy) and replayed from a captured graph.
         launches = 200
-        graph = time_launches(device, [gate_up.calls[i % copies].launch for i in range(launches)], per=launches)
-        eager = time_each(device, [gate_up.calls[i % copies].launch for i in range(launches)])
+        sequence = [gate_up.calls[i % copies].launch for i in range(launches)]
+        graph = time_launches(device, sequence, per=launches)
+        TIMING, mode = "eager", TIMING
+        eager = time_launches(device, sequence, per=launches)
+        TIMING = mode
         figures = profile_figures()
-        live = {
-            "per_dispatch": dict(eager, achieved=round(gate_up.bytes / eager["mean_us"] / 1e3, 1),
-                                 frac=round(gate_up.bytes / eager["mean_us"] / 1e3 / HBM_PEAK_GBS, 4),
-                                 timing=f"{launches} eager launches, each bracketed by HIP events on the launch "
-                                        "stream; mean and median of the per-dispatch durations"),
-            "graph": {"avg_us": graph["median_us"], "avg_us_min": graph["min_us"], "avg_us_max": graph["max_us"],
-                      "achieved": round(gate_up.bytes / graph["median_us"] / 1e3, 1),
-                      "frac": round(gate_up.bytes / graph["median_us"] / 1e3 / HBM_PEAK_GBS, 4),
-                      "timing": f"HIP events around a graph of {launches} launches, median of {REPLAYS} replays"},
-        }
-        avg = figures.get("avg_us_per_launch", eager["mean_us"])
+        def live_figure(stats, how):
+            return {"avg_us": stats["median_us"], "avg_us_min": stats["min_us"], "avg_us_max": stats["max_us"],
+                    "achieved": round(gate_up.bytes / stats["median_us"] / 1e3, 1),
+                    "frac": round(gate_up.bytes / stats["median_us"] / 1e3 / HBM_PEAK_GBS, 4),
+                    "timing": f"HIP events on the launch stream around {launches} launches {how}, "
+                              f"median of {REPLAYS} replays"}
+
+        live = {"eager": live_figure(eager, "enqueued back to back"),
+                "graph": live_figure(graph, "captured in one graph")}
+        avg = figures.get("avg_us_per_launch", eager["median_us"])
         roofline = {
             "bound": "hbm",
             "achieved": round(gate_up.bytes / avg / 1e3, 1),
@@ -843,14 +840,14 @@ def main():
             "kernel": "gemv_q4k_m1<STEPS=1, WAVES=8, MATS=2> gate+up 2 x 12288x4096, M=1, fp16 out",
             "avg_us": avg,
             "timing": ("rocprofv3 --kernel-trace --stats per-dispatch average, profiles/gemv_q4k_m1_qwen3_mlp.md"
-                       if "avg_us_per_launch" in figures else "live per-dispatch mean (no committed profile)"),
+                       if "avg_us_per_launch" in figures else "live eager average (no committed profile)"),
             "algorithmic_bytes": gate_up.bytes,
             "live": live,
-            "live_per_dispatch_vs_profiled": round(eager["mean_us"] / avg, 4),
+            "live_eager_vs_profiled": round(eager["median_us"] / avg, 4),
         }
         achieved = roofline["achieved"]
-        log(f"roofline kernel: profiled {avg:.3f} us -> {achieved:.1f} GB/s; live per dispatch "
-            f"{eager['mean_us']:.3f} us (median {eager['median_us']:.3f}), graph {graph['median_us']:.3f} us")
+        log(f"roofline kernel: profiled {avg:.3f} us -> {achieved:.1f} GB/s; live eager {eager['median_us']:.3f} us, "
+            f"graph {graph['median_us']:.3f} us")
         for layer in mlp:
             layer.release()
 

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import contextlib
 import ctypes as c
+import threading
 
 import numpy as np
 
@@ -25,6 +26,13 @@ from tensor_amd.runtime.buffer import Buffer
 from tensor_amd.runtime.event import Event
 from tensor_amd.runtime.executable import Executable
 from tensor_amd.runtime.session import Session
+
+# The device this library last made current on each thread (HIP's current device is per thread).
+# Launches consult it instead of setting the device again; an entry point that finds another
+# current device (set by other code on the thread) refuses the call before enqueuing anything,
+# and the launch then sets the device and submits once more.
+_thread = threading.local()
+_NOT_CURRENT = b"is not the current device"
 
 
 def device_count() -> int:
@@ -74,7 +82,6 @@ class Device(Session):
         }
         self.stream = 0
         self._buffers: set = set()
-        self._events: set = set()
         self._consumers: set = set()
         self._graphs: set = set()
         self._capture_log = None  # list of buffers while a HipGraph capture is open
@@ -101,6 +108,15 @@ class Device(Session):
         if not self._open:
             raise HipError("Device", 3, "HIP device session is closed")
         _native.call("tensor_hip_set_device", self.ordinal)
+        _thread.ordinal = self.ordinal
+
+    def _make_current(self) -> None:
+        """The launch path's device check: no native call when this thread's device is set."""
+        if not self._open:
+            raise HipError("Device", 3, "HIP device session is closed")
+        if getattr(_thread, "ordinal", None) != self.ordinal:
+            _native.call("tensor_hip_set_device", self.ordinal)
+            _thread.ordinal = self.ordinal
 
     def stream_descriptor(self) -> StreamDescriptor:
         return StreamDescriptor(DEVICE_ROCM, self.ordinal, self.stream)
@@ -331,15 +347,24 @@ class Device(Session):
         # built-in entry points live for the life of the process-wide library
 
     def _launch(self, executable, call) -> None:
-        self._check()
+        self._make_current()
         if self._capture_log is not None:
             self._capture_log.extend(call.storage)
         error = ErrorDescriptor()
         if executable.manifest.get("kind") == "hsaco":
-            status = _native.library().tensor_hip_module_launch_v1(executable.function, c.byref(call.descriptor),
-                                                                  c.byref(error))
+            module_launch = _native.library().tensor_hip_module_launch_v1
+
+            def submit():
+                return module_launch(executable.function, c.byref(call.descriptor), c.byref(error))
         else:
-            status = executable.function(c.byref(call.descriptor), c.byref(error))
+            entry = executable.function
+
+            def submit():
+                return entry(c.byref(call.descriptor), c.byref(error))
+        status = submit()
+        if status == 3 and _NOT_CURRENT in error.message:
+            self._check()  # another caller moved this thread's device; the call was not enqueued
+            status = submit()
         if status:
             raise HipError(executable.manifest["entrypoint"], status, error.message.decode(errors="replace"))
 
@@ -353,9 +378,7 @@ class Device(Session):
         except BaseException:
             _native.call("tensor_hip_event_destroy", handle.value)
             raise
-        event = Event(self, handle.value)
-        self._events.add(event)
-        return event
+        return Event(self, handle.value)
 
     def wait(self, event: Event) -> None:
         self._check()
@@ -423,7 +446,6 @@ class Device(Session):
             attempt(_native.call, "tensor_hip_stream_destroy", self.stream)
         self._open = False
         self._buffers.clear()
-        self._events.clear()
         self._consumers.clear()
         self._graphs.clear()
         self.stream = 0

@@ -181,11 +181,17 @@ class BoundCall:
 
     def launch(self) -> None:
         """Submit again: the descriptors are reused as they are (no allocation, no re-binding);
-        a released executable or buffer is refused before the provider sees the call."""
+        a released executable or buffer is refused before the provider sees the call.  The
+        checks read Python state only; the provider's launch is the one native call (its device
+        check costs none while the thread's device stays set)."""
         executable = self.executable
-        executable._check()
+        fault = executable._fault()
+        if fault:
+            raise executable.device.error(fault)
+        generation = executable._generation
         for buffer in self.storage:
-            buffer._check()
+            if buffer._released or buffer._generation != generation:
+                buffer._check()  # raises the buffer's own error
         executable.device._launch(executable, self)
 
     __call__ = launch

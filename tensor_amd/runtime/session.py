@@ -18,12 +18,12 @@ _sessions = itertools.count(1)
 
 
 class Registry:
-    """Handles issued by one session: executables by handle; events are looked up by the
-    session's event set."""
+    """What one session issued, by ticket: executables and events."""
 
     def __init__(self):
         self.session_id = next(_sessions)
         self.executables = {}
+        self.events = {}
         self._tickets = itertools.count(1)
 
     def ticket(self) -> int:
@@ -44,6 +44,12 @@ class Session:
     @property
     def _executables(self) -> dict:
         return self._registry.executables
+
+    @property
+    def _events(self) -> list:
+        """The live events of the current (or last) session."""
+        registry = getattr(self, "_registry", None)
+        return list(registry.events.values()) if registry is not None else []
 
     def _owns(self, descriptor, expected_type, kind: str) -> None:
         if type(descriptor) is not expected_type or descriptor.abi_version != ABI_MAJOR \
@@ -68,7 +74,7 @@ class Session:
 
     def get_event(self, descriptor):
         self._owns(descriptor, EventDescriptor, "event")
-        match = next((e for e in self._events if e._descriptor.handle == descriptor.handle), None)
+        match = self._registry.events.get(descriptor.handle)
         if match is None:
             raise self.error("event handle is released or unknown")
         if descriptor.flags != match._descriptor.flags or descriptor.reserved:

@@ -83,8 +83,16 @@ _OPERATIONS = {"add": _checked(operator.add), "sub": _checked(operator.sub), "mu
                "min": _checked(min), "max": _checked(max)}
 
 
-def compile_expression(tree):
-    """A closure ``symbols -> int`` for one integer expression tree."""
+def _range_cast(value, dtype):
+    return scalar_value(value, dtype, "dimension cast")
+
+
+def compile_expression(tree, operations=None, cast=_range_cast):
+    """A closure ``symbols -> int`` for one integer expression tree.  ``operations`` maps the
+    operator names to two-argument functions (default: int64-checked integer arithmetic) and
+    ``cast(value, dtype)`` applies a cast node, so the same trees also compile over other
+    integer types (PyTorch's symbolic sizes)."""
+    operations = _OPERATIONS if operations is None else operations
     if type(tree) is int:
         return lambda symbols: tree
     if not isinstance(tree, dict):
@@ -101,11 +109,11 @@ def compile_expression(tree):
                     from None
         return symbol
     if keys == {"cast", "value"}:
-        inner, dtype = compile_expression(tree["value"]), tree["cast"]
-        return lambda symbols: scalar_value(inner(symbols), dtype, "dimension cast")
-    if keys == {"op", "args"} and tree["op"] in _OPERATIONS and len(tree["args"]) == 2:
-        operation = _OPERATIONS[tree["op"]]
-        left, right = (compile_expression(arg) for arg in tree["args"])
+        inner, dtype = compile_expression(tree["value"], operations, cast), tree["cast"]
+        return lambda symbols: cast(inner(symbols), dtype)
+    if keys == {"op", "args"} and tree["op"] in operations and len(tree["args"]) == 2:
+        operation = operations[tree["op"]]
+        left, right = (compile_expression(arg, operations, cast) for arg in tree["args"])
         return lambda symbols: operation(left(symbols), right(symbols))
     raise ValueError(f"invalid shape expression {tree!r}")
 

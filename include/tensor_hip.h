@@ -149,8 +149,11 @@ int32_t tensor_gguf_gemm_group_v1(const TensorCallV1 *call, TensorErrorV1 *error
  * tensor_gguf_gemm_workspace_v1 reports and so gives the same bits, and refuses a shape whose
  * split would need more scratch (by construction none does: a split's partials cover at most
  * 256 tiles of 256 x 128 fp32).  Every partial read is written earlier in the same call, so
- * nothing needs clearing, but calls that overlap on one GPU (two streams, or two threads)
- * share the array and race: serialise them.
+ * nothing needs clearing.  Calls share the array: an eager call on a different stream from the
+ * previous eager call on the GPU first waits (hipStreamWaitEvent) for that call to finish, so
+ * eager calls on several streams or threads take the scratch in turn.  Calls captured into a
+ * graph are not ordered that way (a replay chooses its stream later): replays of such graphs,
+ * and eager calls beside them, that overlap on one GPU race, and the caller serialises them.
  */
 #define TENSOR_GGUF_NOALLOC_SCRATCH_BYTES (32u << 20)
 int32_t tensor_gguf_gemm_group_noalloc_v1(const TensorCallV1 *call, TensorErrorV1 *error);

@@ -26,21 +26,33 @@ namespace {
 
 constexpr int kScratchDevices = 64;
 std::mutex scratch_mutex;
-void* scratch_device[kScratchDevices];  // by ordinal, nullptr until resolved
 
-// Address of the current device's scratch copy, resolved once per device with that device
-// current (the caller has checked that the stream's ordinal is the current device).
-hipError_t scratch_address(int ordinal, void** address) {
+// Per device: the scratch copy's address (nullptr until resolved) and the last eager use of it,
+// the stream it ran on and an event recorded after it.
+struct ScratchState {
+  void* address;
+  hipEvent_t done;
+  hipStream_t last;
+  bool used;
+};
+ScratchState scratch_state[kScratchDevices];
+
+// The current device's scratch state, set up once per device with that device current (the
+// caller has checked that the stream's ordinal is the current device): the copy's address and
+// the event that orders eager calls on different streams.  Call with scratch_mutex held.
+hipError_t scratch_setup(int ordinal, ScratchState** state) {
   if (ordinal < 0 || ordinal >= kScratchDevices) return hipErrorInvalidDevice;
-  std::lock_guard<std::mutex> lock(scratch_mutex);
-  if (!scratch_device[ordinal]) {
+  ScratchState& s = scratch_state[ordinal];
+  if (!s.address) {
     void* resolved = nullptr;
-    const hipError_t status = hipGetSymbolAddress(&resolved, HIP_SYMBOL(scratch));
+    hipError_t status = hipGetSymbolAddress(&resolved, HIP_SYMBOL(scratch));
     if (status != hipSuccess) return status;
     if (!resolved) return hipErrorInvalidSymbol;
-    scratch_device[ordinal] = resolved;
+    status = hipEventCreateWithFlags(&s.done, hipEventDisableTiming);
+    if (status != hipSuccess) return status;
+    s.address = resolved;
   }
-  *address = scratch_device[ordinal];
+  *state = &s;
   return hipSuccess;
 }
 
@@ -435,11 +447,28 @@ int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has
     workspace_bytes = kScratchBytes;
   }
   if (int32_t s = check_device(call, error)) return s;
-  if (!has_workspace) {
-    const hipError_t status = scratch_address(call->stream.device_ordinal, &workspace);
-    if (status != hipSuccess) return hip_fail(error, status, "hipGetSymbolAddress(scratch)");
-  }
   hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
+  // The scratch is one array per device: an eager call on another stream than the previous eager
+  // call first waits for that call's event, and the mutex keeps host threads from interleaving
+  // between the wait and the record.  Under stream capture nothing is waited for or recorded
+  // (the graph's replays choose their streams later).
+  std::unique_lock<std::mutex> scratch_lock(scratch_mutex, std::defer_lock);
+  ScratchState* scratch_use = nullptr;
+  bool eager = false;
+  if (!has_workspace) {
+    scratch_lock.lock();
+    hipError_t status = scratch_setup(call->stream.device_ordinal, &scratch_use);
+    if (status != hipSuccess) return hip_fail(error, status, "scratch set-up");
+    workspace = scratch_use->address;
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    status = hipStreamIsCapturing(stream, &capture);
+    if (status != hipSuccess) return hip_fail(error, status, "hipStreamIsCapturing");
+    eager = capture == hipStreamCaptureStatusNone;
+    if (eager && scratch_use->used && scratch_use->last != stream) {
+      status = hipStreamWaitEvent(stream, scratch_use->done, 0);
+      if (status != hipSuccess) return hip_fail(error, status, "hipStreamWaitEvent(scratch)");
+    }
+  }
   hipError_t status = hipSuccess;
   tensor_gguf::GemvArgs one[tensor_gguf::kGemmGroupMax];
   bool small = true;  // every matrix on the small-M kernel, as tensor_gguf_gemm_v1 would run it
@@ -462,6 +491,12 @@ int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has
     for (int i = 0; i < count && status == hipSuccess; ++i) status = tensor_gguf::launch_gemm(one[i], stream);
   }
   if (status != hipSuccess) return hip_fail(error, status, "GGUF grouped GEMM launch");
+  if (eager) {
+    status = hipEventRecord(scratch_use->done, stream);
+    if (status != hipSuccess) return hip_fail(error, status, "hipEventRecord(scratch)");
+    scratch_use->last = stream;
+    scratch_use->used = true;
+  }
   return TENSOR_OK;
 }
 

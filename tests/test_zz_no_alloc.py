@@ -63,3 +63,45 @@ def test_noalloc_matches_the_workspace_form_on_two_calls(hip_device, c_oracle, o
             if out_dtype == "float32":
                 err = R.relative_l2(got[i], c_oracle.linear(x, raws[i], Q.ggml_type(encoding), n, k, prefill=True))
                 assert err <= 1e-5, (index, i, err)
+
+
+def test_noalloc_calls_on_two_streams_take_the_scratch_in_turn(c_oracle):
+    """Eager calls on two sessions' streams, enqueued back to back with no host wait between
+    them: the library orders each call after the previous one on the other stream, so both give
+    the workspace form's bits although they share the scratch."""
+    import tensor_amd as tx
+
+    encoding, m, k, rows = CALLS[0]
+    inputs = [(cases.activation(m, k, 950 + i), [cases.weight(n, k, encoding, 960 + 10 * i + j)
+                                                 for j, n in enumerate(rows)]) for i in range(2)]
+    with tx.Device(0, provider="hip") as first, tx.Device(0, provider="hip") as second:
+        assert first.stream != second.stream
+        sessions = (first, second)
+        exes = [d.load("gguf_gemm_group_noalloc", encoding=encoding, out_dtype="float32", count=len(rows))
+                for d in sessions]
+        calls, keep = [], []
+        for device, exe, (x, raws) in zip(sessions, exes, inputs):
+            xb = device.from_numpy(x)
+            wbs = [device.from_numpy(raw) for raw in raws]
+            outs = [device.empty((m, n), "float32") for n in rows]
+            args = [xb]
+            for wb, out in zip(wbs, outs):
+                device.fill_bytes(out, 0xFF)
+                args += [wb, out]
+            device.synchronize()
+            calls.append(exe.bind(*args))
+            keep.append((xb, wbs, outs))
+        print("[noalloc] two streams, three alternating rounds", flush=True)
+        for _ in range(3):
+            calls[0].launch()
+            calls[1].launch()
+        for device in sessions:
+            device.synchronize()
+        got = [[out.to_numpy() for out in outs] for _, _, outs in keep]
+        want = [_run(device, "gguf_gemm_group", encoding, x, raws, "float32",
+                     device.gemm_workspace(encoding, m, k, list(rows)))
+                for device, (x, raws) in zip(sessions, inputs)]
+    for session in range(2):
+        for i in range(len(rows)):
+            assert not np.isnan(got[session][i]).any(), (session, i)
+            assert np.array_equal(got[session][i].view(np.uint8), want[session][i].view(np.uint8)), (session, i)

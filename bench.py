@@ -699,6 +699,25 @@ def detail_cases(device):
         x.release()
         return result
 
+    # The showcase's packed call form (fp32 x and out) at the BASELINE decode shapes, weights
+    # rotated out of the MALL: the cost of the fp32-activation path against the fp16 cases above
+    for encoding, n, k in (("q8_0", 4096, 4096), ("q4_k", 12288, 4096), ("q4_k", 4096, 12288),
+                           ("q6_k", 151936, 4096)):
+        @add(f"packed_{encoding}_m1_{n}x{k}_fp32x")
+        def packed_decode(encoding=encoding, n=n, k=k):
+            copies = copies_for(weight_bytes(encoding, n, k))
+            x = device.from_numpy(cases.activation(1, k, 5).astype(np.float32).reshape(-1))
+            weights = rotated(device, cases.weight(n, k, encoding, 6).reshape(-1), copies)
+            out = device.empty((n,), "float32")
+            exe = device.load("gguf_linear", encoding=encoding, m=1, n=n, k=k)
+            calls = [exe.bind(x, w, out) for w in weights]
+            stats = time_launches(device, [calls[i % copies].launch for i in range(60)], per=60)
+            result = dict(stats, **rate(stats, gemv_bytes(encoding, 1, n, k, 4, 4), "GB/s"), copies=copies)
+            result["hbm_frac"] = round(result["GB/s"] / HBM_PEAK_GBS, 4)
+            for b in [x, out, *weights]:
+                b.release()
+            return result
+
     # The showcase's packed call at its own shapes (N = K = 1024, M in {1, 32}, fp32 x and out,
     # benchmark.py:122-126, :460-464), hot-cache as the reference times it (one weight copy).
     for encoding in ("q4_0", "q4_k", "q6_k"):
@@ -734,6 +753,106 @@ def run_details(device, only=None):
     return details
 
 
+# ------------------------------------------------------------- plan sweep --
+
+SWEEP_SHAPES = (("C4_q4k_m512_12288x4096", "q4_k", 512, 4096, (12288,)),
+                ("C4_q4k_m2048_12288x4096", "q4_k", 2048, 4096, (12288,)),
+                ("C5_m256_qkv", "q4_k", 256, 4096, (4096, 1024, 1024)),
+                ("C5_m256_o", "q4_k", 256, 4096, (4096,)),
+                ("C5_m256_gate_up", "q4_k", 256, 4096, (12288, 12288)),
+                ("C5_m256_down_q6k", "q6_k", 256, 12288, (4096,)))
+SWEEP_SPLITS = (1, 2, 4, 8)
+SWEEP_WORKSPACE = 256 << 20  # plans whose partial sums need more are not candidates
+
+
+def plan_sweep(device, only=None):
+    """Every plan of the pipelined prefill GEMM (tile x K split) at the BASELINE GEMM shapes,
+    timed, then the three fastest re-timed on their own before the winner is named, as the
+    reference's schedule search does (benchmarks/kernels/showcase/benchmark.py:214-237, :917-932);
+    beside the winner, the plan the library picks.  Each candidate's output is checked against the
+    library plan's (rel-L2 <= 2e-3, no NaN) before it is timed."""
+    from oracle import gguf_ref as R
+    from tensor_amd.providers.hip import gemm_tiles
+    from tests import gguf_cases as cases
+
+    tiles = gemm_tiles()
+    report = {}
+    for name, encoding, m, k, rows in SWEEP_SHAPES:
+        if only is not None and not name.startswith(only):
+            continue
+        chosen = device.gemm_plan(encoding, m, k, rows)
+        weights = [device.from_numpy(cases.weight(n, k, encoding, 1200 + i)) for i, n in enumerate(rows)]
+        x = device.from_numpy(cases.activation(m, k, 1210))
+        outs = [device.empty((m, n), "float16") for n in rows]
+        workspace = device.empty((SWEEP_WORKSPACE,), "uint8")
+        exe = device.load("gguf_gemm_group_plan", encoding=encoding, out_dtype="float16", count=len(rows))
+        args = [x]
+        for w, out in zip(weights, outs):
+            args += [w, out]
+        flops = sum(2 * m * n * k for n in rows)
+
+        def run_plan(tile, splits):
+            return exe.bind(*args, workspace, tile=tile, splits=splits)
+
+        reference = run_plan(chosen["tile"], chosen["splits"]) if chosen["pipelined"] else None
+        expected = None
+        if reference is not None:
+            reference.launch()
+            expected = [out.to_numpy().astype(np.float32) for out in outs]
+        candidates = []
+        for tile, geometry in enumerate(tiles):
+            for splits in SWEEP_SPLITS:
+                if splits * m * sum(rows) * 4 > SWEEP_WORKSPACE and splits > 1:
+                    continue
+                try:
+                    call = run_plan(tile, splits)
+                    for out in outs:
+                        device.fill_bytes(out, 0xFF)
+                    call.launch()
+                except Exception as exc:  # the entry refuses plans that do not fit the shape
+                    if getattr(exc, "code", None) == 2:
+                        continue
+                    raise
+                got = [out.to_numpy().astype(np.float32) for out in outs]
+                ok = all(not np.isnan(g).any() for g in got)
+                if ok and expected is not None:
+                    ok = max(R.relative_l2(g, e) for g, e in zip(got, expected)) <= 2e-3
+                stats = time_launches(device, [call.launch] * 10, per=10, replays=5)
+                candidates.append({"tile": tile, **geometry, "splits": splits, "valid": bool(ok),
+                                   "median_us": stats["median_us"], "call": call})
+        finalists = sorted((c for c in candidates if c["valid"]), key=lambda c: c["median_us"])[:3]
+        for c in finalists:
+            c["selection"] = time_launches(device, [c["call"].launch] * 60, per=60, replays=7)
+        winner = min(finalists, key=lambda c: c["selection"]["median_us"])
+        library = next((c for c in candidates if (c["tile"], c["splits"]) == (chosen["tile"], chosen["splits"])), None)
+        if library is not None and "selection" not in library:
+            library["selection"] = time_launches(device, [library["call"].launch] * 60, per=60, replays=7)
+
+        def public(c):
+            out = {key: value for key, value in c.items() if key != "call"}
+            if "selection" in c:
+                out["selection"] = {key: c["selection"][key] for key in ("median_us", "min_us", "max_us")}
+            return out
+
+        entry = {
+            "encoding": encoding, "m": m, "k": k, "rows": list(rows), "gflop": round(flops / 1e9, 3),
+            "library_plan": chosen,
+            "winner": public(winner),
+            "library_us": library["selection"]["median_us"] if library else None,
+            "winner_us": winner["selection"]["median_us"],
+            "library_over_winner": round(library["selection"]["median_us"] / winner["selection"]["median_us"], 4)
+            if library else None,
+            "finalists": [public(c) for c in finalists],
+            "candidates": [public(c) for c in sorted(candidates, key=lambda c: c["median_us"])],
+        }
+        report[name] = entry
+        log("sweep", name, "library", (chosen["tile"], chosen["splits"]), entry["library_us"], "us; winner",
+            (winner["tile"], winner["splits"]), entry["winner_us"], "us")
+        for b in [*weights, x, *outs, workspace]:
+            b.release()
+    return report
+
+
 # ------------------------------------------------------------------- main --
 
 def main():
@@ -756,6 +875,9 @@ def main():
                         help="stop after the eager warmup launches (for per-dispatch counter runs)")
     parser.add_argument("--warm-seconds", type=float, default=WARM_SECONDS,
                         help="untimed replay before each timed sequence (0: one replay, e.g. for counter runs)")
+    parser.add_argument("--sweep", action="store_true",
+                        help="time every tile and K split of the prefill GEMM at the BASELINE shapes, re-time the "
+                             "three fastest, and print the winner beside the library's plan (one JSON line)")
     parser.add_argument("--torch-leg", action="store_true", help=argparse.SUPPRESS)
     args = parser.parse_args()
     if args.gpus != 1:
@@ -776,6 +898,10 @@ def main():
     device = tx.Device(0, provider="hip")
     with device:
         log("device", device.info["name"], device.info["arch_features"], "CUs", device.info["compute_units"])
+        if args.sweep:
+            print(json.dumps({"plan_sweep": plan_sweep(device, args.only), "replays": REPLAYS,
+                              "timing": "HIP graph replays, median; finalists re-timed over 7 replays of 60 launches"}))
+            return 0
         if args.calibrate:
             source = device.zeros((256 << 20,), "uint8")
             target = device.empty((256 << 20,), "uint8")

@@ -166,6 +166,32 @@ int32_t tensor_gguf_gemm_workspace_v1(uint32_t type, int64_t m, int64_t k, const
                                       uint64_t *bytes, TensorErrorV1 *error);
 
 /*
+ * The plan tensor_gguf_gemm_group_v1 takes for this shape given workspace_bytes of workspace:
+ * the pipelined GEMM's tile index and K split across workgroups, and whether the pipelined
+ * kernel runs at all (0: each matrix takes the small-M kernel).  No counterpart in the
+ * reference, whose showcase searches schedules per case (benchmarks/kernels/showcase/
+ * benchmark.py:214-237): with the two entries below a caller re-times the plans the library
+ * could take and checks the one it picks.
+ */
+int32_t tensor_gguf_gemm_plan_v1(uint32_t type, int64_t m, int64_t k, const int64_t *n, uint32_t count,
+                                 uint64_t workspace_bytes, int32_t *tile, int32_t *splits, int32_t *pipelined,
+                                 TensorErrorV1 *error);
+
+/* Rows, columns and K wave groups per workgroup of pipelined-GEMM tile `tile` (an index from 0;
+ * TENSOR_ERROR_ARGUMENT past the last tile).  No counterpart in the reference. */
+int32_t tensor_gguf_gemm_tile_v1(int32_t tile, int32_t *bm, int32_t *bn, int32_t *ks, TensorErrorV1 *error);
+
+/*
+ * tensor_gguf_gemm_group_v1 on a plan the caller names, for plan sweeps: arguments
+ * [x, w0, out0, .., w(c-1), out(c-1), workspace, type, tile, splits] with tile and splits uint32
+ * scalars.  TENSOR_ERROR_ARGUMENT when the pipelined kernel cannot run that tile and split on the
+ * shape, or the workspace is shorter than the split needs; the same bits as any other plan up to
+ * fp32 summation order.  No counterpart in the reference (its schedule search times candidate
+ * builds of one kernel, benchmark.py:214-237, :917-932).
+ */
+int32_t tensor_gguf_gemm_group_plan_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/*
  * Decode GEMV of an MLP's gate and up projections with the SwiGLU epilogue:
  * out[m, n] = silu(g) * u, silu(g) = g / (1 + exp(-g)), where g and u are the
  * fp32 sums x[m, :] . dequant(W_gate)[n, :] and x[m, :] . dequant(W_up)[n, :]

@@ -20,6 +20,7 @@ KERNELS = (
     "tensor_gguf_packed_v1",
     "tensor_gguf_gemm_group_v1",
     "tensor_gguf_gemm_group_noalloc_v1",
+    "tensor_gguf_gemm_group_plan_v1",
     "tensor_gguf_gemv_v1",
     "tensor_gguf_gemm_v1",
     "tensor_gguf_linear_v1",
@@ -83,6 +84,9 @@ SERVICES = {
     "tensor_hip_module_unload": [_u64],
     "tensor_gguf_gemm_workspace_v1": [c.c_uint32, c.c_int64, c.c_int64, c.POINTER(c.c_int64), c.c_uint32,
                                       c.POINTER(_u64)],
+    "tensor_gguf_gemm_plan_v1": [c.c_uint32, c.c_int64, c.c_int64, c.POINTER(c.c_int64), c.c_uint32, _u64,
+                                 c.POINTER(_i32), c.POINTER(_i32), c.POINTER(_i32)],
+    "tensor_gguf_gemm_tile_v1": [_i32, c.POINTER(_i32), c.POINTER(_i32), c.POINTER(_i32)],
 }
 
 

@@ -671,6 +671,14 @@ hipError_t launch_gemm_group_plan(const GemmGroupArgs& a, const GemmPlan& plan, 
   }
 }
 
+bool gemm_tile_geometry(int tile, int* bm, int* bn, int* ks) {
+  if (tile < 0 || tile >= kTileCount) return false;
+  *bm = kTiles[tile].bm;
+  *bn = kTiles[tile].bn;
+  *ks = kTiles[tile].ks;
+  return true;
+}
+
 bool gemm_group_pipelined(const GemmGroupArgs& a, const GemmPlan& plan) {
   return pipe_type(a.type) && valid_plan(a, plan.tile, plan.splits);
 }

@@ -107,6 +107,8 @@ bool gemm_pipe_supported(const GemvArgs& args);
 // Pipelined dequant-GEMM of one matrix; sets *handled to false for the encodings and shapes it
 // does not cover.
 hipError_t launch_gemm_pipe(const GemvArgs& args, hipStream_t stream, bool* handled);
+// Rows, columns and K wave groups of pipelined-GEMM tile `tile`; false past the last tile.
+bool gemm_tile_geometry(int tile, int* bm, int* bn, int* ks);
 // One tile configuration of the pipelined GEMM by index (tile sweeps and tests).
 hipError_t launch_gemm_pipe_config(const GemvArgs& args, hipStream_t stream, int config);
 

@@ -385,18 +385,25 @@ int32_t packed_call(const TensorCallV1* call, TensorErrorV1* error) {
 // workspace (has_workspace), or [x, w0, out0, .., type] on the library's static scratch.
 // The scratch form runs the plan the caller's form runs with the workspace that
 // tensor_gguf_gemm_workspace_v1 reports, so the two give the same bits.
-int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has_workspace) {
+// forced: the plan comes from two trailing uint32 scalars (tile, splits) after the type.
+int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has_workspace, bool forced = false) {
   ok(error);
   if (!call || call->abi_version != TENSOR_ABI_VERSION || call->struct_size < sizeof(TensorCallV1))
     return fail(error, TENSOR_ERROR_ABI, "unsupported call ABI");
-  const uint32_t argc = call->argument_count, fixed = has_workspace ? 3 : 2;
+  const uint32_t tail = forced ? 2 : 0;  // scalars after the type
+  const uint32_t argc = call->argument_count, fixed = (has_workspace ? 3 : 2) + tail;
   if (argc < fixed + 2 || argc > fixed + 2 * tensor_gguf::kGemmGroupMax || (argc - fixed) % 2)
     return fail(error, TENSOR_ERROR_ARGUMENT, "invalid argument count or flags");
   if (int32_t s = check_call(call, argc, error)) return s;
   const int count = (int)(argc - fixed) / 2, ordinal = call->stream.device_ordinal;
   const TensorArgumentV1* a = call->arguments;
+  uint64_t forced_tile = 0, forced_splits = 0;
+  if (forced) {
+    if (int32_t s = check_u32(a[argc - 2], "tile", &forced_tile, error)) return s;
+    if (int32_t s = check_u32(a[argc - 1], "splits", &forced_splits, error)) return s;
+  }
   Format format;
-  if (int32_t s = check_type(a[argc - 1], &format, error)) return s;
+  if (int32_t s = check_type(a[argc - 1 - tail], &format, error)) return s;
   if (int32_t s = check_matrix(a[0], "x", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT16, error)) return s;
   const int64_t m = a[0].buffer.shape[0], k = a[0].buffer.shape[1];
   if (k % format.qk) return fail(error, TENSOR_ERROR_ARGUMENT, "x: K is not a multiple of the block size");
@@ -416,14 +423,14 @@ int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has
     group.n[i] = (int)w.buffer.shape[0];
   }
   group.count = count;
-  group.type = (int)a[argc - 1].scalar;
+  group.type = (int)a[argc - 1 - tail].scalar;
   group.m = (int)m;
   group.k = (int)k;
   group.out_half = a[2].dtype == TENSOR_FLOAT16;
   void* workspace = nullptr;
   size_t workspace_bytes = SIZE_MAX;
   if (has_workspace) {
-    const TensorArgumentV1& ws = a[argc - 2];
+    const TensorArgumentV1& ws = a[argc - 2 - tail];
     const TensorBufferV1& b = ws.buffer;
     if (ws.kind != TENSOR_ARG_BUFFER || ws.dtype != TENSOR_UINT8 || b.dtype != TENSOR_UINT8)
       return fail(error, TENSOR_ERROR_ARGUMENT, "workspace: wrong argument kind or dtype");
@@ -434,7 +441,13 @@ int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has
     workspace = reinterpret_cast<void*>(b.address);
     workspace_bytes = (size_t)b.shape[0];
   }
-  const tensor_gguf::GemmPlan plan = tensor_gguf::plan_gemm_group(group, workspace_bytes);
+  tensor_gguf::GemmPlan plan = tensor_gguf::plan_gemm_group(group, workspace_bytes);
+  if (forced) {
+    plan = tensor_gguf::GemmPlan{(int)forced_tile, (int)forced_splits, true};
+    if (forced_tile > 64 || forced_splits > 64 || !tensor_gguf::gemm_group_pipelined(group, plan))
+      return fail(error, TENSOR_ERROR_ARGUMENT, "tile %u with %u splits does not fit this shape",
+                  (unsigned)forced_tile, (unsigned)forced_splits);
+  }
   const size_t need = tensor_gguf::gemm_group_workspace(group, plan);
   if (need > workspace_bytes)
     return fail(error, TENSOR_ERROR_ARGUMENT, "workspace: the plan needs %zu bytes, %zu available", need,
@@ -512,25 +525,76 @@ int32_t tensor_gguf_gemm_group_noalloc_v1(const TensorCallV1* call, TensorErrorV
   return gemm_group_call(call, error, false);
 }
 
-int32_t tensor_gguf_gemm_workspace_v1(uint32_t type, int64_t m, int64_t k, const int64_t* n, uint32_t count,
-                                      uint64_t* bytes, TensorErrorV1* error) {
+int32_t tensor_gguf_gemm_group_plan_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  return gemm_group_call(call, error, true, true);
+}
+
+int32_t tensor_gguf_gemm_tile_v1(int32_t tile, int32_t* bm, int32_t* bn, int32_t* ks, TensorErrorV1* error) {
+  if (!bm || !bn || !ks || !tensor_gguf::gemm_tile_geometry(tile, bm, bn, ks))
+    return fail(error, TENSOR_ERROR_ARGUMENT, "no pipelined GEMM tile %d", (int)tile);
+  return ok(error);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The group a workspace or plan query describes, checked like a call's shapes.
+int32_t query_group(uint32_t type, int64_t m, int64_t k, const int64_t* n, uint32_t count,
+                    tensor_gguf::GemmGroupArgs* group, TensorErrorV1* error) {
   Format format;
-  if (!bytes || !n || count < 1 || count > (uint32_t)tensor_gguf::kGemmGroupMax)
+  if (!n || count < 1 || count > (uint32_t)tensor_gguf::kGemmGroupMax)
     return fail(error, TENSOR_ERROR_ARGUMENT, "invalid workspace query");
   if (!ggml_format(type, &format))
     return fail(error, TENSOR_ERROR_ARGUMENT, "type: unsupported GGML type %u", type);
   if (m < 1 || k < 1 || k % format.qk || m >= (int64_t)1 << 31 || k >= (int64_t)1 << 31)
     return fail(error, TENSOR_ERROR_ARGUMENT, "m, k: must be positive int32 with k a multiple of %d", format.qk);
-  tensor_gguf::GemmGroupArgs group{};
+  *group = tensor_gguf::GemmGroupArgs{};
   for (uint32_t i = 0; i < count; ++i) {
     if (n[i] < 1 || n[i] >= (int64_t)1 << 31) return fail(error, TENSOR_ERROR_ARGUMENT, "n%u: must be a positive int32", i);
-    group.n[i] = (int)n[i];
+    group->n[i] = (int)n[i];
   }
-  group.count = (int)count;
-  group.type = (int)type;
-  group.m = (int)m;
-  group.k = (int)k;
+  group->count = (int)count;
+  group->type = (int)type;
+  group->m = (int)m;
+  group->k = (int)k;
+  group->out_half = true;
+  return TENSOR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t tensor_gguf_gemm_workspace_v1(uint32_t type, int64_t m, int64_t k, const int64_t* n, uint32_t count,
+                                      uint64_t* bytes, TensorErrorV1* error) {
+  tensor_gguf::GemmGroupArgs group;
+  if (!bytes) return fail(error, TENSOR_ERROR_ARGUMENT, "invalid workspace query");
+  if (int32_t s = query_group(type, m, k, n, count, &group, error)) return s;
   *bytes = tensor_gguf::gemm_group_workspace(group, tensor_gguf::plan_gemm_group(group, SIZE_MAX));
+  return ok(error);
+}
+
+int32_t tensor_gguf_gemm_plan_v1(uint32_t type, int64_t m, int64_t k, const int64_t* n, uint32_t count,
+                                 uint64_t workspace_bytes, int32_t* tile, int32_t* splits, int32_t* pipelined,
+                                 TensorErrorV1* error) {
+  tensor_gguf::GemmGroupArgs group;
+  if (!tile || !splits || !pipelined) return fail(error, TENSOR_ERROR_ARGUMENT, "invalid plan query");
+  if (int32_t s = query_group(type, m, k, n, count, &group, error)) return s;
+  const tensor_gguf::GemmPlan plan = tensor_gguf::plan_gemm_group(group, (size_t)workspace_bytes);
+  bool small = true;  // every matrix on the small-M kernel, as the grouped entry decides
+  for (int i = 0; i < group.count; ++i) {
+    tensor_gguf::GemvArgs one{};
+    one.type = group.type;
+    one.m = group.m;
+    one.n = group.n[i];
+    one.k = group.k;
+    one.out_half = true;
+    small = small && tensor_gguf::gemm_small_m(one);
+  }
+  *tile = plan.tile;
+  *splits = plan.splits;
+  *pipelined = (!small || plan.small_m) && tensor_gguf::gemm_group_pipelined(group, plan);
   return ok(error);
 }
 

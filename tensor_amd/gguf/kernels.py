@@ -27,6 +27,7 @@ ENTRYPOINTS = {
     "gguf_gemv_group": "tensor_gguf_gemv_group_v1",
     "gguf_gemm_group": "tensor_gguf_gemm_group_v1",
     "gguf_gemm_group_noalloc": "tensor_gguf_gemm_group_noalloc_v1",
+    "gguf_gemm_group_plan": "tensor_gguf_gemm_group_plan_v1",
     "gguf_gemv_swiglu": "tensor_gguf_gemv_swiglu_v1",
     "gguf_dequant": "tensor_gguf_dequant_v1",
 }
@@ -44,12 +45,12 @@ def _symbols(kernel: str, count: int | None) -> tuple:
         return ("N", "K")
     if kernel in ("gguf_gemv_group", "gguf_gemm_group_noalloc"):
         return ("M", "K", *(f"N{i}" for i in range(count)))
-    if kernel == "gguf_gemm_group":
+    if kernel in ("gguf_gemm_group", "gguf_gemm_group_plan"):
         return ("M", "K", *(f"N{i}" for i in range(count)), "W")
     return ("M", "N", "K")
 
 
-GROUPS = ("gguf_gemv_group", "gguf_gemm_group", "gguf_gemm_group_noalloc")
+GROUPS = ("gguf_gemv_group", "gguf_gemm_group", "gguf_gemm_group_noalloc", "gguf_gemm_group_plan")
 
 
 def packed_manifest(encoding, m: int, n: int, k: int, *, x_dtype: str = "float32",
@@ -111,7 +112,9 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
     counts ``N0, N1, ...``; ``gguf_gemm_group`` (the prefill GEMM of such a group,
     any M) adds a ``workspace`` uint8 buffer before ``type`` (its size
     ``Device.gemm_workspace`` tells); ``gguf_gemm_group_noalloc`` is the same GEMM
-    without it, on the library's static scratch; every other kernel takes no ``count``.
+    without it, on the library's static scratch; ``gguf_gemm_group_plan`` is ``gguf_gemm_group``
+    with two more scalars, ``tile`` and ``splits``, naming the plan it runs (plan sweeps: see
+    ``Device.gemm_plan``); every other kernel takes no ``count``.
     ``gguf_gemv_swiglu`` takes ``[x, w_gate, w_up, out, type]`` and stores
     silu(x W_gate^T) * (x W_up^T).
     """
@@ -141,9 +144,12 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
         for i in range(count):
             arguments.append({"name": f"w{i}", "dtype": "uint8", "shape": [{"var": f"N{i}"}, _row_bytes(code)], "alignment": 16})
             arguments.append({"name": f"out{i}", "dtype": out_dtype, "shape": [{"var": "M"}, {"var": f"N{i}"}], "alignment": 16})
-        if kernel == "gguf_gemm_group":
+        if kernel in ("gguf_gemm_group", "gguf_gemm_group_plan"):
             arguments.append({"name": "workspace", "dtype": "uint8", "shape": [{"var": "W"}], "alignment": 256})
         arguments.append(type_argument)
+        if kernel == "gguf_gemm_group_plan":  # the plan, supplied per call
+            arguments += [{"name": "tile", "dtype": "uint32", "kind": "scalar"},
+                          {"name": "splits", "dtype": "uint32", "kind": "scalar"}]
     elif kernel == "gguf_gemv_swiglu":
         arguments = [
             {"name": "x", "dtype": "float16", "shape": [{"var": "M"}, {"var": "K"}], "alignment": 16},

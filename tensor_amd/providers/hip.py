@@ -27,6 +27,18 @@ from tensor_amd.runtime.event import Event
 from tensor_amd.runtime.executable import Executable
 from tensor_amd.runtime.session import Session
 
+def gemm_tiles() -> list:
+    """Every tile of the pipelined prefill GEMM, by index: {"bm", "bn", "ks"}."""
+    tiles = []
+    while True:
+        bm, bn, ks = c.c_int32(), c.c_int32(), c.c_int32()
+        error = ErrorDescriptor()
+        if _native.library().tensor_gguf_gemm_tile_v1(len(tiles), c.byref(bm), c.byref(bn), c.byref(ks),
+                                                       c.byref(error)):
+            return tiles
+        tiles.append({"bm": bm.value, "bn": bn.value, "ks": ks.value})
+
+
 # The device this library last made current on each thread (HIP's current device is per thread).
 # Launches consult it instead of setting the device again; an entry point that finds another
 # current device (set by other code on the thread) refuses the call before enqueuing anything,
@@ -410,6 +422,20 @@ class Device(Session):
         _native.call("tensor_gguf_gemm_workspace_v1", ggml_type(encoding), int(m), int(k),
                      (c.c_int64 * len(rows))(*rows), len(rows), c.byref(result))
         return result.value
+
+    def gemm_plan(self, encoding, m: int, k: int, rows, workspace_bytes: int | None = None) -> dict:
+        """The plan ``gguf_gemm_group`` takes for this shape (``workspace_bytes`` of workspace,
+        by default as much as it asks for): tile index, its geometry, the K split, and whether
+        the pipelined kernel runs (otherwise each matrix takes the small-M kernel)."""
+        from tensor_amd.gguf.quant import ggml_type
+
+        rows = [int(n) for n in rows]
+        if workspace_bytes is None:
+            workspace_bytes = self.gemm_workspace(encoding, m, k, rows)
+        tile, splits, pipelined = c.c_int32(), c.c_int32(), c.c_int32()
+        _native.call("tensor_gguf_gemm_plan_v1", ggml_type(encoding), int(m), int(k), (c.c_int64 * len(rows))(*rows),
+                     len(rows), int(workspace_bytes), c.byref(tile), c.byref(splits), c.byref(pipelined))
+        return dict(gemm_tiles()[tile.value], tile=tile.value, splits=splits.value, pipelined=bool(pipelined.value))
 
     def graph(self, callback, *, resources=()):
         """Capture the launches ``callback()`` enqueues into a replayable graph.  The buffers of

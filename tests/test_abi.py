@@ -516,3 +516,70 @@ def test_gemm_group_noalloc_takes_the_group_without_a_workspace():
     assert call.run(noalloc) == (ERR_ARG, "out1: shape, stride, size or dtype mismatch")
     call.call.argument_count = 5
     assert call.run(noalloc)[0] == ERR_ARG
+
+
+def test_gemm_plan_query_names_the_library_plans_at_the_baseline_shapes():
+    """The plans the grouped prefill GEMM takes at C4 and C5 (CPU only: a query, no launch)."""
+    from tensor_amd.providers.hip import gemm_tiles
+
+    tiles = gemm_tiles()
+    assert tiles[0] == {"bm": 256, "bn": 128, "ks": 1} and tiles[8] == {"bm": 256, "bn": 96, "ks": 1}
+    lib = _native.library()
+
+    def plan(code, m, k, rows, workspace=1 << 30):
+        tile, splits, pipelined = c.c_int32(), c.c_int32(), c.c_int32()
+        error = abi.ErrorDescriptor()
+        status = lib.tensor_gguf_gemm_plan_v1(code, m, k, (c.c_int64 * len(rows))(*rows), len(rows), workspace,
+                                              c.byref(tile), c.byref(splits), c.byref(pipelined), c.byref(error))
+        assert status == OK, error.message
+        return tile.value, splits.value, bool(pipelined.value)
+
+    assert plan(12, 512, 4096, [12288]) == (8, 1, True)            # C4 M=512: 256 x 96, one round
+    assert plan(12, 2048, 4096, [12288]) == (0, 1, True)           # C4 M=2048: 256 x 128
+    assert plan(12, 256, 4096, [4096, 1024, 1024]) == (0, 4, True)  # C5 q + k + v, K split 4 ways
+    assert plan(12, 256, 4096, [4096]) == (7, 1, True)             # C5 o: 64 x 64, K over 4 wave groups
+    assert plan(12, 256, 4096, [12288, 12288]) == (8, 1, True)     # C5 gate + up
+    assert plan(14, 256, 12288, [4096]) == (0, 8, True)            # C5 down (Q6_K), K split 8 ways
+    assert plan(14, 256, 12288, [4096], workspace=0) == (7, 1, True)  # no workspace: no split
+    error = abi.ErrorDescriptor()
+    assert lib.tensor_gguf_gemm_tile_v1(len(tiles), c.byref(c.c_int32()), c.byref(c.c_int32()),
+                                        c.byref(c.c_int32()), c.byref(error)) == ERR_ARG
+
+
+def test_gemm_forced_plan_refuses_a_plan_that_does_not_fit():
+    """tensor_gguf_gemm_group_plan_v1 checks the named tile and split against the shape before any
+    HIP call (fake device addresses; CPU only)."""
+    from tensor_amd.gguf import kernels as gguf_kernels
+
+    manifest = gguf_kernels.manifest("gguf_gemm_group_plan", "q4_k", "float16", count=1)
+    names = [a["name"] for a in manifest["arguments"]]
+    assert names == ["x", "w0", "out0", "workspace", "type", "tile", "splits"]
+    m, n, k = 256, 4096, 4096
+    shapes = {"x": (m, k), "w0": (n, k // 256 * 144), "out0": (m, n), "workspace": (1 << 20,)}
+    dtypes = {"x": 10, "w0": 3, "out0": 10, "workspace": 3}
+    sizes = {"x": 2, "w0": 1, "out0": 2, "workspace": 1}
+
+    def call_with(tile, splits):
+        keep, args = [], (abi.Argument * 7)()
+        for j, name in enumerate(names[:4]):
+            shape = shapes[name]
+            strides = [sizes[name]] * len(shape)
+            for axis in range(len(shape) - 2, -1, -1):
+                strides[axis] = strides[axis + 1] * shape[axis + 1]
+            arrays = ((c.c_int64 * len(shape))(*shape), (c.c_int64 * len(shape))(*strides))
+            keep.append(arrays)
+            args[j].kind, args[j].dtype = 1, dtypes[name]
+            args[j].buffer = abi.BufferDescriptor(0x10000 * (j + 1), int(np.prod(shape)) * sizes[name], arrays[0],
+                                                  arrays[1], len(shape), dtypes[name], 10, 0)
+        for j, value in ((4, 12), (5, tile), (6, splits)):
+            args[j].kind, args[j].dtype, args[j].scalar = 2, 7, value
+        call = abi.CallDescriptor(1, 72, args, 7, 0, (c.c_uint32 * 3)(1, 1, 1), (c.c_uint32 * 3)(256, 1, 1), 0,
+                                  abi.StreamDescriptor(10, 0, 0))
+        error = abi.ErrorDescriptor()
+        status = _native.kernel("tensor_gguf_gemm_group_plan_v1")(c.byref(call), c.byref(error))
+        return status, error.message.decode()
+
+    assert call_with(99, 1)[0] == ERR_ARG          # no such tile
+    assert call_with(0, 3)[0] == ERR_ARG           # 64 K steps do not split 3 ways
+    status, message = call_with(0, 8)              # 8 x 256 x 4096 x 4 B of partials > 1 MiB
+    assert status == ERR_ARG and "workspace" in message

@@ -916,3 +916,43 @@ def test_gemm_group_with_a_short_workspace_splits_less(hip_device, c_oracle):
         got, need = run_gemm_group(hip_device, "q6_k", x, raws, "float32", workspace_bytes=size)
         assert need > size
         assert R.relative_l2(got[0], expected) <= 1e-5
+
+
+@pytest.mark.parametrize("encoding", ["q4_k", "q6_k", "q8_0", "q4_0"])
+def test_gemm_every_plan_through_the_plan_entry(hip_device, c_oracle, encoding):
+    """Every tile and K split the plan-naming entry accepts at a ragged grouped shape (two
+    matrices, fp32 out): each within 1e-5 of the prefill oracle; plans that do not fit are
+    refused with an argument error before any launch."""
+    from tensor_amd._native import HipError
+    from tensor_amd.providers.hip import gemm_tiles
+
+    m, k, rows = 300, 1024, (2000, 1000)
+    code = Q.ggml_type(encoding)
+    note("gemm-plans", encoding, m, k, rows)
+    raws = [cases.weight(n, k, encoding, 1300 + i) for i, n in enumerate(rows)]
+    x = cases.activation(m, k, 1310)
+    c_oracle.set_threads(16)
+    expected = [c_oracle.linear(x, raw, code, n, k, prefill=True) for raw, n in zip(raws, rows)]
+    exe = hip_device.load("gguf_gemm_group_plan", encoding=encoding, out_dtype="float32", count=2)
+    xb = hip_device.from_numpy(x)
+    wbs = [hip_device.from_numpy(raw) for raw in raws]
+    outs = [hip_device.empty((m, n), "float32") for n in rows]
+    workspace = hip_device.empty((4 * m * sum(rows) * 4,), "uint8")
+    ran = 0
+    for tile in range(len(gemm_tiles())):
+        for splits in (1, 2, 4):
+            for out in outs:
+                hip_device.fill_bytes(out, 0xFF)
+            try:
+                exe.launch(xb, wbs[0], outs[0], wbs[1], outs[1], workspace, tile=tile, splits=splits)
+            except HipError as exc:
+                assert exc.code == 2, (tile, splits, exc)
+                continue
+            ran += 1
+            for i, out in enumerate(outs):
+                got = out.to_numpy()
+                assert not np.isnan(got).any(), (tile, splits, i)
+                assert R.relative_l2(got, expected[i]) <= 1e-5, (tile, splits, i)
+    assert ran >= 12, ran
+    for b in [xb, *wbs, *outs, workspace]:
+        b.release()

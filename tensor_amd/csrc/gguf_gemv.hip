@@ -460,6 +460,110 @@ static bool launch_q32_m1(const GemvArgs& a, hipStream_t stream) {
   }
 }
 
+// fp32 activations at M = 1 (the packed call form), Q8_0 and Q4_0, K a multiple of 2048:
+// gemv_q32_m1's lane plan and loads (lane = 32-element block, one row per wave), each code
+// converted to fp32 and multiplied by the fp32 activation (the reference's decode numerics, fp32
+// operands, benchmark.py:466-472, up to summation order); the code bias (128 for the int8 codes
+// read as unsigned bytes, 8 for the nibbles) taken off with the block's fp32 sum of x, d once
+// per block.  x sits in LDS as fp32 chunks of 4, 16 bytes of padding per 128-byte block.
+template <int TYPE, int WAVES, int STEPS, typename OutT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q32_m1_f32(const float* __restrict__ x, const uint8_t* __restrict__ w,
+                                                              OutT* __restrict__ out, int n_rows) {
+  constexpr int kBytes = TYPE == kQ8_0 ? 34 : 18;
+  constexpr float kBias = TYPE == kQ8_0 ? 128.0f : 8.0f;
+  constexpr int T = WAVES * 64, K = 2048 * STEPS, BLOCKS = K / 32, CHUNKS = K / 4;
+  constexpr int XC = (CHUNKS + T - 1) / T;
+  __shared__ __attribute__((aligned(16))) float xl[CHUNKS * 4 + BLOCKS * 4];
+  __shared__ float sxl[BLOCKS];
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  const uint8_t* const wr = w + (size_t)min(row, n_rows - 1) * (size_t)(BLOCKS * kBytes);
+  uint4 xr[XC];
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    if (CHUNKS % T == 0 || c < CHUNKS) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * c);
+  }
+  uint32_t head[STEPS];
+  uint4 q0[STEPS], q1[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const uint8_t* block = wr + (lane + 64 * s) * kBytes;
+    head[s] = load4(block);
+    q0[s] = load16(block + 2);
+    if constexpr (TYPE == kQ8_0) q1[s] = load16(block + 18);
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    if (CHUNKS % T == 0 || c < CHUNKS) {
+      const uint4 v = xr[i];
+      *reinterpret_cast<uint4*>(&xl[4 * c + 4 * (c >> 3)]) = v;
+      // a block is 8 consecutive chunks, held by 8 consecutive lanes (CHUNKS is a multiple of 8)
+      const float part = (__uint_as_float(v.x) + __uint_as_float(v.y)) + (__uint_as_float(v.z) + __uint_as_float(v.w));
+      const float sum = dpp_add<0x141>(quad_sum(part));
+      if ((c & 7) == 0) sxl[c >> 3] = sum;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  if (row >= n_rows) return;
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int b = lane + 64 * s;
+    const float* xp = &xl[36 * b];  // the block's 8 chunks (32 floats and 4 of padding per block)
+    float a = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      uint32_t codes;
+      int e;  // first element of the four codes
+      if constexpr (TYPE == kQ8_0) {
+        codes = word(u < 4 ? q0[s] : q1[s], u & 3) ^ 0x80808080u;  // q + 128 as unsigned bytes
+        e = 4 * u;
+      } else {
+        // byte j's low nibble is element j, its high nibble element j + 16
+        codes = (word(q0[s], u & 3) >> (4 * (u >> 2))) & 0x0F0F0F0Fu;
+        e = 4 * (u & 3) + 16 * (u >> 2);
+      }
+      const float4 xv = *reinterpret_cast<const float4*>(xp + e);
+      a = fmaf((float)(codes & 0xFF), xv.x, a);
+      a = fmaf((float)((codes >> 8) & 0xFF), xv.y, a);
+      a = fmaf((float)((codes >> 16) & 0xFF), xv.z, a);
+      a = fmaf((float)(codes >> 24), xv.w, a);
+    }
+    acc = fmaf(half_bits_to_float(head[s]), a - kBias * sxl[b], acc);
+  }
+  const float v = wave_sum(acc);
+  if (lane == 0) store_out<OutT>(out, (size_t)row, v);
+}
+
+template <int TYPE, int STEPS, typename OutT>
+static void launch_q32_m1_f32_steps(const GemvArgs& a, hipStream_t stream) {
+  constexpr int WAVES = STEPS <= 2 ? 8 : 4;
+  hipLaunchKernelGGL((gemv_q32_m1_f32<TYPE, WAVES, STEPS, OutT>), dim3((a.n + WAVES - 1) / WAVES), dim3(WAVES * 64),
+                     0, stream, static_cast<const float*>(a.x), static_cast<const uint8_t*>(a.w),
+                     static_cast<OutT*>(a.out), a.n);
+}
+
+template <int TYPE, typename OutT>
+static bool launch_q32_m1_f32(const GemvArgs& a, hipStream_t stream) {
+  if (a.m != 1 || a.k % 2048) return false;
+  switch (a.k / 2048) {
+    case 1: launch_q32_m1_f32_steps<TYPE, 1, OutT>(a, stream); return true;
+    case 2: launch_q32_m1_f32_steps<TYPE, 2, OutT>(a, stream); return true;
+    case 3: launch_q32_m1_f32_steps<TYPE, 3, OutT>(a, stream); return true;
+    case 4: launch_q32_m1_f32_steps<TYPE, 4, OutT>(a, stream); return true;
+    case 5: launch_q32_m1_f32_steps<TYPE, 5, OutT>(a, stream); return true;
+    case 6: launch_q32_m1_f32_steps<TYPE, 6, OutT>(a, stream); return true;
+    case 7: launch_q32_m1_f32_steps<TYPE, 7, OutT>(a, stream); return true;
+    case 8: launch_q32_m1_f32_steps<TYPE, 8, OutT>(a, stream); return true;
+    default: return false;
+  }
+}
+
 // ------------------------------------------------------ other encodings ---
 // Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K: each lane decodes 16-element groups with the
 // dequantizer's arithmetic (decode8, twice) and accumulates their products with the
@@ -596,6 +700,17 @@ static hipError_t launch_f32x(const GemvArgs& a, hipStream_t stream) {
 
 hipError_t launch_gemv_f32x(const GemvArgs& a, hipStream_t stream) {
   if (a.m != 1) return hipErrorInvalidValue;
+  bool handled = false;
+  hipError_t status = launch_gemv_q4k_f32x(a, stream, &handled);
+  if (handled) return status;
+  status = launch_gemv_q6k_f32x(a, stream, &handled);
+  if (handled) return status;
+  if (a.type == kQ8_0 || a.type == kQ4_0) {
+    const bool q8 = a.type == kQ8_0;
+    if (a.out_half ? (q8 ? launch_q32_m1_f32<kQ8_0, _Float16>(a, stream) : launch_q32_m1_f32<kQ4_0, _Float16>(a, stream))
+                   : (q8 ? launch_q32_m1_f32<kQ8_0, float>(a, stream) : launch_q32_m1_f32<kQ4_0, float>(a, stream)))
+      return hipGetLastError();
+  }
   return a.out_half ? launch_f32x<_Float16>(a, stream) : launch_f32x<float>(a, stream);
 }
 

@@ -239,6 +239,126 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1(const _Float16* __rest
   }
 }
 
+// ------------------------------------------------------ M = 1, fp32 x ---
+
+// fp32 activations at M = 1 (the showcase's packed call form, benchmark.py:460-464): the lane
+// plan and loads of gemv_q4k_m1 (one row per wave, lane = super-block slot x quant pair j, x
+// staged once per workgroup), with each 4-bit code converted to fp32 and multiplied by the fp32
+// activation, so the products are the reference's decode numerics (fp32 operands,
+// benchmark.py:466-472) up to summation order: d * sc once per sub-block, dmin * m with the
+// sub-block's fp32 sum of x.  x sits in LDS as fp32 chunks of 4 with 16 bytes of padding per
+// 256, so the sixteen (slot, j) start offsets of one b128 read fall in distinct banks.
+__device__ __forceinline__ int f32_chunk(int c) { return 4 * c + 4 * (c >> 4); }
+
+template <int STEPS, int WAVES, typename OutT, int TYPE>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q4k_m1_f32(const float* __restrict__ x, const uint8_t* __restrict__ w,
+                                                              OutT* __restrict__ out, int n_rows) {
+  constexpr bool Q5 = TYPE == kQ5_K;
+  constexpr int BLOCK = Q5 ? 176 : 144, QOFF = Q5 ? 48 : 16, SB = 16 * BLOCK;  // SB: one 4096-column step
+  constexpr int K = STEPS * 4096, ROW_BYTES = STEPS * SB, T = WAVES * 64;
+  constexpr int XC = K / 4 / T;  // 16-byte x chunks (4 floats) per thread
+  static_assert(XC * T * 4 == K, "every thread stages whole chunks");
+  __shared__ __attribute__((aligned(16))) float xlds[K + K / 16];
+  __shared__ float sxl[K / 32];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  uint4 xr[XC];
+#pragma unroll
+  for (int i = 0; i < XC; ++i) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * (threadIdx.x + i * T));
+  const int row = blockIdx.x * WAVES + wv, slot = lane >> 2, j = lane & 3;
+  const uint8_t* wl = w + (size_t)min(row, n_rows - 1) * ROW_BYTES + slot * BLOCK;
+  const uint8_t* wq = wl + 32 * j;
+  uint4 hd[STEPS], q0[STEPS], q1[STEPS];
+  uint4 h0[Q5 ? STEPS : 1], h1[Q5 ? STEPS : 1];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    hd[s] = load16(wl + s * SB);
+    q0[s] = load16(wq + s * SB + QOFF);
+    q1[s] = load16(wq + s * SB + QOFF + 16);
+    if constexpr (Q5) {
+      h0[s] = load16(wl + s * SB + 16);
+      h1[s] = load16(wl + s * SB + 32);
+    }
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    const uint4 v = xr[i];
+    *reinterpret_cast<uint4*>(&xlds[f32_chunk(c)]) = v;
+    // a sub-block is 8 consecutive chunks, held by 8 consecutive lanes: their sum in all 8
+    const float part = (__uint_as_float(v.x) + __uint_as_float(v.y)) + (__uint_as_float(v.z) + __uint_as_float(v.w));
+    const float sum = dpp_add<0x141>(quad_sum(part));
+    if ((c & 7) == 0) sxl[c >> 3] = sum;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  if (row >= n_rows) return;
+
+  const PairSelect sel(j);
+  float total = 0.f;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int sub = (s * 16 + slot) * 8 + 2 * j;  // sub-block 2j of the super-block
+    const float2 sx = *reinterpret_cast<const float2*>(&sxl[sub]);
+    float acc2[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c0 = 8 * (sub + h);  // first x chunk of sub-block 2j + h
+      float a = 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        uint32_t codes = (word(u < 4 ? q0[s] : q1[s], u & 3) >> (4 * h)) & 0x0F0F0F0Fu;
+        if constexpr (Q5) codes |= ((word(u < 4 ? h0[s] : h1[s], u & 3) >> (2 * j + h)) & 0x01010101u) << 4;
+        const float4 xv = *reinterpret_cast<const float4*>(&xlds[f32_chunk(c0 + u)]);
+        a = fmaf((float)(codes & 0xFF), xv.x, a);
+        a = fmaf((float)((codes >> 8) & 0xFF), xv.y, a);
+        a = fmaf((float)((codes >> 16) & 0xFF), xv.z, a);
+        a = fmaf((float)(codes >> 24), xv.w, a);
+      }
+      acc2[h] = a;
+    }
+    uint32_t scs, mns;
+    sel.codes(hd[s], scs, mns);
+    const float dd = half_bits_to_float(hd[s].x), dmin = half_bits_to_float(hd[s].x >> 16);
+    total = fmaf(dd * (float)(scs & 0xFF), acc2[0], total);
+    total = fmaf(dd * (float)(scs >> 8), acc2[1], total);
+    total = fmaf(-dmin * (float)(mns & 0xFF), sx.x, total);
+    total = fmaf(-dmin * (float)(mns >> 8), sx.y, total);
+  }
+  const float v = wave_sum(total);
+  if (lane == 0) store_out<OutT>(out, (size_t)row, v);
+}
+
+template <int STEPS, typename OutT, int TYPE>
+static void launch_m1_f32_steps(const GemvArgs& a, hipStream_t stream) {
+  constexpr int WAVES = 8;
+  hipLaunchKernelGGL((gemv_q4k_m1_f32<STEPS, WAVES, OutT, TYPE>), dim3((a.n + WAVES - 1) / WAVES), dim3(WAVES * 64),
+                     0, stream, static_cast<const float*>(a.x), static_cast<const uint8_t*>(a.w),
+                     static_cast<OutT*>(a.out), a.n);
+}
+
+template <typename OutT, int TYPE>
+static hipError_t launch_m1_f32(const GemvArgs& a, hipStream_t stream) {
+  switch (a.k / 4096) {
+    case 1: launch_m1_f32_steps<1, OutT, TYPE>(a, stream); break;
+    case 2: launch_m1_f32_steps<2, OutT, TYPE>(a, stream); break;
+    case 3: launch_m1_f32_steps<3, OutT, TYPE>(a, stream); break;
+    case 4: launch_m1_f32_steps<4, OutT, TYPE>(a, stream); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// Q4_K and Q5_K with fp32 x at M = 1, K a multiple of 4096 up to 16384.
+hipError_t launch_gemv_q4k_f32x(const GemvArgs& a, hipStream_t stream, bool* handled) {
+  *handled = (a.type == kQ4_K || a.type == kQ5_K) && a.x_f32 && gemv_q4k_group_supported(a.m, a.k, a.n);
+  if (!*handled) return hipSuccess;
+  if (a.type == kQ5_K)
+    return a.out_half ? launch_m1_f32<_Float16, kQ5_K>(a, stream) : launch_m1_f32<float, kQ5_K>(a, stream);
+  return a.out_half ? launch_m1_f32<_Float16, kQ4_K>(a, stream) : launch_m1_f32<float, kQ4_K>(a, stream);
+}
+
 // ------------------------------------------------------- 2 <= M, MFMA ---
 
 __device__ __forceinline__ uint32_t pk_fma(uint32_t a, uint32_t b, uint32_t c) {

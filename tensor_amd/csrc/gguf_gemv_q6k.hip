@@ -129,6 +129,115 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __res
   }
 }
 
+// fp32 activations at M = 1 (the packed call form): gemv_q6k_lds's lane plan and loads, each
+// six-bit code converted to fp32 and multiplied by the fp32 activation (the reference's decode
+// numerics, fp32 operands, benchmark.py:466-472, up to summation order), d * scale and the bias
+// 32 applied once per 16-element run with the run's fp32 sum of x.  x sits in LDS as 16-byte
+// chunks of 4 floats, chunk c at a swizzled position: the lanes of one b128 read (slot s, part p)
+// read chunks 64 s + 32 (p >> 1) + 4 (p & 1) + 8 run + u, which differ only in bits 2, 5, 6 and
+// 7; XOR-ing bits 5-7 into bits 0-3 spreads 16 of them over all 64 banks.
+__device__ __forceinline__ int q6k_f32_chunk(int c) { return 4 * (c ^ ((((c >> 5) & 1) << 3) | ((c >> 6) & 3))); }
+
+template <int STEPS, int WAVES, typename OutT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q6k_f32(const float* __restrict__ x, const uint8_t* __restrict__ w,
+                                                           OutT* __restrict__ out, int n_rows) {
+  constexpr int K = STEPS * 4096, ROW_BYTES = STEPS * 16 * 210, T = WAVES * 64, XC = K / 4 / T;
+  static_assert(XC * T * 4 == K, "every thread stages whole chunks");
+  __shared__ __attribute__((aligned(16))) float xlds[K];
+  __shared__ __attribute__((aligned(16))) float sxl[K / 16];  // run sums, in run_slot order
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  const int slot = lane >> 2, part = lane & 3, hh = part >> 1, l0 = 16 * (part & 1);
+  uint4 xr[XC];
+#pragma unroll
+  for (int i = 0; i < XC; ++i) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * (threadIdx.x + i * T));
+  uint4 qa[STEPS], qb[STEPS], qh[STEPS];
+  uint2 sc8[STEPS];
+  uint32_t dw[STEPS];
+  const uint8_t* wr = w + (size_t)min(row, n_rows - 1) * ROW_BYTES + slot * 210;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const uint8_t* block = wr + s * 16 * 210;
+    qa[s] = load16(block + 64 * hh + l0);
+    qb[s] = load16(block + 64 * hh + 32 + l0);
+    qh[s] = load16(block + 128 + 32 * hh + l0);
+    sc8[s] = load8(block + 192 + 8 * hh);
+    dw[s] = load4(block + 206);  // high half: d
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    const uint4 v = xr[i];
+    *reinterpret_cast<uint4*>(&xlds[q6k_f32_chunk(c)]) = v;
+    // a 16-element run is 4 consecutive chunks, held by one quad of lanes
+    const float sum = quad_sum((__uint_as_float(v.x) + __uint_as_float(v.y)) + (__uint_as_float(v.z) + __uint_as_float(v.w)));
+    if ((c & 3) == 0) sxl[run_slot(c >> 2)] = sum;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  if (row >= n_rows) return;
+  float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const float4 s4 = *reinterpret_cast<const float4*>(&sxl[(s * 16 + slot) * 16 + 8 * hh + 4 * (part & 1)]);
+    const float sx[4] = {s4.x, s4.y, s4.z, s4.w};
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t A = word(qa[s], u), B = word(qb[s], u), H = word(qh[s], u);
+      uint32_t q[4];
+      q[0] = (A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u);
+      q[1] = (B & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u);
+      q[2] = ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
+      q[3] = ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        // run c: elements 256 sb + 128 hh + 32 c + l0 + 4 u .. + 3
+        const int chunk = ((s * 16 + slot) * 256 + 128 * hh + 32 * c + l0 + 4 * u) >> 2;
+        const float4 xv = *reinterpret_cast<const float4*>(&xlds[q6k_f32_chunk(chunk)]);
+        a[c] = fmaf((float)(q[c] & 0xFF), xv.x, a[c]);
+        a[c] = fmaf((float)((q[c] >> 8) & 0xFF), xv.y, a[c]);
+        a[c] = fmaf((float)((q[c] >> 16) & 0xFF), xv.z, a[c]);
+        a[c] = fmaf((float)(q[c] >> 24), xv.w, a[c]);
+      }
+    }
+    const float d = half_bits_to_float(dw[s] >> 16);
+    const int p = part & 1;
+    acc = fmaf(d * (float)(int8_t)(sc8[s].x >> (8 * p)), a[0] - 32.0f * sx[0], acc);
+    acc = fmaf(d * (float)(int8_t)(sc8[s].x >> (8 * (2 + p))), a[1] - 32.0f * sx[1], acc);
+    acc = fmaf(d * (float)(int8_t)(sc8[s].y >> (8 * p)), a[2] - 32.0f * sx[2], acc);
+    acc = fmaf(d * (float)(int8_t)(sc8[s].y >> (8 * (2 + p))), a[3] - 32.0f * sx[3], acc);
+  }
+  const float v = wave_sum(acc);
+  if (lane == 0) store_out<OutT>(out, (size_t)row, v);
+}
+
+template <int STEPS, typename OutT>
+static hipError_t launch_q6k_f32(const GemvArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((gemv_q6k_f32<STEPS, 8, OutT>), dim3((a.n + 7) / 8), dim3(512), 0, stream,
+                     static_cast<const float*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out), a.n);
+  return hipGetLastError();
+}
+
+template <typename OutT>
+static hipError_t launch_q6k_f32_typed(const GemvArgs& a, hipStream_t stream, bool* handled) {
+  *handled = true;
+  switch (a.k) {
+    case 4096: return launch_q6k_f32<1, OutT>(a, stream);
+    case 8192: return launch_q6k_f32<2, OutT>(a, stream);
+    case 12288: return launch_q6k_f32<3, OutT>(a, stream);
+    default: *handled = false; return hipSuccess;
+  }
+}
+
+hipError_t launch_gemv_q6k_f32x(const GemvArgs& a, hipStream_t stream, bool* handled) {
+  *handled = false;
+  if (a.m != 1 || a.type != kQ6_K || !a.x_f32) return hipSuccess;
+  return a.out_half ? launch_q6k_f32_typed<_Float16>(a, stream, handled) : launch_q6k_f32_typed<float>(a, stream, handled);
+}
+
 template <int R, int STEPS, int WAVES, typename OutT>
 static hipError_t launch_q6k(const GemvArgs& a, hipStream_t stream) {
   constexpr int per_block = WAVES * R;

@@ -56,6 +56,11 @@ hipError_t launch_gemv_swiglu(const GemvArgs& gate, const void* w_up, hipStream_
 // workgroup, 0 the default) and Q4_K at 2 <= M <= 8 (a gate tile and its up tile per workgroup).
 hipError_t launch_gemv_q4k_swiglu_fast(const GemvArgs& gate, const void* w_up, hipStream_t stream, bool* handled,
                                        int waves = 0);
+// fp32-activation fast path at M = 1 for Q4_K and Q5_K (K a multiple of 4096, at most 16384);
+// *handled is false for the other shapes and encodings.
+hipError_t launch_gemv_q4k_f32x(const GemvArgs& args, hipStream_t stream, bool* handled);
+// The same for Q6_K (K in {4096, 8192, 12288}).
+hipError_t launch_gemv_q6k_f32x(const GemvArgs& args, hipStream_t stream, bool* handled);
 // Q5_K fast path (the M = 1 Q4_K kernel with the fifth bits; K a multiple of 4096, at most 16384).
 hipError_t launch_gemv_q5k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 // Q6_K fast path (LDS-staged x, M = 1, K in {4096, 8192, 12288}).

@@ -843,6 +843,43 @@ def test_packed_form_every_encoding(hip_device, c_oracle, encoding, x_dtype, m):
             assert err <= 1e-5, err
 
 
+@pytest.mark.parametrize("encoding,n,k", [
+    ("q4_k", 1003, 4096),    # the fp32-x M = 1 kernel: one step, ragged last workgroup
+    ("q4_k", 777, 12288),    # three steps (C2's down row length)
+    ("q5_k", 500, 8192),
+    ("q5_k", 100, 16384),    # four steps
+    ("q6_k", 1001, 4096),    # LM-head row length
+    ("q6_k", 300, 12288),
+    ("q8_0", 1003, 4096),    # C1's row length
+    ("q8_0", 257, 12288),
+    ("q4_0", 300, 6144),
+])
+def test_packed_form_fp32_x_at_decode_row_lengths(hip_device, c_oracle, encoding, n, k):
+    """fp32 x at M = 1 on the packed entry at the BASELINE row lengths, where the tuned decode
+    kernels take the fp32 activations themselves: every row within tolerance of the fp32-operand
+    oracle (benchmark.py:466-472), fp32 and fp16 out."""
+    code = Q.ggml_type(encoding)
+    note("packed-f32x", encoding, n, k)
+    x, raw = showcase_inputs(encoding, 1, n, k, 700 + k // 1024)
+    expected = packed_reference(c_oracle, x, raw, code, 1, n, k)
+    for out_dtype in ("float32", "float16"):
+        exe = hip_device.load("gguf_packed", encoding=encoding, m=1, n=n, k=k, out_dtype=out_dtype)
+        xb, wb = hip_device.from_numpy(x), hip_device.from_numpy(raw.reshape(-1))
+        out = hip_device.empty((n,), out_dtype)
+        hip_device.fill_bytes(out, 0xFF)
+        exe.launch(xb, wb, out)
+        got = out.to_numpy().astype(np.float32)
+        for b in (xb, wb, out):
+            b.release()
+        assert not np.isnan(got).any(), out_dtype
+        # fp32 operands: only the summation order differs from the oracle's k-order sums
+        assert R.relative_l2(got, expected) <= (1e-5 if out_dtype == "float32" else TOLERANCE), out_dtype
+        err = np.abs(got - expected)
+        scale = float(np.sqrt(np.mean(expected.astype(np.float64) ** 2)))
+        bound = (1e-4 if out_dtype == "float32" else 2e-3) * scale + (0 if out_dtype == "float32" else 1e-3) * np.abs(expected)
+        assert (err <= bound).all(), (out_dtype, int(np.argmax(err - bound)))
+
+
 # ------------------------------------------------------- grouped prefill --
 
 def run_gemm_group(device, encoding, x, raws, out_dtype, workspace_bytes=None):

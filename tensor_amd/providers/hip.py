@@ -273,8 +273,11 @@ class Device(Session):
         buffer._check()
         _native.call("tensor_hip_fill_u8", buffer.pointer, int(value) & 0xFF, buffer.nbytes, self.stream)
 
-    def _download(self, buffer: Buffer):
-        result = np.empty(buffer.shape, dtype=buffer.dtype)
+    def _download(self, buffer: Buffer) -> np.ndarray:
+        """The buffer's bytes on the host, as an array of its storage dtype (bfloat16, which
+        numpy lacks, as the uint16 bit patterns), after the work queued on this stream."""
+        storage = np.uint16 if str(buffer.dtype) == "bfloat16" else buffer.dtype
+        result = np.empty(buffer.shape, dtype=storage)
         _native.call("tensor_hip_copy_dtoh", result.ctypes.data, buffer.pointer, buffer.nbytes, self.stream)
         return result
 

@@ -273,13 +273,17 @@ class Device(Session):
         buffer._check()
         _native.call("tensor_hip_fill_u8", buffer.pointer, int(value) & 0xFF, buffer.nbytes, self.stream)
 
-    def _download(self, buffer: Buffer) -> np.ndarray:
-        """The buffer's bytes on the host, as an array of its storage dtype (bfloat16, which
-        numpy lacks, as the uint16 bit patterns), after the work queued on this stream."""
-        storage = np.uint16 if str(buffer.dtype) == "bfloat16" else buffer.dtype
-        result = np.empty(buffer.shape, dtype=storage)
+    def _download_storage(self, buffer) -> np.ndarray:
+        """The buffer's bytes on the host as an array of its storage dtype, after the work
+        queued on this stream: the hook the reference's ``Buffer.to_bytes`` calls
+        (src/tensor/runtime/buffer.py:107-112).  This provider's buffers have numpy dtypes (it
+        does not offer ``bfloat16_storage``), so storage and value dtypes coincide."""
+        result = np.empty(buffer.shape, dtype=buffer.dtype)
         _native.call("tensor_hip_copy_dtoh", result.ctypes.data, buffer.pointer, buffer.nbytes, self.stream)
         return result
+
+    def _download(self, buffer: Buffer) -> np.ndarray:
+        return self._download_storage(buffer)
 
     def _copy(self, destination: Buffer, source: Buffer) -> None:
         if destination.pointer != source.pointer:

@@ -341,6 +341,21 @@ def test_gemv_input_families_and_graph_replay(hip_device, encoding):
             b.release()
 
 
+def test_download_hooks_return_the_device_bytes(hip_device):
+    """``_download_storage`` (the hook the reference's ``Buffer.to_bytes`` calls) and
+    ``to_numpy`` / ``to_bytes`` give back the bytes uploaded, for a matrix and a view of it."""
+    note("download-hooks")
+    data = np.arange(3 * 40, dtype=np.float32).reshape(3, 40) * np.float32(-0.75)
+    buffer = hip_device.from_numpy(data)
+    stored = hip_device._download_storage(buffer)
+    assert stored.dtype == np.float32 and stored.shape == (3, 40)
+    assert np.array_equal(stored, data) and buffer.to_bytes() == data.tobytes()
+    raw = hip_device.from_numpy(data.view(np.uint8).reshape(3, 160))
+    assert np.array_equal(raw.view((480,)).to_numpy(), data.view(np.uint8).reshape(480))
+    raw.release()
+    buffer.release()
+
+
 def test_graph_replay_refused_once_a_captured_buffer_is_released(hip_device):
     """A graph records the buffers of every call launched while it was captured (here through
     a lambda, so nothing is passed explicitly) and refuses to replay once one is released."""

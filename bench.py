@@ -853,6 +853,79 @@ def plan_sweep(device, only=None):
     return report
 
 
+GEMV_SWEEP_SHAPES = (("C2_q4k_gemv_m4_12288x4096", 4, 12288, 4096),
+                     ("C2_q4k_gemv_m4_4096x12288", 4, 4096, 12288),
+                     ("C2_q4k_gemv_m8_12288x4096", 8, 12288, 4096),
+                     ("C2_q4k_gemv_m8_4096x12288", 8, 4096, 12288))
+
+
+def gemv_plan_sweep(device, only=None):
+    """Every multi-row plan of the Q4_K decode GEMV (kernel x launch fields) at C2's M=4 and M=8
+    shapes, on rotated weight copies as the details cases run them, timed, then the three
+    fastest re-timed before the winner is named, beside the plan the library picks (the
+    protocol of ``plan_sweep``).  Each candidate's output is checked against the library
+    plan's (rel-L2 <= 2e-3, no NaN) before it is timed."""
+    from oracle import gguf_ref as R
+    from tensor_amd.providers.hip import GEMV_FIELDS, GEMV_KERNELS
+    from tests import gguf_cases as cases
+
+    report = {}
+    for name, m, n, k in GEMV_SWEEP_SHAPES:
+        if only is not None and not name.startswith(only):
+            continue
+        chosen = device.gemv_plan("q4_k", m, k, n)
+        copies = copies_for(weight_bytes("q4_k", n, k))
+        weights = rotated(device, cases.weight(n, k, "q4_k", 1500 + m), copies)
+        x = device.from_numpy(cases.activation(m, k, 1510 + m))
+        out = device.empty((m, n), "float16")
+        exe = device.load("gguf_gemv_variant", encoding="q4_k", out_dtype="float16")
+        work = gemv_bytes("q4_k", m, n, k, 2)
+        device.load("gguf_gemv", encoding="q4_k", out_dtype="float16").launch(x, weights[0], out)
+        expected = out.to_numpy().astype(np.float32)
+        candidates = []
+        for kernel, fields in GEMV_FIELDS.items():
+            for a, b in fields:
+                try:
+                    calls = [exe.bind(x, w, out, kernel=kernel, a=a, b=b) for w in weights]
+                    device.fill_bytes(out, 0xFF)
+                    calls[0].launch()
+                except Exception as exc:  # the entry refuses plans that do not fit the shape
+                    if getattr(exc, "code", None) == 2:
+                        continue
+                    raise
+                got = out.to_numpy().astype(np.float32)
+                ok = not np.isnan(got).any() and R.relative_l2(got, expected) <= 2e-3
+                stats = time_launches(device, [calls[i % copies].launch for i in range(60)], per=60, replays=5)
+                candidates.append({"kernel": kernel, "name": GEMV_KERNELS[kernel], "a": a, "b": b, "valid": bool(ok),
+                                   "median_us": stats["median_us"], "calls": calls})
+        finalists = sorted((c for c in candidates if c["valid"]), key=lambda c: c["median_us"])[:3]
+        library = next(c for c in candidates if (c["kernel"], c["a"], c["b"]) == (chosen["kernel"], chosen["a"], chosen["b"]))
+        for c in {id(c): c for c in [*finalists, library]}.values():
+            c["selection"] = time_launches(device, [c["calls"][i % copies].launch for i in range(200)], per=200,
+                                           replays=7)
+        winner = min(finalists, key=lambda c: c["selection"]["median_us"])
+
+        def public(c):
+            out_ = {key: value for key, value in c.items() if key != "calls"}
+            if "selection" in c:
+                out_["selection"] = {key: c["selection"][key] for key in ("median_us", "min_us", "max_us")}
+                out_["hbm_frac"] = round(work / c["selection"]["median_us"] * 1e-3 / HBM_PEAK_GBS, 4)
+            return out_
+
+        entry = {"m": m, "n": n, "k": k, "bytes": work, "copies": copies, "library_plan": chosen,
+                 "winner": public(winner), "library_us": library["selection"]["median_us"],
+                 "winner_us": winner["selection"]["median_us"],
+                 "library_over_winner": round(library["selection"]["median_us"] / winner["selection"]["median_us"], 4),
+                 "finalists": [public(c) for c in finalists],
+                 "candidates": [public(c) for c in sorted(candidates, key=lambda c: c["median_us"])]}
+        report[name] = entry
+        log("sweep", name, "library", (chosen["name"], chosen["a"], chosen["b"]), entry["library_us"], "us; winner",
+            (winner["name"], winner["a"], winner["b"]), entry["winner_us"], "us")
+        for buffer in [*weights, x, out]:
+            buffer.release()
+    return report
+
+
 # ------------------------------------------------------------------- main --
 
 def main():
@@ -876,8 +949,9 @@ def main():
     parser.add_argument("--warm-seconds", type=float, default=WARM_SECONDS,
                         help="untimed replay before each timed sequence (0: one replay, e.g. for counter runs)")
     parser.add_argument("--sweep", action="store_true",
-                        help="time every tile and K split of the prefill GEMM at the BASELINE shapes, re-time the "
-                             "three fastest, and print the winner beside the library's plan (one JSON line)")
+                        help="time every tile and K split of the prefill GEMM at the BASELINE shapes and every "
+                             "multi-row plan of the Q4_K decode GEMV at C2's M=4 / M=8 shapes, re-time the three "
+                             "fastest, and print the winners beside the library's plans (one JSON line)")
     parser.add_argument("--torch-leg", action="store_true", help=argparse.SUPPRESS)
     args = parser.parse_args()
     if args.gpus != 1:
@@ -899,8 +973,10 @@ def main():
     with device:
         log("device", device.info["name"], device.info["arch_features"], "CUs", device.info["compute_units"])
         if args.sweep:
-            print(json.dumps({"plan_sweep": plan_sweep(device, args.only), "replays": REPLAYS,
-                              "timing": "HIP graph replays, median; finalists re-timed over 7 replays of 60 launches"}))
+            print(json.dumps({"plan_sweep": plan_sweep(device, args.only),
+                              "gemv_plan_sweep": gemv_plan_sweep(device, args.only), "replays": REPLAYS,
+                              "timing": "HIP graph replays, median; GEMM finalists re-timed over 7 replays of 60 "
+                                        "launches, GEMV finalists over 7 replays of 200 launches on rotated weights"}))
             return 0
         if args.calibrate:
             source = device.zeros((256 << 20,), "uint8")

@@ -192,6 +192,27 @@ int32_t tensor_gguf_gemm_tile_v1(int32_t tile, int32_t *bm, int32_t *bn, int32_t
 int32_t tensor_gguf_gemm_group_plan_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 
 /*
+ * The multi-row plan tensor_gguf_gemv_v1 takes for a Q4_K call with 2 <= m <= 8 rows: the kernel
+ * (0 sector-aligned tiles with x staged in LDS, 1 multi-tile with x in LDS, 2 x read per wave)
+ * and its two launch fields (kernel 0: 16-row tiles per workgroup 1-3 and 1 to stage x before
+ * the weight loads are issued; kernel 1: tiles per workgroup 1-2 and super-blocks per wave 2-3;
+ * kernel 2: waves splitting K, 4 or 8, and 0).  kernel = -1 where the call takes another path
+ * (m = 1, the other encodings).  No counterpart in the reference, whose showcase picks
+ * schedules by timing them (benchmarks/kernels/showcase/benchmark.py:214-237).
+ */
+int32_t tensor_gguf_gemv_plan_v1(uint32_t type, int64_t m, int64_t k, int64_t n, int32_t *kernel, int32_t *a,
+                                 int32_t *b, TensorErrorV1 *error);
+
+/*
+ * tensor_gguf_gemv_v1 for Q4_K at 2 <= M <= 8 on a plan the caller names, for plan sweeps:
+ * arguments [x, w, out, type, kernel, a, b], the last three uint32 scalars as reported by
+ * tensor_gguf_gemv_plan_v1.  TENSOR_ERROR_ARGUMENT where that kernel cannot run the shape with
+ * those fields; results equal the library plan's up to fp32 summation order.  No counterpart in
+ * the reference.
+ */
+int32_t tensor_gguf_gemv_variant_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/*
  * Decode GEMV of an MLP's gate and up projections with the SwiGLU epilogue:
  * out[m, n] = silu(g) * u, silu(g) = g / (1 + exp(-g)), where g and u are the
  * fp32 sums x[m, :] . dequant(W_gate)[n, :] and x[m, :] . dequant(W_up)[n, :]

@@ -26,6 +26,7 @@ KERNELS = (
     "tensor_gguf_linear_v1",
     "tensor_gguf_gemv_group_v1",
     "tensor_gguf_gemv_swiglu_v1",
+    "tensor_gguf_gemv_variant_v1",
     "tensor_gguf_dequant_v1",
 )
 
@@ -87,6 +88,8 @@ SERVICES = {
     "tensor_gguf_gemm_plan_v1": [c.c_uint32, c.c_int64, c.c_int64, c.POINTER(c.c_int64), c.c_uint32, _u64,
                                  c.POINTER(_i32), c.POINTER(_i32), c.POINTER(_i32)],
     "tensor_gguf_gemm_tile_v1": [_i32, c.POINTER(_i32), c.POINTER(_i32), c.POINTER(_i32)],
+    "tensor_gguf_gemv_plan_v1": [c.c_uint32, c.c_int64, c.c_int64, c.c_int64, c.POINTER(_i32), c.POINTER(_i32),
+                                 c.POINTER(_i32)],
 }
 
 

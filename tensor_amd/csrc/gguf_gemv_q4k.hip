@@ -856,13 +856,12 @@ static hipError_t launch_m1_group(const GemvArgs* a, int count, hipStream_t stre
 }
 
 template <int M, typename OutT>
-static hipError_t launch_mfma(const GemvArgs& a, hipStream_t stream) {
+static hipError_t launch_mfma(const GemvArgs& a, hipStream_t stream, int waves) {
   const _Float16* x = static_cast<const _Float16*>(a.x);
   const uint8_t* w = static_cast<const uint8_t*>(a.w);
   OutT* out = static_cast<OutT*>(a.out);
   const int tiles = (a.n + 15) / 16;
-  // split K so the grid holds roughly 12 waves per CU on a 256-CU part
-  if (tiles <= 512)
+  if (waves == 8)
     hipLaunchKernelGGL((gemv_q4k_mfma<M, 8, OutT>), dim3(tiles), dim3(8 * 64), 0, stream, x, w, out, a.n, a.k);
   else
     hipLaunchKernelGGL((gemv_q4k_mfma<M, 4, OutT>), dim3(tiles), dim3(4 * 64), 0, stream, x, w, out, a.n, a.k);
@@ -880,17 +879,10 @@ static hipError_t launch_mt_cfg(const GemvArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// x in LDS when it fits; 2 super-blocks per wave up to K = 8192, 3 up to K = 12288.
 template <int M, typename OutT>
-static hipError_t launch_mt(const GemvArgs& a, hipStream_t stream, bool* handled) {
-  const int blocks = a.k / 256;
-  const int s = blocks <= 32 ? 2 : 3, waves = (blocks + s - 1) / s;
-  // the kernel assumes at most 16 waves and at most 8 x chunks per thread
-  *handled = a.k % 256 == 0 && M * a.k <= kMtMaxMK && waves <= 16 && M * a.k / 8 <= waves * 64 * 8;
-  if (!*handled) return hipSuccess;
-  const bool wide = a.n >= 8192;
-  if (s == 2) return wide ? launch_mt_cfg<M, 2, 2, OutT>(a, stream) : launch_mt_cfg<M, 1, 2, OutT>(a, stream);
-  return wide ? launch_mt_cfg<M, 2, 3, OutT>(a, stream) : launch_mt_cfg<M, 1, 3, OutT>(a, stream);
+static hipError_t launch_mt(const GemvArgs& a, hipStream_t stream, int tiles, int s) {
+  if (s == 2) return tiles == 2 ? launch_mt_cfg<M, 2, 2, OutT>(a, stream) : launch_mt_cfg<M, 1, 2, OutT>(a, stream);
+  return tiles == 2 ? launch_mt_cfg<M, 2, 3, OutT>(a, stream) : launch_mt_cfg<M, 1, 3, OutT>(a, stream);
 }
 
 // x rows, the 16-element x sums and one header table per wave; the partial tiles of the
@@ -901,25 +893,12 @@ static size_t sec_lds_bytes(int m, int k, int waves) {
   return std::max(staged, (size_t)waves * 64 * sizeof(float4v_t));
 }
 
-// Sector-aligned kernel for matrices of at least 512 tiles (gate / up, 12288 x 4096: 11.0 us
-// at M = 4 against 12.8 us for gemv_q4k_mt) and rows of at least 8192 columns (down,
-// 4096 x 12288: 12.5 against 14.5 us); shorter and narrower shapes keep gemv_q4k_mt
-// (4096 x 4096: 6.1 us both).  Three tiles per workgroup when that still gives 256
-// workgroups, so every CU holds one.
 template <int M, typename OutT>
-static hipError_t launch_sec(const GemvArgs& a, hipStream_t stream, bool* handled) {
-  *handled = false;
-  const int kw = a.k / 1024, tiles = (a.n + 15) / 16;
-  if (a.k % 1024 != 0 || (tiles < 512 && kw < 8) || kw > 16) return hipSuccess;
-  const int per = tiles >= 768 && 3 * kw <= 16 ? 3 : tiles >= 512 && 2 * kw <= 16 ? 2 : 1;
-  const int threads = per * kw * 64;
+static hipError_t launch_sec(const GemvArgs& a, hipStream_t stream, int per, bool xfirst) {
+  const int kw = a.k / 1024, tiles = (a.n + 15) / 16, threads = per * kw * 64;
   const size_t lds = sec_lds_bytes(M, a.k, per * kw);
-  // x is staged with eight 16-byte chunks per thread at most, and must fit in LDS with its sums
-  if ((long)M * a.k / 8 > 8L * threads || lds > kSecMaxLds) return hipSuccess;
-  *handled = true;
   const int grid = (tiles + per - 1) / per;
-  // x first only where every workgroup starts at once: at most one per CU of the 256
-  if (grid <= 256)
+  if (xfirst)
     hipLaunchKernelGGL((gemv_q4k_sec<M, OutT, 0, true>), dim3(grid), dim3(threads), lds, stream,
                        static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out),
                        a.n, a.k, per);
@@ -961,31 +940,96 @@ static hipError_t launch_pair_multirow(const GemvArgs& a, const void* w2, void* 
   }
 }
 
-// 2 <= M <= 8: the sector-aligned kernel, else the LDS multi-tile kernel, else one super-block per step.
 template <int M, typename OutT>
-static hipError_t launch_multirow(const GemvArgs& a, hipStream_t stream) {
-  bool done = false;
-  hipError_t status = launch_sec<M, OutT>(a, stream, &done);
-  if (done) return status;
-  status = launch_mt<M, OutT>(a, stream, &done);
-  if (done) return status;
-  return launch_mfma<M, OutT>(a, stream);
+static hipError_t launch_plan_typed(const GemvArgs& a, const GemvPlan& plan, hipStream_t stream) {
+  switch (plan.kernel) {
+    case kGemvSec: return launch_sec<M, OutT>(a, stream, plan.a, plan.b != 0);
+    case kGemvMt: return launch_mt<M, OutT>(a, stream, plan.a, plan.b);
+    default: return launch_mfma<M, OutT>(a, stream, plan.a);
+  }
+}
+
+template <typename OutT>
+static hipError_t launch_plan_m(const GemvArgs& a, const GemvPlan& plan, hipStream_t stream) {
+  switch (a.m) {
+    case 2: return launch_plan_typed<2, OutT>(a, plan, stream);
+    case 3: return launch_plan_typed<3, OutT>(a, plan, stream);
+    case 4: return launch_plan_typed<4, OutT>(a, plan, stream);
+    case 5: return launch_plan_typed<5, OutT>(a, plan, stream);
+    case 6: return launch_plan_typed<6, OutT>(a, plan, stream);
+    case 7: return launch_plan_typed<7, OutT>(a, plan, stream);
+    default: return launch_plan_typed<8, OutT>(a, plan, stream);
+  }
+}
+
+// Launch limits of each multi-row kernel (what its indexing and LDS layout assume).
+static bool sec_fits(const GemvArgs& a, int per) {
+  const int kw = a.k / 1024;
+  if (a.k % 1024 != 0 || kw < 1 || kw > 16 || per < 1 || per > 3 || per * kw > 16) return false;
+  const int threads = per * kw * 64;
+  // x is staged with eight 16-byte chunks per thread at most, and must fit in LDS with its sums
+  return (long)a.m * a.k / 8 <= 8L * threads && sec_lds_bytes(a.m, a.k, per * kw) <= kSecMaxLds;
+}
+
+static bool mt_fits(const GemvArgs& a, int tiles, int s) {
+  if (a.k % 256 != 0 || (tiles != 1 && tiles != 2) || (s != 2 && s != 3)) return false;
+  const int waves = (a.k / 256 + s - 1) / s;
+  // at most 16 waves and at most 8 x chunks per thread; x in LDS
+  return waves <= 16 && (long)a.m * a.k <= kMtMaxMK && (long)a.m * a.k / 8 <= (long)waves * 64 * 8;
+}
+
+bool gemv_q4k_plan_fits(const GemvArgs& a, const GemvPlan& plan) {
+  if (a.type != kQ4_K || a.x_f32 || a.m < 2 || a.m > 8 || a.k % 256 != 0 || a.n < 1) return false;
+  switch (plan.kernel) {
+    case kGemvSec: return (plan.b == 0 || plan.b == 1) && sec_fits(a, plan.a);
+    case kGemvMt: return mt_fits(a, plan.a, plan.b);
+    case kGemvMfma: return (plan.a == 4 || plan.a == 8) && plan.b == 0;
+    default: return false;
+  }
+}
+
+// The library's multi-row plan.  Sector-aligned kernel for matrices of at least 512 tiles
+// (gate / up, 12288 x 4096: 11.0 us at M = 4 against 12.8 us for gemv_q4k_mt) and rows of at
+// least 8192 columns (down, 4096 x 12288: 12.5 against 14.5 us), three tiles per workgroup when
+// that still gives 256 workgroups (so every CU holds one), x first only where every workgroup
+// starts at once (at most one per CU of the 256); shorter and narrower shapes take
+// gemv_q4k_mt (4096 x 4096: 6.1 us both) with x in LDS, 2 super-blocks per wave up to K = 8192
+// and 3 up to 12288, two tiles per workgroup from 8192 rows; else gemv_q4k_mfma, K split over
+// 8 waves up to 512 tiles (about 12 waves per CU on 256 CUs), else over 4.
+bool gemv_q4k_plan(const GemvArgs& a, GemvPlan* plan) {
+  if (a.type != kQ4_K || a.x_f32 || a.m < 2 || a.m > 8 || a.k % 256 != 0) return false;
+  const int kw = a.k / 1024, tiles = (a.n + 15) / 16, blocks = a.k / 256;
+  if (a.k % 1024 == 0 && (tiles >= 512 || kw >= 8)) {
+    const int per = tiles >= 768 && 3 * kw <= 16 ? 3 : tiles >= 512 && 2 * kw <= 16 ? 2 : 1;
+    if (sec_fits(a, per)) {
+      *plan = GemvPlan{kGemvSec, per, (tiles + per - 1) / per <= 256 ? 1 : 0};
+      return true;
+    }
+  }
+  const GemvPlan mt{kGemvMt, a.n >= 8192 ? 2 : 1, blocks <= 32 ? 2 : 3};
+  if (mt_fits(a, mt.a, mt.b)) {
+    *plan = mt;
+    return true;
+  }
+  *plan = GemvPlan{kGemvMfma, tiles <= 512 ? 8 : 4, 0};
+  return true;
+}
+
+hipError_t launch_gemv_q4k_plan(const GemvArgs& a, const GemvPlan& plan, hipStream_t stream) {
+  if (!gemv_q4k_plan_fits(a, plan)) return hipErrorInvalidValue;
+  return a.out_half ? launch_plan_m<_Float16>(a, plan, stream) : launch_plan_m<float>(a, plan, stream);
 }
 
 template <typename OutT>
 static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream, bool* handled) {
   *handled = true;
   if (gemv_q4k_group_supported(a.m, a.k, a.n)) return launch_m1_group<OutT>(&a, 1, stream);
-  switch (a.m) {
-    case 2: return launch_multirow<2, OutT>(a, stream);
-    case 3: return launch_multirow<3, OutT>(a, stream);
-    case 4: return launch_multirow<4, OutT>(a, stream);
-    case 5: return launch_multirow<5, OutT>(a, stream);
-    case 6: return launch_multirow<6, OutT>(a, stream);
-    case 7: return launch_multirow<7, OutT>(a, stream);
-    case 8: return launch_multirow<8, OutT>(a, stream);
-    default: *handled = false; return hipSuccess;
+  GemvPlan plan;
+  if (!gemv_q4k_plan(a, &plan)) {
+    *handled = false;
+    return hipSuccess;
   }
+  return launch_plan_m<OutT>(a, plan, stream);
 }
 
 // Q5_K at M = 1 (K a multiple of 4096, at most 16384): the M = 1 kernel with the fifth bits.

@@ -49,6 +49,22 @@ hipError_t launch_gemv_q4k_group(const GemvArgs* args, int count, hipStream_t st
 // when x does not fit the kernel's LDS.
 bool gemv_q4k_pair_supported(const GemvArgs* args, int count);
 hipError_t launch_gemv_q4k_pair(const GemvArgs* args, hipStream_t stream, bool* handled);
+// Multi-row Q4_K decode GEMV plans (2 <= M <= 8, fp16 x): the kernel and its launch shape.
+//   kGemvSec  (gemv_q4k_sec):  a = 16-row tiles per workgroup (1-3), b = 1 to stage x before
+//                              the weight loads are issued, 0 to issue them behind x
+//   kGemvMt   (gemv_q4k_mt):   a = tiles per workgroup (1-2), b = super-blocks per wave (2-3)
+//   kGemvMfma (gemv_q4k_mfma): a = waves per workgroup splitting K (4 or 8), b = 0
+enum { kGemvSec = 0, kGemvMt = 1, kGemvMfma = 2 };
+struct GemvPlan {
+  int kernel, a, b;
+};
+// The plan the library takes for args; false where another path takes the call (other
+// encodings, M = 1, M > 8, fp32 x).
+bool gemv_q4k_plan(const GemvArgs& args, GemvPlan* plan);
+// Whether plan fits args's shape (the launch limits of its kernel).
+bool gemv_q4k_plan_fits(const GemvArgs& args, const GemvPlan& plan);
+// Launch a plan that fits (hipErrorInvalidValue otherwise).
+hipError_t launch_gemv_q4k_plan(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream);
 // Decode GEMV with the SwiGLU epilogue of an MLP: out = silu(x W_gate^T) * (x W_up^T),
 // args.w the gate matrix, w_up the up matrix of the same shape and encoding.
 hipError_t launch_gemv_swiglu(const GemvArgs& gate, const void* w_up, hipStream_t stream);

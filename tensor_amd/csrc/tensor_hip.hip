@@ -343,6 +343,49 @@ int32_t check_u32(const TensorArgumentV1& arg, const char* name, uint64_t* value
   return TENSOR_OK;
 }
 
+// The multi-row Q4_K decode GEMV on a plan the caller names: [x, w, out, type, kernel, a, b]
+// (the plan fields of tensor_gguf::GemvPlan as uint32 scalars).
+int32_t gemv_variant_call(const TensorCallV1* call, TensorErrorV1* error) {
+  ok(error);
+  if (int32_t s = check_call(call, 7, error)) return s;
+  const int ordinal = call->stream.device_ordinal;
+  const TensorArgumentV1* a = call->arguments;
+  Format format;
+  if (int32_t s = check_type(a[3], &format, error)) return s;
+  uint64_t kernel = 0, pa = 0, pb = 0;
+  if (int32_t s = check_u32(a[4], "kernel", &kernel, error)) return s;
+  if (int32_t s = check_u32(a[5], "a", &pa, error)) return s;
+  if (int32_t s = check_u32(a[6], "b", &pb, error)) return s;
+  if (int32_t s = check_matrix(a[0], "x", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT16, error)) return s;
+  if (int32_t s = check_matrix(a[1], "w", ordinal, TENSOR_UINT8, TENSOR_UINT8, error)) return s;
+  if (int32_t s = check_matrix(a[2], "out", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT32, error)) return s;
+  const int64_t m = a[0].buffer.shape[0], k = a[0].buffer.shape[1], n = a[1].buffer.shape[0];
+  if (k % format.qk || a[1].buffer.shape[1] != k / format.qk * format.bytes)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "w: shape, stride or size mismatch");
+  if (a[2].buffer.shape[0] != m || a[2].buffer.shape[1] != n)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "out: shape, stride or size mismatch");
+  tensor_gguf::GemvArgs args;
+  args.x = reinterpret_cast<const void*>(a[0].buffer.address);
+  args.w = reinterpret_cast<const void*>(a[1].buffer.address);
+  args.out = reinterpret_cast<void*>(a[2].buffer.address);
+  args.type = (int)a[3].scalar;
+  args.m = (int)m;
+  args.n = (int)n;
+  args.k = (int)k;
+  args.out_half = a[2].dtype == TENSOR_FLOAT16;
+  tensor_gguf::GemvPlan probe;
+  if (!tensor_gguf::gemv_q4k_plan(args, &probe))
+    return fail(error, TENSOR_ERROR_ARGUMENT, "multi-row GEMV plans take Q4_K with 2 <= M <= 8");
+  const tensor_gguf::GemvPlan plan{(int)kernel, (int)pa, (int)pb};
+  if (kernel > 2 || pa > 16 || pb > 16 || !tensor_gguf::gemv_q4k_plan_fits(args, plan))
+    return fail(error, TENSOR_ERROR_ARGUMENT, "GEMV plan (%u, %u, %u) does not fit this shape", (unsigned)kernel,
+                (unsigned)pa, (unsigned)pb);
+  if (int32_t s = check_device(call, error)) return s;
+  hipError_t status = tensor_gguf::launch_gemv_q4k_plan(args, plan, reinterpret_cast<hipStream_t>(call->stream.handle));
+  if (status != hipSuccess) return hip_fail(error, status, "GGUF GEMV launch");
+  return TENSOR_OK;
+}
+
 // The packed call form: [x, w, out, type, m, n, k] with flat buffers (see tensor_hip.h).
 int32_t packed_call(const TensorCallV1* call, TensorErrorV1* error) {
   ok(error);
@@ -596,6 +639,34 @@ int32_t tensor_gguf_gemm_plan_v1(uint32_t type, int64_t m, int64_t k, const int6
   *splits = plan.splits;
   *pipelined = (!small || plan.small_m) && tensor_gguf::gemm_group_pipelined(group, plan);
   return ok(error);
+}
+
+int32_t tensor_gguf_gemv_plan_v1(uint32_t type, int64_t m, int64_t k, int64_t n, int32_t* kernel, int32_t* a,
+                                 int32_t* b, TensorErrorV1* error) {
+  Format format;
+  if (!kernel || !a || !b) return fail(error, TENSOR_ERROR_ARGUMENT, "invalid plan query");
+  if (!ggml_format(type, &format))
+    return fail(error, TENSOR_ERROR_ARGUMENT, "type: unsupported GGML type %u", type);
+  if (m < 1 || m > tensor_gguf::kGemvMaxM || k < 1 || k % format.qk || k >= (int64_t)1 << 31 || n < 1 ||
+      n >= (int64_t)1 << 31)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "m, k, n: 1 <= m <= %d, k a positive multiple of %d, n positive",
+                tensor_gguf::kGemvMaxM, format.qk);
+  tensor_gguf::GemvArgs args{};
+  args.type = (int)type;
+  args.m = (int)m;
+  args.n = (int)n;
+  args.k = (int)k;
+  args.out_half = true;
+  tensor_gguf::GemvPlan plan{-1, 0, 0};  // -1: the call takes another path (M = 1, other encodings)
+  if (!tensor_gguf::gemv_q4k_plan(args, &plan)) plan = tensor_gguf::GemvPlan{-1, 0, 0};
+  *kernel = plan.kernel;
+  *a = plan.a;
+  *b = plan.b;
+  return ok(error);
+}
+
+int32_t tensor_gguf_gemv_variant_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  return gemv_variant_call(call, error);
 }
 
 int32_t tensor_gguf_packed_v1(const TensorCallV1* call, TensorErrorV1* error) {

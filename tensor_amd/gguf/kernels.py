@@ -29,6 +29,7 @@ ENTRYPOINTS = {
     "gguf_gemm_group_noalloc": "tensor_gguf_gemm_group_noalloc_v1",
     "gguf_gemm_group_plan": "tensor_gguf_gemm_group_plan_v1",
     "gguf_gemv_swiglu": "tensor_gguf_gemv_swiglu_v1",
+    "gguf_gemv_variant": "tensor_gguf_gemv_variant_v1",
     "gguf_dequant": "tensor_gguf_dequant_v1",
 }
 GEMV_GROUP_MAX = 3  # TENSOR_GGUF_GEMV_GROUP_MAX
@@ -116,7 +117,9 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
     with two more scalars, ``tile`` and ``splits``, naming the plan it runs (plan sweeps: see
     ``Device.gemm_plan``); every other kernel takes no ``count``.
     ``gguf_gemv_swiglu`` takes ``[x, w_gate, w_up, out, type]`` and stores
-    silu(x W_gate^T) * (x W_up^T).
+    silu(x W_gate^T) * (x W_up^T).  ``gguf_gemv_variant`` (Q4_K, 2 <= M <= 8) is ``gguf_gemv``
+    with three more scalars, ``kernel``, ``a`` and ``b``, naming the multi-row plan it runs (plan
+    sweeps: see ``Device.gemv_plan``).
     """
     if kernel not in ENTRYPOINTS:
         raise ValueError(f"unknown HIP kernel {kernel!r}; choose {', '.join(ENTRYPOINTS)}")
@@ -171,6 +174,10 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
             {"name": "out", "dtype": out_dtype, "shape": [{"var": "M"}, {"var": "N"}], "alignment": 16},
             type_argument,
         ]
+        if kernel == "gguf_gemv_variant":  # the multi-row plan, supplied per call
+            if code != ggml_type("q4_k"):
+                raise ValueError("gguf_gemv_variant runs Q4_K only")
+            arguments += [{"name": name, "dtype": "uint32", "kind": "scalar"} for name in ("kernel", "a", "b")]
     result = {
         "name": f"{kernel}:{NAMES[code]}:{out_dtype}" + (f":{count}" if kernel in GROUPS else ""),
         "provider": "hip",
@@ -194,4 +201,6 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
     }
     if kernel in ("gguf_gemv", "gguf_gemv_group", "gguf_gemv_swiglu"):
         result["shape_domain"] = {"M": [1, GEMV_MAX_M]}
+    if kernel == "gguf_gemv_variant":
+        result["shape_domain"] = {"M": [2, GEMV_MAX_M]}
     return result

@@ -27,6 +27,15 @@ from tensor_amd.runtime.event import Event
 from tensor_amd.runtime.executable import Executable
 from tensor_amd.runtime.session import Session
 
+# Multi-row Q4_K GEMV kernels by plan index, and the launch fields (a, b) each accepts:
+# sector-aligned tiles (tiles per workgroup, x staged before the weight loads), multi-tile with x
+# in LDS (tiles per workgroup, super-blocks per wave), x read per wave (waves splitting K, 0).
+GEMV_KERNELS = ("sec", "mt", "mfma")
+GEMV_FIELDS = {0: [(a, b) for a in (1, 2, 3) for b in (0, 1)],
+               1: [(a, b) for a in (1, 2) for b in (2, 3)],
+               2: [(4, 0), (8, 0)]}
+
+
 def gemm_tiles() -> list:
     """Every tile of the pipelined prefill GEMM, by index: {"bm", "bn", "ks"}."""
     tiles = []
@@ -429,6 +438,19 @@ class Device(Session):
         _native.call("tensor_gguf_gemm_workspace_v1", ggml_type(encoding), int(m), int(k),
                      (c.c_int64 * len(rows))(*rows), len(rows), c.byref(result))
         return result.value
+
+    def gemv_plan(self, encoding, m: int, k: int, n: int) -> dict | None:
+        """The multi-row plan ``gguf_gemv`` takes for a Q4_K call with 2 <= m <= 8 (None where
+        the call takes another path): the kernel (``GEMV_KERNELS``) and its two launch fields,
+        which ``gguf_gemv_variant`` accepts as its ``kernel``, ``a`` and ``b`` scalars."""
+        from tensor_amd.gguf.quant import ggml_type
+
+        kernel, a, b = c.c_int32(), c.c_int32(), c.c_int32()
+        _native.call("tensor_gguf_gemv_plan_v1", ggml_type(encoding), int(m), int(k), int(n), c.byref(kernel),
+                     c.byref(a), c.byref(b))
+        if kernel.value < 0:
+            return None
+        return {"kernel": kernel.value, "name": GEMV_KERNELS[kernel.value], "a": a.value, "b": b.value}
 
     def gemm_plan(self, encoding, m: int, k: int, rows, workspace_bytes: int | None = None) -> dict:
         """The plan ``gguf_gemm_group`` takes for this shape (``workspace_bytes`` of workspace,

@@ -546,6 +546,77 @@ def test_gemm_plan_query_names_the_library_plans_at_the_baseline_shapes():
                                         c.byref(c.c_int32()), c.byref(error)) == ERR_ARG
 
 
+def test_gemv_plan_query_names_the_library_plans_at_the_baseline_shapes():
+    """The multi-row plans the Q4_K decode GEMV takes at C2's M=4 and M=8 shapes (CPU only: a
+    query, no launch), and the paths the query leaves to other kernels."""
+    from tensor_amd.providers.hip import GEMV_FIELDS, GEMV_KERNELS
+
+    assert GEMV_KERNELS == ("sec", "mt", "mfma")
+    lib = _native.library()
+
+    def plan(code, m, k, n):
+        kernel, a, b = c.c_int32(), c.c_int32(), c.c_int32()
+        error = abi.ErrorDescriptor()
+        status = lib.tensor_gguf_gemv_plan_v1(code, m, k, n, c.byref(kernel), c.byref(a), c.byref(b), c.byref(error))
+        assert status == OK, error.message
+        return kernel.value, a.value, b.value
+
+    assert plan(12, 4, 4096, 12288) == (0, 3, 1)   # gate / up at M=4: sector tiles, 3 per workgroup, x first
+    assert plan(12, 4, 12288, 4096) == (0, 1, 1)   # down at M=4: one tile, 12 K ranges
+    assert plan(12, 8, 4096, 12288) == (0, 3, 1)
+    assert plan(12, 8, 12288, 4096) == (2, 8, 0)   # down at M=8: x (196 KB) does not fit LDS
+    assert plan(12, 4, 4096, 4096) == (1, 1, 2)    # narrower shapes: the multi-tile kernel
+    for query in ((12, 1, 4096, 12288), (14, 4, 4096, 4096), (8, 4, 4096, 4096)):
+        assert plan(*query)[0] == -1               # M = 1 and the other encodings: other kernels
+    for kernel, a, b in (plan(12, 4, 4096, 12288), plan(12, 8, 12288, 4096), plan(12, 4, 4096, 4096)):
+        assert (a, b) in GEMV_FIELDS[kernel]
+    error = abi.ErrorDescriptor()
+    out = [c.c_int32() for _ in range(3)]
+    assert lib.tensor_gguf_gemv_plan_v1(12, 9, 4096, 4096, *map(c.byref, out), c.byref(error)) == ERR_ARG
+    assert lib.tensor_gguf_gemv_plan_v1(12, 4, 4000, 4096, *map(c.byref, out), c.byref(error)) == ERR_ARG
+
+
+def test_gemv_variant_refuses_a_plan_that_does_not_fit():
+    """tensor_gguf_gemv_variant_v1 checks the named kernel and fields against the shape before
+    any HIP call (fake device addresses; CPU only): a plan that fits gets as far as the device
+    check, which fails here with no GPU."""
+    manifest = kernels.manifest("gguf_gemv_variant", "q4_k", "float16")
+    names = [a["name"] for a in manifest["arguments"]]
+    assert names == ["x", "w", "out", "type", "kernel", "a", "b"]
+    with pytest.raises(ValueError):
+        kernels.manifest("gguf_gemv_variant", "q6_k", "float16")
+
+    def call_with(m, n, k, kernel, a, b, code=12):
+        shapes = {"x": (m, k), "w": (n, k // 256 * 144), "out": (m, n)}
+        dtypes, sizes = {"x": 10, "w": 3, "out": 10}, {"x": 2, "w": 1, "out": 2}
+        keep, args = [], (abi.Argument * 7)()
+        for j, name in enumerate(names[:3]):
+            shape = shapes[name]
+            strides = (sizes[name] * shape[1], sizes[name])
+            arrays = ((c.c_int64 * 2)(*shape), (c.c_int64 * 2)(*strides))
+            keep.append(arrays)
+            args[j].kind, args[j].dtype = 1, dtypes[name]
+            args[j].buffer = abi.BufferDescriptor(0x10000 * (j + 1), int(np.prod(shape)) * sizes[name], arrays[0],
+                                                  arrays[1], 2, dtypes[name], 10, 0)
+        for j, value in ((3, code), (4, kernel), (5, a), (6, b)):
+            args[j].kind, args[j].dtype, args[j].scalar = 2, 7, value
+        call = abi.CallDescriptor(1, 72, args, 7, 0, (c.c_uint32 * 3)(1, 1, 1), (c.c_uint32 * 3)(256, 1, 1), 0,
+                                  abi.StreamDescriptor(10, 0, 0))
+        error = abi.ErrorDescriptor()
+        status = _native.kernel("tensor_gguf_gemv_variant_v1")(c.byref(call), c.byref(error))
+        return status, error.message.decode()
+
+    assert call_with(4, 4096, 12288, 0, 3, 1)[0] == ERR_ARG    # 3 tiles x 12 K ranges > 16 waves
+    assert call_with(8, 4096, 12288, 1, 1, 3)[0] == ERR_ARG    # x of 8 x 12288 does not fit the LDS
+    assert call_with(4, 4096, 4096, 2, 5, 0)[0] == ERR_ARG     # 5 waves: not a variant
+    assert call_with(4, 4096, 4096, 3, 1, 0)[0] == ERR_ARG     # no such kernel
+    status, message = call_with(1, 4096, 4096, 2, 8, 0)         # M = 1 takes the decode kernel
+    assert status == ERR_ARG and "2 <= M <= 8" in message
+    status, message = call_with(4, 4096, 4096, 0, 1, 2)         # x-first flag must be 0 or 1
+    assert status == ERR_ARG and "does not fit" in message
+    assert call_with(4, 4096, 12288, 0, 1, 1)[0] == ERR_PROVIDER  # fits: stops at the device check
+
+
 def test_gemm_forced_plan_refuses_a_plan_that_does_not_fit():
     """tensor_gguf_gemm_group_plan_v1 checks the named tile and split against the shape before any
     HIP call (fake device addresses; CPU only)."""

@@ -970,6 +970,45 @@ def test_gemm_group_with_a_short_workspace_splits_less(hip_device, c_oracle):
         assert R.relative_l2(got[0], expected) <= 1e-5
 
 
+@pytest.mark.parametrize("m,n,k", [(4, 2000, 4096), (3, 777, 8192), (8, 1000, 12288), (2, 40, 1280)])
+def test_gemv_every_multirow_plan_through_the_variant_entry(hip_device, c_oracle, m, n, k):
+    """Every multi-row Q4_K plan the variant entry accepts at ragged shapes (fp32 out): each within
+    2e-4 of the decode oracle and within 1e-5 of the library plan's result; plans that do not fit
+    are refused with an argument error before any launch, and the library's own plan is one of
+    those that run."""
+    from tensor_amd._native import HipError
+    from tensor_amd.providers.hip import GEMV_FIELDS
+
+    code = Q.ggml_type("q4_k")
+    note("gemv-plans", m, n, k)
+    raw, x = cases.weight(n, k, "q4_k", 1400 + m), cases.activation(m, k, 1410 + m)
+    expected = c_oracle.linear(x, raw, code, n, k)
+    library = hip_device.gemv_plan("q4_k", m, k, n)
+    baseline = run_linear(hip_device, "gguf_gemv", "q4_k", x, raw, "float32")
+    assert R.relative_l2(baseline, expected) <= 2e-4
+    exe = hip_device.load("gguf_gemv_variant", encoding="q4_k", out_dtype="float32")
+    xb, wb = hip_device.from_numpy(x), hip_device.from_numpy(raw)
+    out = hip_device.empty((m, n), "float32")
+    ran = []
+    for kernel, fields in GEMV_FIELDS.items():
+        for a, b in fields:
+            hip_device.fill_bytes(out, 0xFF)
+            try:
+                exe.launch(xb, wb, out, kernel=kernel, a=a, b=b)
+            except HipError as exc:
+                assert exc.code == 2, (kernel, a, b, exc)
+                continue
+            ran.append((kernel, a, b))
+            got = out.to_numpy()
+            assert not np.isnan(got).any(), (kernel, a, b)
+            assert R.relative_l2(got, expected) <= 2e-4, (kernel, a, b)
+            assert R.relative_l2(got, baseline) <= 1e-5, (kernel, a, b)
+    assert (library["kernel"], library["a"], library["b"]) in ran, (library, ran)
+    assert len(ran) >= 2, ran
+    for buffer in (xb, wb, out):
+        buffer.release()
+
+
 @pytest.mark.parametrize("encoding", ["q4_k", "q6_k", "q8_0", "q4_0"])
 def test_gemm_every_plan_through_the_plan_entry(hip_device, c_oracle, encoding):
     """Every tile and K split the plan-naming entry accepts at a ragged grouped shape (two

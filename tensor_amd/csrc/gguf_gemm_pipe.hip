@@ -14,7 +14,10 @@
 //     staging stores of one buffer with the fragment reads of the other;
 //   * each step is one straight-line region in which sched_group_barrier
 //     interleaves every MFMA with dequant VALU work, an LDS store or a global
-//     load, keeping the matrix pipe fed while the VALU decodes.
+//     load, keeping the matrix pipe fed while the VALU decodes;
+//   * XDMA (the 256 x 192 tile): the activation tile goes from global memory
+//     straight to LDS (global_load_lds_dwordx4, three swizzled buffers), which
+//     frees the staging registers the wider tile needs.
 //
 // Weights are dequantized with the reference's fp32 arithmetic (every product
 // exact, one rounding) and converted to fp16 with round-to-nearest-even, so
@@ -118,34 +121,37 @@ struct Raw {
 //
 // XT = float: fp32 activations (the packed call form), rounded to fp16 as they are loaded, so
 // the staged tile is fp16(x) as in the reference's prefill numerics (benchmark.py:473-477).
-template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT, typename XT = _Float16>
+template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT, typename XT = _Float16, bool XDMA = false>
 __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restrict__ x, const GemmJob job,
                                                                int M, int K) {
   using namespace pipe;
   constexpr int THREADS = WM * WN * 64;  // per K group
   constexpr int MT = BM / WM / 16, NT = BN / WN / 16;
-  constexpr int XL = BM * 8 / THREADS;  // 16-byte activation chunks per thread per step
+  constexpr int XL = XDMA ? 1 : BM * 8 / THREADS;  // 16-byte activation chunks per thread per step
+  static_assert(!XDMA || (KS == 1 && sizeof(XT) == 2), "x by LDS DMA: fp16 x, one K group");
+  constexpr int XS = BM * BK;                  // halves per DMA'd x buffer (128-byte rows, swizzled)
+  constexpr int XPW = BM * BK * 2 / 1024 / (WM * WN);  // 1 KB DMA blocks per wave per step
   // TPR parts per weight row (a part: the row's step bytes one thread decodes).  Where BN
   // divides the threads, every thread takes one part of one row; otherwise (BN = 96, 192)
   // rows take 4 parts and thread t the parts t, t + THREADS, ... below BN * 4, so a wave
   // either has a part at a given index or has none (the test is wave-uniform).
   constexpr int TPR = THREADS % BN == 0 ? THREADS / BN : 4;
   constexpr int PARTS = (BN * TPR + THREADS - 1) / THREADS;
-  static_assert(XL * THREADS == BM * 8 && (TPR == 1 || TPR == 2 || TPR == 4) && PARTS <= 2 &&
+  static_assert((XDMA || XL * THREADS == BM * 8) && (TPR == 1 || TPR == 2 || TPR == 4) && PARTS <= 2 &&
                     (BN * TPR) % 64 == 0, "tile shape");
   using G = Geometry<TYPE, TPR>;
   using RawT = Raw<XL, G::W0, G::W1, PARTS>;
   constexpr int QK = Block<TYPE>::QK, BYTES = Block<TYPE>::BYTES;
   constexpr bool KQ = TYPE == kQ4_K || TYPE == kQ5_K;  // Q4_K's header and nibble layout
   constexpr bool B32 = TYPE == kQ8_0 || TYPE == kQ4_0;  // 32-element blocks, two per step
-  constexpr int STAGE = 2 * (BM + BN) * ROW;  // halves of one group's double-buffered tiles
-  __shared__ __attribute__((aligned(16))) _Float16 stage[KS * STAGE];
+  constexpr int STAGE = XDMA ? 3 * XS + 2 * BN * ROW : 2 * (BM + BN) * ROW;  // halves of one group's tiles
+  __shared__ __attribute__((aligned(1024))) _Float16 stage[KS * STAGE];
   // wave-uniform (THREADS is a multiple of 64): keeps the step counter and the
   // addressing derived from it in scalar registers
   const int group = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x / THREADS);
   _Float16* const xs0 = stage + group * STAGE;
-  _Float16* const xs1 = xs0 + BM * ROW;
-  _Float16* const ws0 = xs1 + BM * ROW;
+  _Float16* const xs1 = xs0 + (XDMA ? XS : BM * ROW);
+  _Float16* const ws0 = XDMA ? xs0 + 3 * XS : xs1 + BM * ROW;
   _Float16* const ws1 = ws0 + BN * ROW;
 
   const int tid = threadIdx.x % THREADS, lane = tid & 63, wave = tid >> 6;
@@ -171,10 +177,31 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
   const int split_steps = K / BK / job.splits;
   const int steps = split_steps / KS, first = blockIdx.z * split_steps + group * steps;
 
+  // XDMA: DMA source rows of this lane.  Block b = XPW wave + i of the x tile (1 KB, 8 rows of
+  // 128 B) goes to LDS lane-linear: lane l writes 16 B at 16 l, row 8 b + l / 8, slot l % 8, which
+  // holds chunk (l % 8) ^ ((row >> 1) & 7) of the row, so a 16-row fragment read hits 16 bank groups
+  const XT* xsrc[XDMA ? XPW : 1];
+  if constexpr (XDMA) {
+#pragma unroll
+    for (int i = 0; i < XPW; ++i) {
+      const int r = 8 * (XPW * wave + i) + (lane >> 3);
+      const int cch = (lane & 7) ^ ((r >> 1) & 7);
+      xsrc[i] = x + (size_t)min(m0 + r, M - 1) * K + 8 * cch;
+    }
+  }
+  auto dma = [&](int step, _Float16* xbuf) {
+    if constexpr (XDMA) {
+#pragma unroll
+      for (int i = 0; i < XPW; ++i)
+        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(xsrc[i] + step * BK),
+                                         (void __attribute__((address_space(3)))*)(xbuf + (XPW * wave + i) * 512),
+                                         16, 0, 0);
+    }
+  };
   auto load = [&](RawT& r, int step) {
     const int k0 = step * BK;
 #pragma unroll
-    for (int i = 0; i < XL; ++i) {
+    for (int i = 0; i < (XDMA ? 0 : XL); ++i) {
       const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
       // rows past M reload row M - 1: their products land in output rows that are never stored
       const XT* src = x + (size_t)min(m0 + row, M - 1) * K + k0 + c8;
@@ -240,7 +267,7 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
 
   auto store = [&](const RawT& r, _Float16* xs, _Float16* ws, int step) {
 #pragma unroll
-    for (int i = 0; i < XL; ++i) {
+    for (int i = 0; i < (XDMA ? 0 : XL); ++i) {
       const int c = i * THREADS + tid, row = c >> 3, c8 = (c & 7) * 8;
       *reinterpret_cast<uint4*>(&xs[row * ROW + c8]) = make_uint4(r.x[4 * i], r.x[4 * i + 1], r.x[4 * i + 2], r.x[4 * i + 3]);
     }
@@ -329,19 +356,32 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
   // one K step: fragment reads of (xs, ws), then MFMAs interleaved with the
   // staging of `staged` into (xn, wnext) and the prefetch of `fetch_step`
   auto step_body = [&](const _Float16* xs, const _Float16* ws, _Float16* xn, _Float16* wnext, const RawT& staged,
-                       int staged_step, RawT& fetched, int fetch_step) {
+                       int staged_step, RawT& fetched, int fetch_step, _Float16* xdma = nullptr) {
     half8_t a[2][MT], b[2][NT];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int koff = 32 * kk + 8 * (lane >> 4);
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
-        a[kk][i] = *reinterpret_cast<const half8_t*>(&xs[(wm + 16 * i + (lane & 15)) * ROW + koff]);
+      for (int i = 0; i < MT; ++i) {
+        const int row = wm + 16 * i + (lane & 15);
+        if constexpr (XDMA)
+          a[kk][i] = *reinterpret_cast<const half8_t*>(&xs[row * BK + 8 * ((4 * kk + (lane >> 4)) ^ ((row >> 1) & 7))]);
+        else
+          a[kk][i] = *reinterpret_cast<const half8_t*>(&xs[row * ROW + koff]);
+      }
 #pragma unroll
       for (int j = 0; j < NT; ++j)
         b[kk][j] = *reinterpret_cast<const half8_t*>(&ws[(wn + 16 * j + (lane & 15)) * ROW + koff]);
     }
     store(staged, xn, wnext, staged_step);
+    if constexpr (XDMA) {
+      // the x DMA of the fetched step is issued ahead of its weight loads and the order is pinned:
+      // loads complete in order, so once a wave's dequant has waited on those weights (the next
+      // step's store), its DMA'd x has landed too, before the barrier that follows
+      dma(fetch_step, xdma);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    }
     load(fetched, fetch_step);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
@@ -362,16 +402,41 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
   // two register sets of raw bytes: step s+1 is staged into LDS while step s+2 is fetched
   RawT ra, rb;
   const int last = first + steps - 1;
-  load(ra, first);
-  load(rb, first + 1);
-  store(ra, xs0, ws0, first);
-  __syncthreads();
-  for (int step = first; step < first + steps; step += 2) {
-    // the last step stages and fetches clamped copies that are never read
-    step_body(xs0, ws0, xs1, ws1, rb, step + 1, ra, min(step + 2, last));
+  if constexpr (XDMA) {
+    // three x buffers: step s reads buffer s % 3 while the DMA of step s + 2 fills (s + 2) % 3;
+    // the barrier between steps orders LDS only (this wave's DMA'd x of the next step has landed
+    // by then), so the weight loads in flight stay in flight
+    dma(first, xs0);
+    asm volatile("" ::: "memory");
+    dma(first + 1, xs1);
+    asm volatile("" ::: "memory");
+    load(ra, first);
+    load(rb, first + 1);
+    store(ra, xs0, ws0, first);
+    __builtin_amdgcn_s_waitcnt(0);  // the first two x tiles have landed (every counter)
     __syncthreads();
-    step_body(xs1, ws1, xs0, ws0, ra, min(step + 2, last), rb, min(step + 3, last));
+    int cur = 0;
+    for (int step = first; step < first + steps; step += 2) {
+      const int c1 = cur == 2 ? 0 : cur + 1, c2 = c1 == 2 ? 0 : c1 + 1;
+      step_body(xs0 + cur * XS, ws0, nullptr, ws1, rb, step + 1, ra, min(step + 2, last), xs0 + c2 * XS);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const int c3 = c2 == 2 ? 0 : c2 + 1;
+      step_body(xs0 + c1 * XS, ws1, nullptr, ws0, ra, min(step + 2, last), rb, min(step + 3, last), xs0 + c3 * XS);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      cur = c2;
+    }
+  } else {
+    load(ra, first);
+    load(rb, first + 1);
+    store(ra, xs0, ws0, first);
     __syncthreads();
+    for (int step = first; step < first + steps; step += 2) {
+      // the last step stages and fetches clamped copies that are never read
+      step_body(xs0, ws0, xs1, ws1, rb, step + 1, ra, min(step + 2, last));
+      __syncthreads();
+      step_body(xs1, ws1, xs0, ws0, ra, min(step + 2, last), rb, min(step + 3, last));
+      __syncthreads();
+    }
   }
   if constexpr (KS > 1) {
     // partial tiles of groups 1 .. KS-1 -> LDS (over the staging buffers), summed by group 0
@@ -478,9 +543,17 @@ namespace {
 struct Tile {
   int bm, bn, ks;
 };
-constexpr int kTileCount = 9;
+constexpr int kTileCount = 10;
 constexpr Tile kTiles[kTileCount] = {{256, 128, 1}, {128, 128, 1}, {128, 64, 1}, {64, 64, 1}, {128, 128, 2},
-                                     {128, 64, 2},  {64, 64, 2},   {64, 64, 4},  {256, 96, 1}};
+                                     {128, 64, 2},  {64, 64, 2},   {64, 64, 4},  {256, 96, 1}, {256, 192, 1}};
+constexpr int kDmaTile = 9;  // x tile by LDS DMA: fp16 x only
+
+// The 256 x 192 tile's 8 waves of 64 x 96 fit the register file only without the activation
+// staging registers (x by LDS DMA); with Q5_K's fifth bits or Q6_K's layout they still spill.
+template <int TYPE, typename XT>
+constexpr bool dma_tile_type() {
+  return sizeof(XT) == 2 && (TYPE == kQ4_K || TYPE == kQ8_0 || TYPE == kQ4_0);
+}
 
 long tile_count(const GemmGroupArgs& a, const Tile& t) {
   long columns = 0;
@@ -518,11 +591,11 @@ GemmJob make_job(const GemmGroupArgs& a, const Tile& t, int splits, void* worksp
   return job;
 }
 
-template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT, typename XT>
+template <int TYPE, int BM, int BN, int WM, int WN, int KS, typename OutT, typename XT, bool XDMA = false>
 hipError_t launch_pipe(const GemmGroupArgs& a, int splits, void* workspace, hipStream_t stream) {
   const GemmJob job = make_job(a, Tile{BM, BN, KS}, splits, workspace);
   const dim3 grid(job.tile_end[kGemmGroupMax - 1], (a.m + BM - 1) / BM, splits), block(WM * WN * 64 * KS);
-  hipLaunchKernelGGL((gemm_pipe<TYPE, BM, BN, WM, WN, KS, OutT, XT>), grid, block, 0, stream,
+  hipLaunchKernelGGL((gemm_pipe<TYPE, BM, BN, WM, WN, KS, OutT, XT, XDMA>), grid, block, 0, stream,
                      static_cast<const XT*>(a.x), job, a.m, a.k);
   if (splits > 1) {
     // four columns per thread across x; rows over y (strided past 65535 rows)
@@ -544,6 +617,10 @@ hipError_t launch_tile(const GemmGroupArgs& a, int tile, int splits, void* works
     case 6: return launch_pipe<TYPE, 64, 64, 1, 2, 2, OutT, XT>(a, splits, workspace, stream);
     case 7: return launch_pipe<TYPE, 64, 64, 1, 2, 4, OutT, XT>(a, splits, workspace, stream);
     case 8: return launch_pipe<TYPE, 256, 96, 4, 2, 1, OutT, XT>(a, splits, workspace, stream);
+    case kDmaTile:
+      if constexpr (dma_tile_type<TYPE, XT>())
+        return launch_pipe<TYPE, 256, 192, 4, 2, 1, OutT, XT, true>(a, splits, workspace, stream);
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
@@ -565,8 +642,10 @@ bool pipe_type(int type) {
 // split divide evenly into the workgroup's wave groups, each taking an even number of them (the
 // main loop runs two steps per pass) that starts on a super-block (4 steps) for the 256-element
 // encodings.
+// The LDS-DMA tile takes fp16 x and the encodings whose kernel fits the register file.
 bool valid_plan(const GemmGroupArgs& a, int tile, int splits) {
   const int steps = a.k / pipe::BK, unit = a.type == kQ8_0 || a.type == kQ4_0 ? 2 : 4;
+  if (tile == kDmaTile && (a.x_f32 || !(a.type == kQ4_K || a.type == kQ8_0 || a.type == kQ4_0))) return false;
   return tile >= 0 && tile < kTileCount && splits >= 1 && a.k % pipe::BK == 0 &&
          steps % (unit * kTiles[tile].ks * splits) == 0;
 }
@@ -589,9 +668,19 @@ constexpr long kMinBlocks = 160;
 // + up at M = 256 (192 -> 256 workgroups, one round): 70.9 -> 64.9 us and 71.1 -> 64.6 us; Q6_K
 // and Q8_0 at C4 M = 512 88.4 -> 79.9 and 79.2 -> 67.0 us; at M = 2048 (three rounds against
 // four) the 128-column tile stays (229.7 against 257.4 us).
+//
+// 256 x 192 (x by LDS DMA) steps take 1.38 of a 256 x 128 step (Q4_K, M = 1024 / 2048 / 4096 in
+// one / two / four rounds: 1.63 against 1.19 us per step) for 1.5 times its columns; it wins
+// where it needs fewer rounds: C4 at M = 2048 227.7 -> 207.4 us (Q8_0 244.0 -> 240.2, Q4_0 228.5
+// -> 220.3), M = 1024 126.1 -> 105.7 us (one round against two of 256 x 96), M = 4096 452.1 ->
+// 415.0 us; at M = 1536 (two rounds against three of 256 x 96) 197.0 against 190.6 us, so the
+// model keeps 256 x 96 there.
 int wide_tile(const GemmGroupArgs& a) {
-  const long rounds0 = (tile_count(a, kTiles[0]) + 255) / 256, rounds8 = (tile_count(a, kTiles[8]) + 255) / 256;
-  return rounds8 * 84 < rounds0 * 100 ? 8 : 0;
+  const auto rounds = [&](int tile) { return (tile_count(a, kTiles[tile]) + 255) / 256; };
+  const long cost0 = rounds(0) * 119, cost8 = rounds(8) * 99;  // rounds x step time (10 ns)
+  const long cost9 = valid_plan(a, kDmaTile, 1) ? rounds(kDmaTile) * 163 : cost0 + 1;
+  if (cost9 < cost0 && cost9 < cost8) return kDmaTile;
+  return rounds(8) * 84 < rounds(0) * 100 ? 8 : 0;
 }
 
 int base_tile(const GemmGroupArgs& a) {

@@ -445,6 +445,7 @@ def test_gemm_parity_baseline_shapes(hip_device, c_oracle, encoding, m, n, k):
 @pytest.mark.parametrize("encoding,m,n,k", [
     ("q4_k", 512, 2304, 4096),    # 256 x 128 tiles, ragged last N tile
     ("q6_k", 300, 1000, 12288),   # K split inside the workgroup, ragged M and N
+    ("q4_k", 1000, 12200, 512),   # 256 x 192 tiles, x by LDS DMA, ragged M and N
 ])
 def test_gemm_input_families_and_graph_replay(hip_device, encoding, m, n, k):
     """The reference's prefill qualification (benchmark.py:499-555): one captured graph
@@ -554,6 +555,7 @@ def test_c5_layer_chained_in_one_graph(hip_device, c_oracle, m):
     (256, 9984, 1024),   # 64x64, K split 4
     (300, 11000, 512),   # 256x96 (one round of 230 workgroups against 172 of 256x128), ragged M and N
     (512, 14000, 512),   # 256x128 (256x96 would need a second round)
+    (1000, 12200, 512),  # 256x192 with x by LDS DMA for Q4_K / Q8_0 / Q4_0 (one round against two), ragged
 ])
 def test_gemm_tile_configurations(hip_device, c_oracle, encoding, m, n, k):
     """Shapes that select each workgroup tile and K split of the prefill kernel."""

@@ -718,6 +718,25 @@ def detail_cases(device):
                 b.release()
             return result
 
+    # The Q8_1-activation integer-dot GEMV (GGML's path; fp32 x quantized in each workgroup,
+    # fp16 out) at BASELINE decode shapes, weights rotated: beside the fp32-decode kernels above
+    for encoding, m, n, k in (("q8_0", 1, 4096, 4096), ("q4_k", 1, 12288, 4096), ("q6_k", 1, 4096, 12288),
+                              ("q4_k", 4, 12288, 4096)):
+        @add(f"q8_1_{encoding}_m{m}_{n}x{k}")
+        def q8_1_decode(encoding=encoding, m=m, n=n, k=k):
+            copies = copies_for(weight_bytes(encoding, n, k))
+            x = device.from_numpy(cases.activation(m, k, 5).astype(np.float32))
+            weights = rotated(device, cases.weight(n, k, encoding, 6), copies)
+            out = device.empty((m, n), "float16")
+            exe = device.load("gguf_gemv_q8_1", encoding=encoding, out_dtype="float16", x_dtype="float32")
+            calls = [exe.bind(x, w, out) for w in weights]
+            stats = time_launches(device, [calls[i % copies].launch for i in range(60)], per=60)
+            result = dict(stats, **rate(stats, gemv_bytes(encoding, m, n, k, 2, 4), "GB/s"), copies=copies)
+            result["hbm_frac"] = round(result["GB/s"] / HBM_PEAK_GBS, 4)
+            for b in [x, out, *weights]:
+                b.release()
+            return result
+
     # The showcase's packed call at its own shapes (N = K = 1024, M in {1, 32}, fp32 x and out,
     # benchmark.py:122-126, :460-464), hot-cache as the reference times it (one weight copy).
     for encoding in ("q4_0", "q4_k", "q6_k"):

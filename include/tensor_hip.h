@@ -192,6 +192,19 @@ int32_t tensor_gguf_gemm_tile_v1(int32_t tile, int32_t *bm, int32_t *bn, int32_t
 int32_t tensor_gguf_gemm_group_plan_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 
 /*
+ * Decode GEMV on Q8_1-quantized activations with integer dot products, GGML's path for quantized
+ * matrix-vector products, which the reference measures as its external GGML baseline
+ * (benchmarks/kernels/showcase/external_baselines.py:24-58: "GGML may quantize F32 activations
+ * to Q8_1", qualified at relative L2 <= 0.02 against the fp32 oracle).  Arguments [x, w, out,
+ * type]: x fp16 or fp32 [M, K] (M <= TENSOR_GGUF_GEMV_MAX_M, M * K <= 98304), w the raw rows of
+ * a Q4_0, Q8_0, Q4_K or Q6_K matrix, out fp16 or fp32 [M, N].  x is quantized in blocks of 32
+ * (d = max|x| / 127, q = roundf(x / d), d and s = d * sum(q) kept as fp16); each weight block's
+ * codes meet the activation codes in int32 dot products, scaled per block in fp32.  An
+ * alternative to tensor_gguf_gemv_v1, whose numerics are the reference's fp32 decode.
+ */
+int32_t tensor_gguf_gemv_q8_1_v1(const TensorCallV1 *call, TensorErrorV1 *error);
+
+/*
  * The multi-row plan tensor_gguf_gemv_v1 takes for a Q4_K call with 2 <= m <= 8 rows: the kernel
  * (0 sector-aligned tiles with x staged in LDS, 1 multi-tile with x in LDS, 2 x read per wave)
  * and its two launch fields (kernel 0: 16-row tiles per workgroup 1-3 and 1 to stage x before

@@ -27,6 +27,7 @@ KERNELS = (
     "tensor_gguf_gemv_group_v1",
     "tensor_gguf_gemv_swiglu_v1",
     "tensor_gguf_gemv_variant_v1",
+    "tensor_gguf_gemv_q8_1_v1",
     "tensor_gguf_dequant_v1",
 )
 

@@ -65,6 +65,11 @@ bool gemv_q4k_plan(const GemvArgs& args, GemvPlan* plan);
 bool gemv_q4k_plan_fits(const GemvArgs& args, const GemvPlan& plan);
 // Launch a plan that fits (hipErrorInvalidValue otherwise).
 hipError_t launch_gemv_q4k_plan(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream);
+// Decode GEMV on Q8_1-quantized activations with integer dot products (GGML's path), Q4_0,
+// Q8_0, Q4_K and Q6_K, M <= 8, fp16 or fp32 x (args.x_f32); x is quantized inside each
+// workgroup, so M * K is bounded by LDS.
+bool gemv_q8_1_supported(const GemvArgs& args);
+hipError_t launch_gemv_q8_1(const GemvArgs& args, hipStream_t stream);
 // Decode GEMV with the SwiGLU epilogue of an MLP: out = silu(x W_gate^T) * (x W_up^T),
 // args.w the gate matrix, w_up the up matrix of the same shape and encoding.
 hipError_t launch_gemv_swiglu(const GemvArgs& gate, const void* w_up, hipStream_t stream);

@@ -343,6 +343,42 @@ int32_t check_u32(const TensorArgumentV1& arg, const char* name, uint64_t* value
   return TENSOR_OK;
 }
 
+// The Q8_1-activation integer-dot decode GEMV: [x, w, out, type], x fp16 or fp32 [M, K].
+int32_t gemv_q8_1_call(const TensorCallV1* call, TensorErrorV1* error) {
+  ok(error);
+  if (int32_t s = check_call(call, 4, error)) return s;
+  const int ordinal = call->stream.device_ordinal;
+  const TensorArgumentV1* a = call->arguments;
+  Format format;
+  if (int32_t s = check_type(a[3], &format, error)) return s;
+  if (int32_t s = check_matrix(a[0], "x", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT32, error)) return s;
+  if (int32_t s = check_matrix(a[1], "w", ordinal, TENSOR_UINT8, TENSOR_UINT8, error)) return s;
+  if (int32_t s = check_matrix(a[2], "out", ordinal, TENSOR_FLOAT16, TENSOR_FLOAT32, error)) return s;
+  const int64_t m = a[0].buffer.shape[0], k = a[0].buffer.shape[1], n = a[1].buffer.shape[0];
+  if (k % format.qk || a[1].buffer.shape[1] != k / format.qk * format.bytes)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "w: shape, stride or size mismatch");
+  if (a[2].buffer.shape[0] != m || a[2].buffer.shape[1] != n)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "out: shape, stride or size mismatch");
+  tensor_gguf::GemvArgs args;
+  args.x = reinterpret_cast<const void*>(a[0].buffer.address);
+  args.w = reinterpret_cast<const void*>(a[1].buffer.address);
+  args.out = reinterpret_cast<void*>(a[2].buffer.address);
+  args.type = (int)a[3].scalar;
+  args.m = (int)m;
+  args.n = (int)n;
+  args.k = (int)k;
+  args.out_half = a[2].dtype == TENSOR_FLOAT16;
+  args.x_f32 = a[0].dtype == TENSOR_FLOAT32;
+  if (!tensor_gguf::gemv_q8_1_supported(args))
+    return fail(error, TENSOR_ERROR_ARGUMENT,
+                "Q8_1 activation GEMV takes Q4_0, Q8_0, Q4_K or Q6_K, M <= %d and M * K <= 98304",
+                tensor_gguf::kGemvMaxM);
+  if (int32_t s = check_device(call, error)) return s;
+  hipError_t status = tensor_gguf::launch_gemv_q8_1(args, reinterpret_cast<hipStream_t>(call->stream.handle));
+  if (status != hipSuccess) return hip_fail(error, status, "GGUF Q8_1 GEMV launch");
+  return TENSOR_OK;
+}
+
 // The multi-row Q4_K decode GEMV on a plan the caller names: [x, w, out, type, kernel, a, b]
 // (the plan fields of tensor_gguf::GemvPlan as uint32 scalars).
 int32_t gemv_variant_call(const TensorCallV1* call, TensorErrorV1* error) {
@@ -663,6 +699,10 @@ int32_t tensor_gguf_gemv_plan_v1(uint32_t type, int64_t m, int64_t k, int64_t n,
   *a = plan.a;
   *b = plan.b;
   return ok(error);
+}
+
+int32_t tensor_gguf_gemv_q8_1_v1(const TensorCallV1* call, TensorErrorV1* error) {
+  return gemv_q8_1_call(call, error);
 }
 
 int32_t tensor_gguf_gemv_variant_v1(const TensorCallV1* call, TensorErrorV1* error) {

@@ -30,9 +30,11 @@ ENTRYPOINTS = {
     "gguf_gemm_group_plan": "tensor_gguf_gemm_group_plan_v1",
     "gguf_gemv_swiglu": "tensor_gguf_gemv_swiglu_v1",
     "gguf_gemv_variant": "tensor_gguf_gemv_variant_v1",
+    "gguf_gemv_q8_1": "tensor_gguf_gemv_q8_1_v1",
     "gguf_dequant": "tensor_gguf_dequant_v1",
 }
 GEMV_GROUP_MAX = 3  # TENSOR_GGUF_GEMV_GROUP_MAX
+Q8_1_TYPES = (2, 8, 12, 14)  # encodings of gguf_gemv_q8_1: Q4_0, Q8_0, Q4_K, Q6_K
 OUT_DTYPES = ("float16", "float32")
 
 
@@ -117,7 +119,9 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
     with two more scalars, ``tile`` and ``splits``, naming the plan it runs (plan sweeps: see
     ``Device.gemm_plan``); every other kernel takes no ``count``.
     ``gguf_gemv_swiglu`` takes ``[x, w_gate, w_up, out, type]`` and stores
-    silu(x W_gate^T) * (x W_up^T).  ``gguf_gemv_variant`` (Q4_K, 2 <= M <= 8) is ``gguf_gemv``
+    silu(x W_gate^T) * (x W_up^T).  ``gguf_gemv_q8_1`` (Q4_0, Q8_0, Q4_K, Q6_K; ``x_dtype``
+    float32 by default, or float16) is the decode GEMV on Q8_1-quantized activations with
+    integer dot products (GGML's path).  ``gguf_gemv_variant`` (Q4_K, 2 <= M <= 8) is ``gguf_gemv``
     with three more scalars, ``kernel``, ``a`` and ``b``, naming the multi-row plan it runs (plan
     sweeps: see ``Device.gemv_plan``).
     """
@@ -128,8 +132,8 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
         if kernel not in ("gguf_linear", "gguf_packed") or any(v is None for v in shape) or count is not None:
             raise ValueError("m, n and k (all three) select the packed form of gguf_linear / gguf_packed")
         return packed_manifest(encoding, m, n, k, x_dtype=x_dtype or "float32", out_dtype=out_dtype or "float32")
-    if x_dtype is not None:
-        raise ValueError("x_dtype applies to the packed form (m, n, k) only")
+    if x_dtype is not None and kernel != "gguf_gemv_q8_1":
+        raise ValueError("x_dtype applies to the packed form (m, n, k) and gguf_gemv_q8_1 only")
     code = ggml_type(encoding)
     out_dtype = str(out_dtype or "float16")
     if out_dtype not in OUT_DTYPES:
@@ -168,8 +172,15 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
             type_argument,
         ]
     else:
+        x_type = "float16"
+        if kernel == "gguf_gemv_q8_1":
+            if code not in Q8_1_TYPES:
+                raise ValueError("gguf_gemv_q8_1 runs Q4_0, Q8_0, Q4_K and Q6_K")
+            x_type = str(x_dtype or "float32")
+            if x_type not in OUT_DTYPES:
+                raise ValueError(f"x_dtype must be one of {OUT_DTYPES}")
         arguments = [
-            {"name": "x", "dtype": "float16", "shape": [{"var": "M"}, {"var": "K"}], "alignment": 16},
+            {"name": "x", "dtype": x_type, "shape": [{"var": "M"}, {"var": "K"}], "alignment": 16},
             weight,
             {"name": "out", "dtype": out_dtype, "shape": [{"var": "M"}, {"var": "N"}], "alignment": 16},
             type_argument,
@@ -199,7 +210,7 @@ def manifest(kernel: str, encoding, out_dtype: str | None = None, count: int | N
         "launch": {"grid": [1, 1, 1], "block": [256, 1, 1], "shared_memory_bytes": 0},
         "ggml_type": code,
     }
-    if kernel in ("gguf_gemv", "gguf_gemv_group", "gguf_gemv_swiglu"):
+    if kernel in ("gguf_gemv", "gguf_gemv_group", "gguf_gemv_swiglu", "gguf_gemv_q8_1"):
         result["shape_domain"] = {"M": [1, GEMV_MAX_M]}
     if kernel == "gguf_gemv_variant":
         result["shape_domain"] = {"M": [2, GEMV_MAX_M]}

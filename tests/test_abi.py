@@ -618,6 +618,43 @@ def test_gemv_variant_refuses_a_plan_that_does_not_fit():
     assert call_with(4, 4096, 12288, 0, 1, 1)[0] == ERR_PROVIDER  # fits: stops at the device check
 
 
+def test_gemv_q8_1_refuses_what_it_does_not_run():
+    """tensor_gguf_gemv_q8_1_v1 checks encoding and shape before any HIP call (fake device
+    addresses; CPU only): a call it runs stops at the device check, which fails with no GPU."""
+    manifest = kernels.manifest("gguf_gemv_q8_1", "q4_k", "float32")
+    assert [a["name"] for a in manifest["arguments"]] == ["x", "w", "out", "type"]
+    assert manifest["arguments"][0]["dtype"] == "float32"
+    with pytest.raises(ValueError):
+        kernels.manifest("gguf_gemv_q8_1", "q5_k", "float32")
+
+    def call_with(m, n, k, code, x_dtype=11, block=(256, 144)):
+        qk, size = block
+        shapes = {0: (m, k), 1: (n, k // qk * size), 2: (m, n)}
+        dtypes, sizes = {0: x_dtype, 1: 3, 2: 11}, {0: 4 if x_dtype == 11 else 2, 1: 1, 2: 4}
+        keep, args = [], (abi.Argument * 4)()
+        for j in range(3):
+            shape = shapes[j]
+            arrays = ((c.c_int64 * 2)(*shape), (c.c_int64 * 2)(sizes[j] * shape[1], sizes[j]))
+            keep.append(arrays)
+            args[j].kind, args[j].dtype = 1, dtypes[j]
+            args[j].buffer = abi.BufferDescriptor(0x10000 * (j + 1), int(np.prod(shape)) * sizes[j], arrays[0],
+                                                  arrays[1], 2, dtypes[j], 10, 0)
+        args[3].kind, args[3].dtype, args[3].scalar = 2, 7, code
+        call = abi.CallDescriptor(1, 72, args, 4, 0, (c.c_uint32 * 3)(1, 1, 1), (c.c_uint32 * 3)(256, 1, 1), 0,
+                                  abi.StreamDescriptor(10, 0, 0))
+        error = abi.ErrorDescriptor()
+        status = _native.kernel("tensor_gguf_gemv_q8_1_v1")(c.byref(call), c.byref(error))
+        return status, error.message.decode()
+
+    status, message = call_with(1, 64, 4096, 13, block=(256, 176))      # Q5_K: no Q8_1 dot product
+    assert status == ERR_ARG and "Q8_1" in message
+    assert call_with(9, 64, 4096, 12)[0] == ERR_ARG                      # M > 8
+    assert call_with(8, 64, 16384, 12)[0] == ERR_ARG                     # M * K beyond the LDS
+    assert call_with(1, 64, 4096, 12)[0] == ERR_PROVIDER                 # runs: stops at the device
+    assert call_with(8, 64, 12288, 14, x_dtype=10, block=(256, 210))[0] == ERR_PROVIDER
+    assert call_with(2, 64, 1024, 2, block=(32, 18))[0] == ERR_PROVIDER  # Q4_0
+
+
 def test_gemm_forced_plan_refuses_a_plan_that_does_not_fit():
     """tensor_gguf_gemm_group_plan_v1 checks the named tile and split against the shape before any
     HIP call (fake device addresses; CPU only)."""

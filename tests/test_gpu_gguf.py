@@ -972,6 +972,44 @@ def test_gemm_group_with_a_short_workspace_splits_less(hip_device, c_oracle):
         assert R.relative_l2(got[0], expected) <= 1e-5
 
 
+@pytest.mark.parametrize("encoding", ["q4_0", "q8_0", "q4_k", "q6_k"])
+@pytest.mark.parametrize("m,n,k,x_dtype", [
+    (1, 1003, 4096, "float32"),   # ragged workgroup of rows
+    (3, 777, 2560, "float16"),    # fp16 activations, K not a multiple of 1024
+    (8, 300, 12288, "float32"),   # the most x the workgroup quantizes in LDS (M * K = 98304)
+    (1, 12288, 4096, "float32"),  # C2 gate / up
+    (1, 4096, 12288, "float16"),  # C2 / C5 down
+])
+def test_gemv_q8_1_parity(hip_device, c_oracle, encoding, m, n, k, x_dtype):
+    """The Q8_1-activation integer-dot GEMV against its CPU restatement (the same quantized
+    codes, integer sums exact, fp32 scaling up to summation order: rel-L2 <= 1e-5 and every
+    element within 2e-5 of the largest) and against the fp32 decode within the reference's GGML
+    qualification (rel-L2 <= 0.02, external_baselines.py:53)."""
+    from oracle import q8_1_ref as Q81
+
+    code = Q.ggml_type(encoding)
+    note("gemv-q8_1", encoding, m, n, k, x_dtype)
+    raw = cases.weight(n, k, encoding, 700 + m)
+    x = cases.activation(m, k, 710 + m).astype(x_dtype)
+    expected = Q81.gemv_q8_1(x.astype(np.float32), raw, code, n, k)
+    exe = hip_device.load("gguf_gemv_q8_1", encoding=encoding, out_dtype="float32", x_dtype=x_dtype)
+    xb, wb = hip_device.from_numpy(x), hip_device.from_numpy(raw)
+    out = hip_device.empty((m, n), "float32")
+    hip_device.fill_bytes(out, 0xFF)
+    exe.launch(xb, wb, out)
+    got = out.to_numpy()
+    assert not np.isnan(got).any()
+    assert R.relative_l2(got, expected) <= 1e-5
+    assert np.abs(got - expected).max() <= 2e-5 * np.abs(expected).max()
+    c_oracle.set_threads(16)
+    assert R.relative_l2(got, c_oracle.linear(x.astype(np.float32), raw, code, n, k)) <= 0.02
+    out16 = hip_device.empty((m, n), "float16")
+    hip_device.load("gguf_gemv_q8_1", encoding=encoding, out_dtype="float16", x_dtype=x_dtype).launch(xb, wb, out16)
+    assert np.array_equal(out16.to_numpy(), got.astype(np.float16))
+    for buffer in (xb, wb, out, out16):
+        buffer.release()
+
+
 @pytest.mark.parametrize("m,n,k", [(4, 2000, 4096), (3, 777, 8192), (8, 1000, 12288), (2, 40, 1280)])
 def test_gemv_every_multirow_plan_through_the_variant_entry(hip_device, c_oracle, m, n, k):
     """Every multi-row Q4_K plan the variant entry accepts at ragged shapes (fp32 out): each within

@@ -539,7 +539,7 @@ namespace {
 // Workgroup tiles of the pipelined GEMM, by index: 0..3 without a K split inside the workgroup,
 // 4..7 with two or four wave groups per workgroup (LDS holds one double-buffered stage per
 // group, so 128 x 128 and 128 x 64 take KS <= 2 and 64 x 64 KS <= 4), 8 the 256 x 96 tile (8
-// waves of 64 x 48).
+// waves of 64 x 48), 9 the 256 x 192 tile (8 waves of 64 x 96, x by LDS DMA).
 struct Tile {
   int bm, bn, ks;
 };

@@ -1010,6 +1010,35 @@ def test_gemv_q8_1_parity(hip_device, c_oracle, encoding, m, n, k, x_dtype):
         buffer.release()
 
 
+@pytest.mark.parametrize("encoding,m,n,k", [("q8_0", 1, 1, 32), ("q4_0", 2, 3, 64), ("q4_k", 2, 65, 256),
+                                            ("q6_k", 3, 9, 512)])
+def test_gemv_q8_1_edge_shapes_and_zero_blocks(hip_device, encoding, m, n, k):
+    """The smallest rows (one Q8_1 block, lane 0 alone), single output rows and activation rows
+    with all-zero blocks (d = 0, codes 0): equal to the CPU restatement, zero rows exactly zero."""
+    from oracle import q8_1_ref as Q81
+
+    code = Q.ggml_type(encoding)
+    note("gemv-q8_1-edges", encoding, m, n, k)
+    raw = cases.weight(n, k, encoding, 720)
+    x = cases.activation(m, k, 721).astype(np.float32)
+    x[0, :32] = 0.0                    # a zero block in the first row
+    if m > 1:
+        x[1] = 0.0                     # and a zero row
+    expected = Q81.gemv_q8_1(x, raw, code, n, k)
+    exe = hip_device.load("gguf_gemv_q8_1", encoding=encoding, out_dtype="float32", x_dtype="float32")
+    xb, wb = hip_device.from_numpy(x), hip_device.from_numpy(raw)
+    out = hip_device.empty((m, n), "float32")
+    hip_device.fill_bytes(out, 0xFF)
+    exe.launch(xb, wb, out)
+    got = out.to_numpy()
+    assert not np.isnan(got).any()
+    assert np.abs(got - expected).max() <= 2e-5 * max(np.abs(expected).max(), 1e-30)
+    if m > 1:
+        assert np.array_equal(got[1], np.zeros(n, np.float32))
+    for buffer in (xb, wb, out):
+        buffer.release()
+
+
 @pytest.mark.parametrize("m,n,k", [(4, 2000, 4096), (3, 777, 8192), (8, 1000, 12288), (2, 40, 1280)])
 def test_gemv_every_multirow_plan_through_the_variant_entry(hip_device, c_oracle, m, n, k):
     """Every multi-row Q4_K plan the variant entry accepts at ragged shapes (fp32 out): each within

@@ -721,7 +721,7 @@ def detail_cases(device):
     # The Q8_1-activation integer-dot GEMV (GGML's path; fp32 x quantized in each workgroup,
     # fp16 out) at BASELINE decode shapes, weights rotated: beside the fp32-decode kernels above
     for encoding, m, n, k in (("q8_0", 1, 4096, 4096), ("q4_k", 1, 12288, 4096), ("q6_k", 1, 4096, 12288),
-                              ("q4_k", 4, 12288, 4096)):
+                              ("q4_k", 4, 12288, 4096), ("q4_k", 8, 12288, 4096)):
         @add(f"q8_1_{encoding}_m{m}_{n}x{k}")
         def q8_1_decode(encoding=encoding, m=m, n=n, k=k):
             copies = copies_for(weight_bytes(encoding, n, k))

@@ -4,14 +4,15 @@
 // against the fp32 oracle): out[m, n] = sum over 32-element blocks of x[m] (quantized to Q8_1)
 // and W[n] of an integer dot product of their codes, scaled in fp32.
 //
-// A workgroup of 8 waves first quantizes all of x (M <= 8 rows) into LDS: per 32-element
-// block d = max|x| / 127, q = roundf(x * (1 / d)) (0 for an all-zero block), and the block's
-// d and s = d * sum(q), both rounded to fp16 as ggml's block_q8_1 stores them; 8 lanes per
-// block, 4 elements each; a lane's first weight bytes are requested before that, so they arrive
-// meanwhile.  Then each wave takes one weight row and its lanes take the row's blocks in turn
-// (Q4_K: 64-element quant pairs, two Q8_1 blocks; Q6_K: 32-element runs; Q8_0 / Q4_0: whole
-// blocks), the next unit's loads in flight during the current one, each meeting the M
-// activation blocks through v_dot4_i32_i8:
+// The grid is one round of resident workgroups of 8 waves.  Each first quantizes all of x
+// (M <= 8 rows) into LDS: per 32-element block d = max|x| / 127, q = roundf(x * (1 / d)) (0 for
+// an all-zero block), and the block's d and s = d * sum(q), both rounded to fp16 as ggml's
+// block_q8_1 stores them; 8 lanes per block, 4 elements each, the loads of 8 blocks per lane
+// issued together; a lane's first weight bytes are requested before that, so they arrive
+// meanwhile.  Then each wave takes the rows r, r + S, r + 2S, ... (S waves in the grid), so x is
+// quantized once per workgroup however many rows there are, and its lanes take a row's units
+// in turn (Q4_K: 64-element quant pairs, two Q8_1 blocks; Q6_K: 32-element runs; Q8_0 / Q4_0:
+// whole blocks), each meeting the M activation blocks through v_dot4_i32_i8:
 //
 //   Q8_0  (d_w d_x) sum(q_w q_x)
 //   Q4_0  d_w (d_x sum(q_w q_x) - 8 s_x)               q_w in 0..15
@@ -23,6 +24,8 @@
 //
 // Block formats: benchmarks/kernels/showcase/triton_kernels.py:135-180 (Q4_0, Q4_K, Q6_K) and
 // the public GGML block_q8_0.
+#include <algorithm>
+
 #include "gguf_common.h"
 #include "gguf_launch.h"
 
@@ -31,6 +34,12 @@ namespace {
 
 constexpr int kQ81Waves = 8, kQ81Threads = kQ81Waves * 64;
 constexpr int kQ81MaxMK = 98304;  // int8 x codes plus two floats per block within LDS
+
+// LDS layout of the activation codes: 32-byte blocks with 16 bytes of padding after every 8, so
+// the 16 lanes of a b128 read that take consecutive blocks (or block pairs) meet 16 distinct
+// 16-byte bank groups.
+__host__ __device__ constexpr int q81_row_bytes(int nb) { return 32 * nb + 16 * ((nb + 7) >> 3); }
+__device__ __forceinline__ int q81_block(int b) { return 32 * b + 16 * (b >> 3); }
 
 __device__ __forceinline__ float group8_max(float v) {
   v = fmaxf(v, __shfl_xor(v, 1));
@@ -140,53 +149,77 @@ __global__ __launch_bounds__(kQ81Threads) void gemv_q8_1(const XT* __restrict__ 
                                                          OutT* __restrict__ out, int n, int k) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int nb = k >> 5;                            // Q8_1 blocks per activation row
-  int8_t* const qx = reinterpret_cast<int8_t*>(lds);  // [M][K] codes
-  float* const dx = reinterpret_cast<float*>(lds + M * k);
+  int8_t* const qx = reinterpret_cast<int8_t*>(lds);  // [M] rows of padded code blocks
+  const int xrow = q81_row_bytes(nb);
+  float* const dx = reinterpret_cast<float*>(lds + M * xrow);
   float* const sx = dx + M * nb;
   constexpr int ROW_BLOCK = TYPE == kQ8_0 ? 34 : TYPE == kQ4_0 ? 18 : 0;
   constexpr int ROW_SUPER = TYPE == kQ4_K ? 144 : TYPE == kQ6_K ? 210 : 0;
-  const int lane = threadIdx.x & 63, wrow = blockIdx.x * kQ81Waves + (threadIdx.x >> 6);
-  const uint8_t* const wr =
-      w + (size_t)min(wrow, n - 1) * (ROW_BLOCK ? (size_t)nb * ROW_BLOCK : (size_t)(k >> 8) * ROW_SUPER);
+  const size_t row_bytes = ROW_BLOCK ? (size_t)nb * ROW_BLOCK : (size_t)(k >> 8) * ROW_SUPER;
+  const int lane = threadIdx.x & 63, stride = gridDim.x * kQ81Waves;
+  const int row0 = blockIdx.x * kQ81Waves + (threadIdx.x >> 6);  // the wave's rows: row0, row0 + stride, ...
   const int units = Unit<TYPE>::count(k);
-  // the lane's first unit is requested before x is quantized: its bytes arrive meanwhile
+  // A lane's items, in order: for each row of the wave, its units lane, lane + 64, ...  One
+  // item at a time is held in registers: the waves resident on a CU keep the weight stream
+  // busy, and a second item's registers would cost resident waves.
+  const int per_row = (units + 63) >> 6;
+  const int total = row0 < n ? ((n - 1 - row0) / stride + 1) * per_row : 0;
+  int load_row = row0, load_j = 0;
+  auto load_next = [&](Unit<TYPE>& t) {
+    const int u = lane + 64 * load_j;
+    if (load_row < n && u < units) t.load(w + (size_t)load_row * row_bytes, u);
+    if (++load_j == per_row) {
+      load_j = 0;
+      load_row += stride;
+    }
+  };
+  // the first item is requested before x is quantized: its bytes arrive meanwhile
   Unit<TYPE> cur;
-  if (lane < units) cur.load(wr, lane);
+  load_next(cur);
   asm volatile("" ::: "memory");
 
-  // quantize x: 8 lanes per block, blocks in turn over the workgroup
-  for (int blk = threadIdx.x >> 3; blk < M * nb; blk += kQ81Threads / 8) {
-    const int part = threadIdx.x & 7, m = blk / nb, b = blk - m * nb;
-    float v[4];
-    load4x<XT>(x + (size_t)m * k + 32 * b + 4 * part, v);
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = group8_max(amax);
-    const float d = amax / 127.0f;
-    const float inv = d != 0.0f ? 1.0f / d : 0.0f;
-    int q[4], sum = 0;
+  // quantize x: 8 lanes per block, blocks in turn over the workgroup, the loads of up to
+  // kQ81Batch blocks per lane in flight together
+  constexpr int kQ81Batch = 8;
+  for (int base = threadIdx.x >> 3; base < M * nb; base += kQ81Batch * (kQ81Threads / 8)) {
+    const int part = threadIdx.x & 7;
+    float v[kQ81Batch][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      q[i] = (int)roundf(v[i] * inv);
-      sum += q[i];
+    for (int i = 0; i < kQ81Batch; ++i) {
+      const int blk = base + i * (kQ81Threads / 8);
+      if (blk < M * nb) load4x<XT>(x + (size_t)blk * 32 + 4 * part, v[i]);
     }
-    sum = group8_sum(sum);
-    *reinterpret_cast<uint32_t*>(qx + (size_t)m * k + 32 * b + 4 * part) =
-        (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
-        ((uint32_t)(q[3] & 0xFF) << 24);
-    if (part == 0) {
-      dx[blk] = (float)(_Float16)d;
-      sx[blk] = (float)(_Float16)((float)sum * d);
+#pragma unroll
+    for (int i = 0; i < kQ81Batch; ++i) {
+      const int blk = base + i * (kQ81Threads / 8);
+      if (blk >= M * nb) break;
+      const int m = blk / nb, b = blk - m * nb;
+      float amax = fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3])));
+      amax = group8_max(amax);
+      const float d = amax / 127.0f;
+      const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+      int q[4], sum = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        q[j] = (int)roundf(v[i][j] * inv);
+        sum += q[j];
+      }
+      sum = group8_sum(sum);
+      *reinterpret_cast<uint32_t*>(qx + m * xrow + q81_block(b) + 4 * part) =
+          (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
+          ((uint32_t)(q[3] & 0xFF) << 24);
+      if (part == 0) {
+        dx[blk] = (float)(_Float16)d;
+        sx[blk] = (float)(_Float16)((float)sum * d);
+      }
     }
   }
   __syncthreads();
-  if (wrow >= n) return;
 
   float acc[M];
-#pragma unroll
-  for (int m = 0; m < M; ++m) acc[m] = 0.0f;
   auto xwords = [&](int m, int b, uint32_t xw[8]) {
-    const uint4 a = *reinterpret_cast<const uint4*>(qx + (size_t)m * k + 32 * b);
-    const uint4 c = *reinterpret_cast<const uint4*>(qx + (size_t)m * k + 32 * b + 16);
+    const uint4 a = *reinterpret_cast<const uint4*>(qx + m * xrow + q81_block(b));
+    const uint4 c = *reinterpret_cast<const uint4*>(qx + m * xrow + q81_block(b) + 16);
     xw[0] = a.x; xw[1] = a.y; xw[2] = a.z; xw[3] = a.w;
     xw[4] = c.x; xw[5] = c.y; xw[6] = c.z; xw[7] = c.w;
   };
@@ -265,25 +298,46 @@ __global__ __launch_bounds__(kQ81Threads) void gemv_q8_1(const XT* __restrict__ 
       }
     }
   };
-  for (int u = lane; u < units; u += 64) {
-    Unit<TYPE> next;
-    if (u + 64 < units) next.load(wr, u + 64);
-    dot(cur, u);
-    cur = next;
-  }
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    const float v = wave_sum(acc[m]);
-    if (lane == 0) store_out<OutT>(out, (size_t)m * n + wrow, v);
+  for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+  int row = row0, j = 0;
+  for (int t = 0; t < total; ++t) {
+    const int u = lane + 64 * j;
+    if (u < units) dot(cur, u);
+    load_next(cur);
+    if (++j == per_row) {  // the row is complete
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float v = wave_sum(acc[m]);
+        if (lane == 0) store_out<OutT>(out, (size_t)m * n + row, v);
+        acc[m] = 0.0f;
+      }
+      j = 0;
+      row += stride;
+    }
   }
 }
 
+// Grid: as many workgroups as are resident at once on the 256 CUs (registers and LDS
+// permitting), each wave taking ceil(rows / waves) rows, so every workgroup quantizes x once
+// and the weight stream of its waves follows without a second round of workgroups.
 template <int TYPE, int M, typename XT, typename OutT>
 hipError_t launch_typed(const GemvArgs& a, hipStream_t stream) {
-  const size_t lds = (size_t)M * a.k + 2 * sizeof(float) * (size_t)M * (a.k >> 5);
-  hipLaunchKernelGGL((gemv_q8_1<TYPE, M, XT, OutT>), dim3((a.n + kQ81Waves - 1) / kQ81Waves), dim3(kQ81Threads), lds,
-                     stream, static_cast<const XT*>(a.x), static_cast<const uint8_t*>(a.w),
-                     static_cast<OutT*>(a.out), a.n, a.k);
+  constexpr int kCUs = 256, kLdsPerCU = 160 * 1024;
+  const size_t lds = (size_t)M * q81_row_bytes(a.k >> 5) + 2 * sizeof(float) * (size_t)M * (a.k >> 5);
+  static const int by_regs = [] {
+    int blocks = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &blocks, reinterpret_cast<const void*>(gemv_q8_1<TYPE, M, XT, OutT>), kQ81Threads, 0);
+    return e == hipSuccess && blocks > 0 ? blocks : 1;
+  }();
+  const int per_cu = std::max(1, std::min(by_regs, (int)(kLdsPerCU / std::max<size_t>(lds, 1))));
+  const long waves = (long)kCUs * per_cu * kQ81Waves;
+  const long rows_per_wave = (a.n + waves - 1) / waves;
+  const int grid = (int)((a.n + rows_per_wave * kQ81Waves - 1) / (rows_per_wave * kQ81Waves));
+  hipLaunchKernelGGL((gemv_q8_1<TYPE, M, XT, OutT>), dim3(grid), dim3(kQ81Threads), lds, stream,
+                     static_cast<const XT*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out), a.n,
+                     a.k);
   return hipGetLastError();
 }
 

@@ -979,6 +979,7 @@ def test_gemm_group_with_a_short_workspace_splits_less(hip_device, c_oracle):
     (8, 300, 12288, "float32"),   # the most x the workgroup quantizes in LDS (M * K = 98304)
     (1, 12288, 4096, "float32"),  # C2 gate / up
     (1, 4096, 12288, "float16"),  # C2 / C5 down
+    (4, 20001, 512, "float16"),   # several rows per wave, the last waves one row short
 ])
 def test_gemv_q8_1_parity(hip_device, c_oracle, encoding, m, n, k, x_dtype):
     """The Q8_1-activation integer-dot GEMV against its CPU restatement (the same quantized

@@ -212,9 +212,17 @@ template <>
 __device__ __forceinline__ void store_out<float>(float* out, size_t index, float v) {
   out[index] = v;
 }
+// fp16 of v after v has been rounded to fp32: without the empty asm the compiler folds a
+// multiply or fma that produces v into v_fma_mixlo_f16, which rounds the exact product to fp16
+// once and differs from fp32-then-fp16 rounding next to fp16 midpoints.
+__device__ __forceinline__ _Float16 fp16_of_fp32(float v) {
+  asm("" : "+v"(v));
+  return (_Float16)v;  // v_cvt_f16_f32: round to nearest even
+}
+
 template <>
 __device__ __forceinline__ void store_out<_Float16>(_Float16* out, size_t index, float v) {
-  out[index] = (_Float16)v;  // v_cvt_f16_f32: round to nearest even
+  out[index] = fp16_of_fp32(v);
 }
 
 }  // namespace tensor_gguf

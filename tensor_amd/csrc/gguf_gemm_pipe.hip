@@ -17,7 +17,12 @@
 //     load, keeping the matrix pipe fed while the VALU decodes;
 //   * XDMA (the 256 x 192 tile): the activation tile goes from global memory
 //     straight to LDS (global_load_lds_dwordx4, three swizzled buffers), which
-//     frees the staging registers the wider tile needs.
+//     frees the staging registers the wider tile needs; half of its waves issue
+//     a step's MFMAs before their dequant and half after, so the two waves of a
+//     SIMD overlap matrix and vector work (ping-pong);
+//   * Q4_K / Q5_K with four threads per weight row: the four lanes of a row (a
+//     DPP quad) each decode one of the step's four scale factors and share them
+//     by quad broadcasts, instead of each decoding all four.
 //
 // Weights are dequantized with the reference's fp32 arithmetic (every product
 // exact, one rounding) and converted to fp16 with round-to-nearest-even, so
@@ -38,7 +43,7 @@ namespace tensor_gguf {
 namespace pipe {
 
 constexpr int BK = 64, ROW = 80;  // halves per LDS row (16-byte aligned, padded)
-constexpr float kTwo24 = 16777216.0f;
+constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
 
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
   const _Float16 ha = (_Float16)a, hb = (_Float16)b;
@@ -154,7 +159,8 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
   _Float16* const ws0 = XDMA ? xs0 + 3 * XS : xs1 + BM * ROW;
   _Float16* const ws1 = ws0 + BN * ROW;
 
-  const int tid = threadIdx.x % THREADS, lane = tid & 63, wave = tid >> 6;
+  // the wave index in a scalar register: the wave's tile offsets then take no vector registers
+  const int tid = threadIdx.x % THREADS, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = (wave / WN) * (16 * MT), wn = (wave % WN) * (16 * NT);
   // the matrix of this column tile (workgroup-uniform)
   const int tile = blockIdx.x;
@@ -163,14 +169,16 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
   const int m0 = blockIdx.y * BM, n0 = (tile - (mi ? job.tile_end[mi - 1] : 0)) * BN;
   int wrow[PARTS], wpart[PARTS];
   bool has[PARTS];
-  const uint8_t* wbase[PARTS];
+  // weight rows as 32-bit byte offsets from the matrix base (matrices stay under 4 GiB)
+  const uint8_t* const wmat = job.w[mi];
+  uint32_t wbase[PARTS];
 #pragma unroll
   for (int p = 0; p < PARTS; ++p) {
     const int part = tid + p * THREADS;
     has[p] = part < BN * TPR;
     wrow[p] = has[p] ? part / TPR : 0;
     wpart[p] = part % TPR;
-    wbase[p] = job.w[mi] + (size_t)min(n0 + wrow[p], N - 1) * (size_t)(K / QK) * BYTES;
+    wbase[p] = (uint32_t)min(n0 + wrow[p], N - 1) * (uint32_t)((K / QK) * BYTES);
   }
   // this group's steps of this split; the host guarantees that every group takes an even number
   // of steps and (for the 256-element encodings) starts on a super-block
@@ -180,20 +188,22 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
   // XDMA: DMA source rows of this lane.  Block b = XPW wave + i of the x tile (1 KB, 8 rows of
   // 128 B) goes to LDS lane-linear: lane l writes 16 B at 16 l, row 8 b + l / 8, slot l % 8, which
   // holds chunk (l % 8) ^ ((row >> 1) & 7) of the row, so a 16-row fragment read hits 16 bank groups
-  const XT* xsrc[XDMA ? XPW : 1];
+  // as 32-bit byte offsets from the tile's first row (M * K * 2 stays under 4 GiB)
+  const uint8_t* const xtile = reinterpret_cast<const uint8_t*>(x + (size_t)m0 * K);
+  uint32_t xsrc[XDMA ? XPW : 1];
   if constexpr (XDMA) {
 #pragma unroll
     for (int i = 0; i < XPW; ++i) {
       const int r = 8 * (XPW * wave + i) + (lane >> 3);
       const int cch = (lane & 7) ^ ((r >> 1) & 7);
-      xsrc[i] = x + (size_t)min(m0 + r, M - 1) * K + 8 * cch;
+      xsrc[i] = 2u * ((uint32_t)(min(m0 + r, M - 1) - m0) * (uint32_t)K + 8 * cch);
     }
   }
   auto dma = [&](int step, _Float16* xbuf) {
     if constexpr (XDMA) {
 #pragma unroll
       for (int i = 0; i < XPW; ++i)
-        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(xsrc[i] + step * BK),
+        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(xtile + (xsrc[i] + (uint32_t)(2 * step * BK))),
                                          (void __attribute__((address_space(3)))*)(xbuf + (XPW * wave + i) * 512),
                                          16, 0, 0);
     }
@@ -220,7 +230,7 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
 #pragma unroll
     for (int p = 0; p < PARTS; ++p) {
       if (!has[p]) continue;
-      const uint8_t* blk = wbase[p] + (size_t)(k0 / QK) * BYTES;
+      const uint8_t* blk = wmat + (wbase[p] + (uint32_t)((k0 / QK) * BYTES));
       typename RawT::AV& ra = r.a[p];
       typename RawT::BV& rb = r.b[p];
       if constexpr (B32) {
@@ -291,36 +301,58 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
             *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(u & 0x00FF00FFu, (u >> 8) & 0x00FF00FFu, d24, bias);
           }
         } else {
-          // (q - 8) * d: byte j's low nibble is element j, its high nibble element j + 16
-          const float d24 = d * kTwo24, bias = -8.0f * d;
+          // (q - 8) * d: byte j's low nibble is element j, its high nibble element j + 16 (left in
+          // bits 4-7 of its half, 16 q * 2^-24, against d 2^20)
+          const float d24 = d * kTwo24, d20 = d * kTwo20, bias = -8.0f * d;
 #pragma unroll
           for (int i = 0; i < G::W0; ++i) {
-            const uint32_t q = ra[i];
-            *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(q & 0x000F000Fu, (q >> 8) & 0x000F000Fu, d24, bias);
-            *reinterpret_cast<uint2*>(dst + 16 + 4 * i) =
-                affine4((q >> 4) & 0x000F000Fu, (q >> 12) & 0x000F000Fu, d24, bias);
+            const uint32_t q = ra[i], q8 = q >> 8;
+            *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(q & 0x000F000Fu, q8 & 0x000F000Fu, d24, bias);
+            *reinterpret_cast<uint2*>(dst + 16 + 4 * i) = affine4(q & 0x00F000F0u, q8 & 0x00F000F0u, d20, bias);
           }
         }
       } else if constexpr (KQ) {
-        int sc_lo, mn_lo, sc_hi, mn_hi;
-        q4k_scale_pair(rb[1], rb[2], rb[3], step & 3, sc_lo, mn_lo, sc_hi, mn_hi);
-        const float d = half_bits_to_float(rb[0]), dmin = half_bits_to_float(rb[0] >> 16);
-        // d*sc*q - dmin*m: the product is exact, the subtraction rounds once
-        const float ds_lo = d * (float)sc_lo * kTwo24, dm_lo = -(dmin * (float)mn_lo);
-        const float ds_hi = d * (float)sc_hi * kTwo24, dm_hi = -(dmin * (float)mn_hi);
+        // d*sc*q - dmin*m: the product is exact, the subtraction rounds once; high nibbles stay in
+        // bits 4-7 of their halves (16 q * 2^-24), so their scale takes 2^20
+        float ds_lo, dm_lo, ds_hi, dm_hi;
+        if constexpr (TPR == 4) {
+          // the four lanes of a row (a DPP quad) each decode one of the step's four factors,
+          // lane f: f & 2 picks sub-block 2j + 1, f & 1 the min, and share them by broadcasts
+          const int f = lane & 3, jj = step & 3, t = 2 * (jj & 1) + (f >> 1);
+          const uint32_t word = f & 1 ? rb[2] : rb[1];
+          const uint32_t low6 = (word >> (8 * t)) & 63u;  // sub-blocks 0-3
+          const uint32_t split = ((rb[3] >> (8 * t + 4 * (f & 1))) & 15u) | (((word >> (8 * t + 6)) & 3u) << 4);
+          const uint32_t code = jj < 2 ? low6 : split;
+          const float lane_scale = f & 1 ? -1.0f : (f & 2 ? kTwo20 : kTwo24);
+          const float v = half_bits_to_float(rb[0] >> (16 * (f & 1))) * lane_scale * (float)code;
+          const int vi = __builtin_bit_cast(int, v);
+          ds_lo = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(vi, 0x00, 0xF, 0xF, false));
+          dm_lo = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(vi, 0x55, 0xF, 0xF, false));
+          ds_hi = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(vi, 0xAA, 0xF, 0xF, false));
+          dm_hi = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(vi, 0xFF, 0xF, 0xF, false));
+        } else {
+          int sc_lo, mn_lo, sc_hi, mn_hi;
+          q4k_scale_pair(rb[1], rb[2], rb[3], step & 3, sc_lo, mn_lo, sc_hi, mn_hi);
+          const float d = half_bits_to_float(rb[0]), dmin = half_bits_to_float(rb[0] >> 16);
+          ds_lo = d * (float)sc_lo * kTwo24;
+          dm_lo = -(dmin * (float)mn_lo);
+          ds_hi = d * (float)sc_hi * kTwo20;
+          dm_hi = -(dmin * (float)mn_hi);
+        }
         _Float16* dst = &ws[wrow[p] * ROW + G::QB * wpart[p]];
 #pragma unroll
         for (int i = 0; i < G::W0; ++i) {
           const uint32_t q = ra[i];  // low nibbles: sub-block 2j, high nibbles: 2j+1
-          uint32_t lo02 = q & 0x000F000Fu, lo13 = (q >> 8) & 0x000F000Fu;
-          uint32_t hi02 = (q >> 4) & 0x000F000Fu, hi13 = (q >> 12) & 0x000F000Fu;
+          const uint32_t q8 = q >> 8;
+          uint32_t lo02 = q & 0x000F000Fu, lo13 = q8 & 0x000F000Fu;
+          uint32_t hi02 = q & 0x00F000F0u, hi13 = q8 & 0x00F000F0u;
           if constexpr (TYPE == kQ5_K) {
             // fifth bits: bit 2j (sub-block 2j) and 2j+1 of the qh byte at the quant byte's position
             const uint32_t h = rb[4 + i] >> (2 * (step & 3));
             lo02 |= (h & 0x00010001u) << 4;
             lo13 |= ((h >> 8) & 0x00010001u) << 4;
-            hi02 |= ((h >> 1) & 0x00010001u) << 4;
-            hi13 |= ((h >> 9) & 0x00010001u) << 4;
+            hi02 |= ((h >> 1) & 0x00010001u) << 8;
+            hi13 |= ((h >> 9) & 0x00010001u) << 8;
           }
           *reinterpret_cast<uint2*>(dst + 4 * i) = affine4(lo02, lo13, ds_lo, dm_lo);
           *reinterpret_cast<uint2*>(dst + 32 + 4 * i) = affine4(hi02, hi13, ds_hi, dm_hi);
@@ -373,15 +405,39 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
       for (int j = 0; j < NT; ++j)
         b[kk][j] = *reinterpret_cast<const half8_t*>(&ws[(wn + 16 * j + (lane & 15)) * ROW + koff]);
     }
-    store(staged, xn, wnext, staged_step);
     if constexpr (XDMA) {
       // the x DMA of the fetched step is issued ahead of its weight loads and the order is pinned:
       // loads complete in order, so once a wave's dequant has waited on those weights (the next
-      // step's store), its DMA'd x has landed too, before the barrier that follows
+      // step's store), its DMA'd x has landed too, before the barrier that follows.
+      // Ping-pong: the upper half of the waves (one weight part each) issue their MFMAs before
+      // they dequantize, the lower half (two parts) after, so the two waves that share a SIMD
+      // keep its matrix pipe and its VALU busy at the same time.
+      auto mfma_all = [&]() {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[kk][i], b[kk][j], acc[i][j], 0, 0, 0);
+      };
+      const bool mfma_first = wave >= WM * WN / 2;
+      if (mfma_first) {
+        mfma_all();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      store(staged, xn, wnext, staged_step);
       dma(fetch_step, xdma);
       asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
+      load(fetched, fetch_step);
+      if (!mfma_first) {
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_all();
+      }
+      return;
     }
+    store(staged, xn, wnext, staged_step);
     load(fetched, fetch_step);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
@@ -419,10 +475,14 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
     for (int step = first; step < first + steps; step += 2) {
       const int c1 = cur == 2 ? 0 : cur + 1, c2 = c1 == 2 ? 0 : c1 + 1;
       step_body(xs0 + cur * XS, ws0, nullptr, ws1, rb, step + 1, ra, min(step + 2, last), xs0 + c2 * XS);
+      __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
       const int c3 = c2 == 2 ? 0 : c2 + 1;
       step_body(xs0 + c1 * XS, ws1, nullptr, ws0, ra, min(step + 2, last), rb, min(step + 3, last), xs0 + c3 * XS);
+      __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
       cur = c2;
     }
   } else {

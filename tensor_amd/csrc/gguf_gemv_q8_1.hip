@@ -209,8 +209,8 @@ __global__ __launch_bounds__(kQ81Threads) void gemv_q8_1(const XT* __restrict__ 
           (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
           ((uint32_t)(q[3] & 0xFF) << 24);
       if (part == 0) {
-        dx[blk] = (float)(_Float16)d;
-        sx[blk] = (float)(_Float16)((float)sum * d);
+        dx[blk] = (float)fp16_of_fp32(d);
+        sx[blk] = (float)fp16_of_fp32((float)sum * d);
       }
     }
   }

@@ -611,6 +611,31 @@ def test_gemm_one_hot_rows_give_dequantized_weights(hip_device, c_oracle, encodi
     assert np.array_equal(got, deq[:, perm].T), encoding
 
 
+@pytest.mark.parametrize("encoding", ["q4_k", "q8_0", "q4_0"])
+@pytest.mark.parametrize("tile", [0, 8, 9])
+def test_gemm_one_hot_rows_on_the_256_row_tiles(hip_device, c_oracle, encoding, tile):
+    """The one-hot check through the plan entry on the 256-row tiles, the 256 x 192 LDS-DMA tile
+    (half its waves multiply before they dequantize) among them: out[m, n] equals
+    fp16(dequant(W))[n, perm[m]] bit for bit, at a ragged N."""
+    k, n = 512, 1000
+    code = Q.ggml_type(encoding)
+    note("gemm-one-hot-256", encoding, tile)
+    raw = cases.random_blocks(encoding, n, k, 98)
+    deq = c_oracle.dequantize(raw, code, n, k).astype(np.float16).astype(np.float32)
+    perm = np.random.default_rng(99).permutation(k)
+    x = np.zeros((k, k), np.float16)
+    x[np.arange(k), perm] = 1.0
+    exe = hip_device.load("gguf_gemm_group_plan", encoding=encoding, out_dtype="float32", count=1)
+    xb, wb = hip_device.from_numpy(x), hip_device.from_numpy(raw)
+    out = hip_device.empty((k, n), "float32")
+    workspace = hip_device.empty((256,), "uint8")
+    hip_device.fill_bytes(out, 0xFF)
+    exe.launch(xb, wb, out, workspace, tile=tile, splits=1)
+    assert np.array_equal(out.to_numpy(), deq[:, perm].T), (encoding, tile)
+    for buffer in (xb, wb, out, workspace):
+        buffer.release()
+
+
 @pytest.mark.parametrize("encoding,m,n,k,x_dtype", [
     ("q4_0", 2, 1000, 1056, "float32"),    # ragged N, a last half chunk of K (K % 64 == 32)
     ("q8_0", 33, 8200, 1056, "float32"),   # three M tiles, two 16-row tiles per workgroup

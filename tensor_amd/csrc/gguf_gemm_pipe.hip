@@ -729,16 +729,16 @@ constexpr long kMinBlocks = 160;
 // and Q8_0 at C4 M = 512 88.4 -> 79.9 and 79.2 -> 67.0 us; at M = 2048 (three rounds against
 // four) the 128-column tile stays (229.7 against 257.4 us).
 //
-// 256 x 192 (x by LDS DMA) steps take 1.38 of a 256 x 128 step (Q4_K, M = 1024 / 2048 / 4096 in
-// one / two / four rounds: 1.63 against 1.19 us per step) for 1.5 times its columns; it wins
-// where it needs fewer rounds: C4 at M = 2048 227.7 -> 207.4 us (Q8_0 244.0 -> 240.2, Q4_0 228.5
-// -> 220.3), M = 1024 126.1 -> 105.7 us (one round against two of 256 x 96), M = 4096 452.1 ->
-// 415.0 us; at M = 1536 (two rounds against three of 256 x 96) 197.0 against 190.6 us, so the
-// model keeps 256 x 96 there.
+// 256 x 192 (x by LDS DMA, ping-pong waves) steps take 1.3 of a 256 x 128 step and 1.5 of a
+// 256 x 96 one (Q4_K, timing harness: 1.50-1.54 against 1.12 and 0.97-0.99 us per step at
+// M = 1024 / 2048) for 1.5 and 2 times their columns; it wins where it needs fewer rounds: C4 at
+// M = 2048 214.7 (256 x 128) -> 192.6 us, M = 1024 124.6 (256 x 96) -> 98.3 us, and at M = 1536
+// (two rounds, the second half full, against three of 256 x 96) 200.2 -> 185.6 us; at M = 512
+// (half a round) it takes 84 us against 63 on 256 x 96.
 int wide_tile(const GemmGroupArgs& a) {
   const auto rounds = [&](int tile) { return (tile_count(a, kTiles[tile]) + 255) / 256; };
   const long cost0 = rounds(0) * 119, cost8 = rounds(8) * 99;  // rounds x step time (10 ns)
-  const long cost9 = valid_plan(a, kDmaTile, 1) ? rounds(kDmaTile) * 163 : cost0 + 1;
+  const long cost9 = valid_plan(a, kDmaTile, 1) ? rounds(kDmaTile) * 145 : cost0 + 1;
   if (cost9 < cost0 && cost9 < cost8) return kDmaTile;
   return rounds(8) * 84 < rounds(0) * 100 ? 8 : 0;
 }

@@ -537,6 +537,7 @@ def test_gemm_plan_query_names_the_library_plans_at_the_baseline_shapes():
 
     assert plan(12, 512, 4096, [12288]) == (8, 1, True)            # C4 M=512: 256 x 96, one round
     assert plan(12, 2048, 4096, [12288]) == (9, 1, True)           # C4 M=2048: 256 x 192, x by LDS DMA
+    assert plan(12, 1536, 4096, [12288]) == (9, 1, True)           # two rounds of 256 x 192 against three
     assert plan(12, 256, 4096, [4096, 1024, 1024]) == (0, 4, True)  # C5 q + k + v, K split 4 ways
     assert plan(12, 256, 4096, [4096]) == (7, 1, True)             # C5 o: 64 x 64, K over 4 wave groups
     assert plan(12, 256, 4096, [12288, 12288]) == (8, 1, True)     # C5 gate + up

@@ -318,10 +318,12 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
         if constexpr (TPR == 4) {
           // the four lanes of a row (a DPP quad) each decode one of the step's four factors,
           // lane f: f & 2 picks sub-block 2j + 1, f & 1 the min, and share them by broadcasts
-          const int f = lane & 3, jj = step & 3, t = 2 * (jj & 1) + (f >> 1);
-          const uint32_t word = f & 1 ? rb[2] : rb[1];
-          const uint32_t low6 = (word >> (8 * t)) & 63u;  // sub-blocks 0-3
-          const uint32_t split = ((rb[3] >> (8 * t + 4 * (f & 1))) & 15u) | (((word >> (8 * t + 6)) & 3u) << 4);
+          const int f = lane & 3, jj = step & 3, t8 = 16 * (jj & 1) + 8 * (f >> 1);
+          // the scale bytes (rb[1]) or the min bytes (rb[2]) by one byte permute
+          const uint32_t word = __builtin_amdgcn_perm(rb[2], rb[1], f & 1 ? 0x07060504u : 0x03020100u);
+          const uint32_t low6 = __builtin_amdgcn_ubfe(word, t8, 6);  // sub-blocks 0-3
+          const uint32_t split = __builtin_amdgcn_ubfe(rb[3], t8 + 4 * (f & 1), 4) |
+                                 (__builtin_amdgcn_ubfe(word, t8 + 6, 2) << 4);
           const uint32_t code = jj < 2 ? low6 : split;
           const float lane_scale = f & 1 ? -1.0f : (f & 2 ? kTwo20 : kTwo24);
           const float v = half_bits_to_float(rb[0] >> (16 * (f & 1))) * lane_scale * (float)code;

@@ -20,9 +20,9 @@
 //     frees the staging registers the wider tile needs; half of its waves issue
 //     a step's MFMAs before their dequant and half after, so the two waves of a
 //     SIMD overlap matrix and vector work (ping-pong);
-//   * Q4_K / Q5_K with four threads per weight row: the four lanes of a row (a
-//     DPP quad) each decode one of the step's four scale factors and share them
-//     by quad broadcasts, instead of each decoding all four.
+//   * Q4_K / Q5_K with four (two) threads per weight row: the lanes of a row, a
+//     DPP quad (pair), each decode one (two) of the step's four scale factors
+//     and share them by broadcasts, instead of each decoding all four.
 //
 // Weights are dequantized with the reference's fp32 arithmetic (every product
 // exact, one rounding) and converted to fp16 with round-to-nearest-even, so
@@ -332,6 +332,21 @@ __global__ __launch_bounds__(WM * WN * 64 * KS) void gemm_pipe(const XT* __restr
           dm_lo = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(vi, 0x55, 0xF, 0xF, false));
           ds_hi = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(vi, 0xAA, 0xF, 0xF, false));
           dm_hi = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(vi, 0xFF, 0xF, 0xF, false));
+        } else if constexpr (TPR == 2) {
+          // the two lanes of a row each decode the scale and min of one sub-block (lane f: 2j + f)
+          // and take the other lane's by pair broadcasts within the DPP quad
+          const int f = lane & 1, jj = step & 3, t8 = 16 * (jj & 1) + 8 * f;
+          const uint32_t sc = jj < 2 ? __builtin_amdgcn_ubfe(rb[1], t8, 6)
+                                     : __builtin_amdgcn_ubfe(rb[3], t8, 4) | (__builtin_amdgcn_ubfe(rb[1], t8 + 6, 2) << 4);
+          const uint32_t mn = jj < 2 ? __builtin_amdgcn_ubfe(rb[2], t8, 6)
+                                     : __builtin_amdgcn_ubfe(rb[3], t8 + 4, 4) | (__builtin_amdgcn_ubfe(rb[2], t8 + 6, 2) << 4);
+          const float d = half_bits_to_float(rb[0]), dmin = half_bits_to_float(rb[0] >> 16);
+          const int ds = __builtin_bit_cast(int, d * (f ? kTwo20 : kTwo24) * (float)sc);
+          const int dm = __builtin_bit_cast(int, -(dmin * (float)mn));
+          ds_lo = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(ds, 0xA0, 0xF, 0xF, false));  // lanes 0, 2
+          dm_lo = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(dm, 0xA0, 0xF, 0xF, false));
+          ds_hi = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(ds, 0xF5, 0xF, 0xF, false));  // lanes 1, 3
+          dm_hi = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(dm, 0xF5, 0xF, 0xF, false));
         } else {
           int sc_lo, mn_lo, sc_hi, mn_hi;
           q4k_scale_pair(rb[1], rb[2], rb[3], step & 3, sc_lo, mn_lo, sc_hi, mn_hi);

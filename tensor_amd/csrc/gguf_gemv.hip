@@ -460,18 +460,21 @@ static bool launch_q32_m1(const GemvArgs& a, hipStream_t stream) {
   }
 }
 
-// fp32 activations at M = 1 (the packed call form), Q8_0 and Q4_0, K a multiple of 2048:
+// fp32 activations at M = 1 (the packed call form), Q8_0 and Q4_0, K = 1024 or a multiple of 2048
+// (KB = K / 32 blocks; at K = 1024 lanes 32-63 hold no block):
 // gemv_q32_m1's lane plan and loads (lane = 32-element block, one row per wave), each code
 // converted to fp32 and multiplied by the fp32 activation (the reference's decode numerics, fp32
 // operands, benchmark.py:466-472, up to summation order); the code bias (128 for the int8 codes
 // read as unsigned bytes, 8 for the nibbles) taken off with the block's fp32 sum of x, d once
 // per block.  x sits in LDS as fp32 chunks of 4, 16 bytes of padding per 128-byte block.
-template <int TYPE, int WAVES, int STEPS, typename OutT>
+template <int TYPE, int WAVES, int KB, typename OutT>
 __global__ __launch_bounds__(WAVES * 64) void gemv_q32_m1_f32(const float* __restrict__ x, const uint8_t* __restrict__ w,
                                                               OutT* __restrict__ out, int n_rows) {
   constexpr int kBytes = TYPE == kQ8_0 ? 34 : 18;
   constexpr float kBias = TYPE == kQ8_0 ? 128.0f : 8.0f;
-  constexpr int T = WAVES * 64, K = 2048 * STEPS, BLOCKS = K / 32, CHUNKS = K / 4;
+  constexpr int STEPS = (KB + 63) / 64;
+  static_assert(KB == 32 || KB % 64 == 0, "K = 1024 or a multiple of 2048");
+  constexpr int T = WAVES * 64, K = 32 * KB, BLOCKS = KB, CHUNKS = K / 4;
   constexpr int XC = (CHUNKS + T - 1) / T;
   __shared__ __attribute__((aligned(16))) float xl[CHUNKS * 4 + BLOCKS * 4];
   __shared__ float sxl[BLOCKS];
@@ -488,7 +491,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q32_m1_f32(const float* __res
   uint4 q0[STEPS], q1[STEPS];
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
-    const uint8_t* block = wr + (lane + 64 * s) * kBytes;
+    // K = 1024: lanes past the 32 blocks read block 31 again and add nothing
+    const uint8_t* block = wr + min(lane + 64 * s, BLOCKS - 1) * kBytes;
     head[s] = load4(block);
     q0[s] = load16(block + 2);
     if constexpr (TYPE == kQ8_0) q1[s] = load16(block + 18);
@@ -513,7 +517,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q32_m1_f32(const float* __res
   float acc = 0.0f;
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
-    const int b = lane + 64 * s;
+    const int b = min(lane + 64 * s, BLOCKS - 1);
     const float* xp = &xl[36 * b];  // the block's 8 chunks (32 floats and 4 of padding per block)
     float a = 0.0f;
 #pragma unroll
@@ -534,32 +538,37 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q32_m1_f32(const float* __res
       a = fmaf((float)((codes >> 16) & 0xFF), xv.z, a);
       a = fmaf((float)(codes >> 24), xv.w, a);
     }
-    acc = fmaf(half_bits_to_float(head[s]), a - kBias * sxl[b], acc);
+    if (BLOCKS % 64 == 0 || lane + 64 * s < BLOCKS) acc = fmaf(half_bits_to_float(head[s]), a - kBias * sxl[b], acc);
   }
   const float v = wave_sum(acc);
   if (lane == 0) store_out<OutT>(out, (size_t)row, v);
 }
 
-template <int TYPE, int STEPS, typename OutT>
-static void launch_q32_m1_f32_steps(const GemvArgs& a, hipStream_t stream) {
-  constexpr int WAVES = STEPS <= 2 ? 8 : 4;
-  hipLaunchKernelGGL((gemv_q32_m1_f32<TYPE, WAVES, STEPS, OutT>), dim3((a.n + WAVES - 1) / WAVES), dim3(WAVES * 64),
+template <int TYPE, int KB, typename OutT>
+static void launch_q32_m1_f32_blocks(const GemvArgs& a, hipStream_t stream) {
+  constexpr int WAVES = KB <= 128 ? 8 : 4;
+  hipLaunchKernelGGL((gemv_q32_m1_f32<TYPE, WAVES, KB, OutT>), dim3((a.n + WAVES - 1) / WAVES), dim3(WAVES * 64),
                      0, stream, static_cast<const float*>(a.x), static_cast<const uint8_t*>(a.w),
                      static_cast<OutT*>(a.out), a.n);
 }
 
 template <int TYPE, typename OutT>
 static bool launch_q32_m1_f32(const GemvArgs& a, hipStream_t stream) {
-  if (a.m != 1 || a.k % 2048) return false;
+  if (a.m != 1) return false;
+  if (a.k == 1024) {
+    launch_q32_m1_f32_blocks<TYPE, 32, OutT>(a, stream);
+    return true;
+  }
+  if (a.k % 2048) return false;
   switch (a.k / 2048) {
-    case 1: launch_q32_m1_f32_steps<TYPE, 1, OutT>(a, stream); return true;
-    case 2: launch_q32_m1_f32_steps<TYPE, 2, OutT>(a, stream); return true;
-    case 3: launch_q32_m1_f32_steps<TYPE, 3, OutT>(a, stream); return true;
-    case 4: launch_q32_m1_f32_steps<TYPE, 4, OutT>(a, stream); return true;
-    case 5: launch_q32_m1_f32_steps<TYPE, 5, OutT>(a, stream); return true;
-    case 6: launch_q32_m1_f32_steps<TYPE, 6, OutT>(a, stream); return true;
-    case 7: launch_q32_m1_f32_steps<TYPE, 7, OutT>(a, stream); return true;
-    case 8: launch_q32_m1_f32_steps<TYPE, 8, OutT>(a, stream); return true;
+    case 1: launch_q32_m1_f32_blocks<TYPE, 64, OutT>(a, stream); return true;
+    case 2: launch_q32_m1_f32_blocks<TYPE, 128, OutT>(a, stream); return true;
+    case 3: launch_q32_m1_f32_blocks<TYPE, 192, OutT>(a, stream); return true;
+    case 4: launch_q32_m1_f32_blocks<TYPE, 256, OutT>(a, stream); return true;
+    case 5: launch_q32_m1_f32_blocks<TYPE, 320, OutT>(a, stream); return true;
+    case 6: launch_q32_m1_f32_blocks<TYPE, 384, OutT>(a, stream); return true;
+    case 7: launch_q32_m1_f32_blocks<TYPE, 448, OutT>(a, stream); return true;
+    case 8: launch_q32_m1_f32_blocks<TYPE, 512, OutT>(a, stream); return true;
     default: return false;
   }
 }

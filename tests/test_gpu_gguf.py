@@ -895,6 +895,8 @@ def test_packed_form_every_encoding(hip_device, c_oracle, encoding, x_dtype, m):
     ("q8_0", 1003, 4096),    # C1's row length
     ("q8_0", 257, 12288),
     ("q4_0", 300, 6144),
+    ("q4_0", 1024, 1024),    # the showcase's row length: 32 blocks, half of each wave's lanes
+    ("q8_0", 1001, 1024),
 ])
 def test_packed_form_fp32_x_at_decode_row_lengths(hip_device, c_oracle, encoding, n, k):
     """fp32 x at M = 1 on the packed entry at the BASELINE row lengths, where the tuned decode

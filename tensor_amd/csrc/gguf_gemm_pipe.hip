@@ -715,12 +715,27 @@ bool pipe_type(int type) {
   return type == kQ4_K || type == kQ5_K || type == kQ6_K || type == kQ8_0 || type == kQ4_0;
 }
 
+// The kernel addresses weights and the x tile by 32-bit offsets: every matrix stays under 4 GiB
+// and a 256-row x tile under 2 GiB (K <= 2^22); larger shapes take the generic kernel.
+bool offsets_fit(const GemmGroupArgs& a) {
+  if (a.k > (1 << 22)) return false;
+  const uint64_t row = a.type == kQ4_K ? (uint64_t)a.k / 256 * Block<kQ4_K>::BYTES
+                       : a.type == kQ5_K ? (uint64_t)a.k / 256 * Block<kQ5_K>::BYTES
+                       : a.type == kQ6_K ? (uint64_t)a.k / 256 * Block<kQ6_K>::BYTES
+                       : a.type == kQ8_0 ? (uint64_t)a.k / 32 * Block<kQ8_0>::BYTES
+                                         : (uint64_t)a.k / 32 * Block<kQ4_0>::BYTES;
+  for (int i = 0; i < a.count; ++i)
+    if ((uint64_t)a.n[i] * row >= (1ull << 32)) return false;
+  return true;
+}
+
 // A tile and split count that fit the shape: K is whole 64-element steps, and the steps of a
 // split divide evenly into the workgroup's wave groups, each taking an even number of them (the
 // main loop runs two steps per pass) that starts on a super-block (4 steps) for the 256-element
 // encodings.
 // The LDS-DMA tile takes fp16 x and the encodings whose kernel fits the register file.
 bool valid_plan(const GemmGroupArgs& a, int tile, int splits) {
+  if (!offsets_fit(a)) return false;
   const int steps = a.k / pipe::BK, unit = a.type == kQ8_0 || a.type == kQ4_0 ? 2 : 4;
   if (tile == kDmaTile && (a.x_f32 || !(a.type == kQ4_K || a.type == kQ8_0 || a.type == kQ4_0))) return false;
   return tile >= 0 && tile < kTileCount && splits >= 1 && a.k % pipe::BK == 0 &&

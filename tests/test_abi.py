@@ -543,6 +543,9 @@ def test_gemm_plan_query_names_the_library_plans_at_the_baseline_shapes():
     assert plan(12, 256, 4096, [12288, 12288]) == (8, 1, True)     # C5 gate + up
     assert plan(14, 256, 12288, [4096]) == (0, 8, True)            # C5 down (Q6_K), K split 8 ways
     assert plan(14, 256, 12288, [4096], workspace=0) == (7, 1, True)  # no workspace: no split
+    # the pipelined kernels address a matrix by 32-bit offsets: 4 GiB and up takes the generic one
+    assert plan(12, 256, 4096, [1_800_000])[2] is True               # 3.86 GiB
+    assert plan(12, 256, 4096, [1_900_000])[2] is False              # 4.08 GiB
     error = abi.ErrorDescriptor()
     assert lib.tensor_gguf_gemm_tile_v1(len(tiles), c.byref(c.c_int32()), c.byref(c.c_int32()),
                                         c.byref(c.c_int32()), c.byref(error)) == ERR_ARG

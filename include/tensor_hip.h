@@ -65,6 +65,11 @@ extern "C" {
  *   3 type scalar uint32 GGML type id
  * Buffers: device type TENSOR_DEVICE_ROCM, the stream's ordinal, 16-byte
  * aligned addresses, contiguous byte strides.
+ * Q4_K at 4 <= M <= 8 with rows whose x does not fit in LDS (plan kernel 3 of
+ * tensor_gguf_gemv_plan_v1, e.g. M = 8, K = 12288) splits K across workgroups: its fp32 partial
+ * sums go to the library's static scratch (the array of tensor_gguf_gemm_group_noalloc_v1), so
+ * such calls share it with that entry and follow its rules: eager calls on different streams
+ * take it in turn, replays of captured graphs that overlap on one GPU race.
  */
 int32_t tensor_gguf_gemv_v1(const TensorCallV1 *call, TensorErrorV1 *error);
 
@@ -206,10 +211,11 @@ int32_t tensor_gguf_gemv_q8_1_v1(const TensorCallV1 *call, TensorErrorV1 *error)
 
 /*
  * The multi-row plan tensor_gguf_gemv_v1 takes for a Q4_K call with 2 <= m <= 8 rows: the kernel
- * (0 sector-aligned tiles with x staged in LDS, 1 multi-tile with x in LDS, 2 x read per wave)
- * and its two launch fields (kernel 0: 16-row tiles per workgroup 1-3 and 1 to stage x before
- * the weight loads are issued; kernel 1: tiles per workgroup 1-2 and super-blocks per wave 2-3;
- * kernel 2: waves splitting K, 4 or 8, and 0).  kernel = -1 where the call takes another path
+ * (0 sector-aligned tiles with x staged in LDS, 1 multi-tile with x in LDS, 2 x read per wave,
+ * 3 sector-aligned tiles with K split across workgroups, then the ranges added in order) and its
+ * two launch fields (kernel 0: 16-row tiles per workgroup 1-3 and 1 to stage x before the weight
+ * loads are issued; kernel 1: tiles per workgroup 1-2 and super-blocks per wave 2-3; kernel 2:
+ * waves splitting K, 4 or 8, and 0; kernel 3: tiles per workgroup 1-16 and K ranges, 2 or 4).  kernel = -1 where the call takes another path
  * (m = 1, the other encodings).  No counterpart in the reference, whose showcase picks
  * schedules by timing them (benchmarks/kernels/showcase/benchmark.py:214-237).
  */

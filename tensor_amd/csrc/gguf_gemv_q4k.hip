@@ -489,19 +489,31 @@ __device__ __forceinline__ uint32_t half2_bits(half2_t v) { return __builtin_bit
 // and the same tile of w2, a second matrix of the same shape. PAIR = 1: the wave that sums the w
 // (gate) tile also sums the w2 (up) tile's partials and stores silu(gate) * up to out. PAIR = 2:
 // each tile is stored, to out and out2 (the grouped GEMV of two equal matrices in one launch).
-template <int M, typename OutT, int PAIR = 0, bool XFIRST = true>
+//
+// SPLITS > 1 (x of the whole row does not fit in LDS): K is cut into SPLITS equal ranges, and
+// workgroup SPLITS g + s takes range s of tile group g, staging only that range of x.  Its
+// reduced tiles are fp32 partial sums, stored to part[s][m][n]; gemv_q4k_sec_reduce adds the
+// ranges in order.
+template <int M, typename OutT, int PAIR = 0, bool XFIRST = true, int SPLITS = 1>
 __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict__ x, const uint8_t* __restrict__ w,
                                                      OutT* __restrict__ out, int n_rows, int k, int tiles,
                                                      const uint8_t* __restrict__ w2 = nullptr,
-                                                     OutT* __restrict__ out2 = nullptr) {
+                                                     OutT* __restrict__ out2 = nullptr,
+                                                     float* __restrict__ part = nullptr) {
   constexpr bool SWIGLU = PAIR == 1;
+  static_assert(SPLITS == 1 || PAIR == 0, "K ranges split across workgroups store one matrix's partials");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int XCH = 8;  // x chunks per thread (the host checks M * K / 8 <= XCH * threads)
+  const int row_bytes = (k >> 8) * 144;  // the whole row
+  const int split = SPLITS > 1 ? (int)blockIdx.x % SPLITS : 0;
+  const int group = SPLITS > 1 ? (int)blockIdx.x / SPLITS : (int)blockIdx.x;
+  const int kfull = k;
+  if constexpr (SPLITS > 1) k /= SPLITS;  // from here on: this workgroup's K range
   const int KW = k >> 10;
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int t = wv / KW, q = wv - t * KW;
-  const int row_bytes = (k >> 8) * 144, threads = blockDim.x;
+  const int threads = blockDim.x;
   const int xrow = 2 * k + kSecXPad, cpr = k >> 3, srow = sec_sum_row(k);
   uint8_t* xl = lds;                                                       // M rows of x
   float* s16 = reinterpret_cast<float*>(lds + M * xrow);                   // [M][K/16 + pad] run sums
@@ -514,10 +526,19 @@ __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict_
 #pragma unroll
   for (int i = 0; i < XCH; ++i) {
     const int cw = wv * 64 + i * threads;
-    if (cw < M * cpr) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * (size_t)(cw + lane));
+    if (cw < M * cpr) {
+      if constexpr (SPLITS > 1) {
+        const int m = cw / cpr;
+        xr[i] = load16(reinterpret_cast<const uint8_t*>(x + (size_t)m * kfull + (size_t)split * k) +
+                       16 * (size_t)(cw - m * cpr + lane));
+      } else {
+        xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * (size_t)(cw + lane));
+      }
+    }
   }
-  const int tile = PAIR ? (int)blockIdx.x : blockIdx.x * tiles + t;
-  const uint8_t* base = (PAIR && t == 1 ? w2 : w) + (size_t)min(tile * 16 + n, n_rows - 1) * row_bytes + q * 576 + 16 * g;
+  const int tile = PAIR ? group : group * tiles + t;
+  const uint8_t* base = (PAIR && t == 1 ? w2 : w) + (size_t)min(tile * 16 + n, n_rows - 1) * row_bytes +
+                        (split * KW + q) * 576 + 16 * g;
   uint4 v[9];
   auto load_weights = [&]() {
 #pragma unroll
@@ -650,8 +671,27 @@ __global__ __launch_bounds__(1024) void gemv_q4k_sec(const _Float16* __restrict_
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = 4 * g + i;
-    if (m < M && col < n_rows) store_out<OutT>(dst, (size_t)m * n_rows + col, sum[i]);
+    if (m < M && col < n_rows) {
+      if constexpr (SPLITS > 1)
+        part[((size_t)split * M + m) * n_rows + col] = sum[i];
+      else
+        store_out<OutT>(dst, (size_t)m * n_rows + col, sum[i]);
+    }
   }
+}
+
+// out[m][c] = part[0][m][c] + .. + part[SPLITS-1][m][c], added in range order; one thread per
+// output, grid (ceil(n / 256), M).
+template <int SPLITS, typename OutT>
+__global__ __launch_bounds__(256) void gemv_q4k_sec_reduce(const float* __restrict__ part, OutT* __restrict__ out,
+                                                           int n_rows, int m_rows) {
+  const int c = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+  if (c >= n_rows) return;
+  const size_t plane = (size_t)m_rows * n_rows, at = (size_t)m * n_rows + c;
+  float v = part[at];
+#pragma unroll
+  for (int s = 1; s < SPLITS; ++s) v += part[at + s * plane];
+  store_out<OutT>(out, at, v);
 }
 
 // Multi-tile variant for 2 <= M <= 8 when x fits in LDS (M * K <= kMtMaxMK).
@@ -909,6 +949,37 @@ static hipError_t launch_sec(const GemvArgs& a, hipStream_t stream, int per, boo
   return hipGetLastError();
 }
 
+// Bytes of fp32 partial sums a K split into `splits` ranges stores.
+static size_t sec_split_bytes(const GemvArgs& a, int splits) { return (size_t)splits * a.m * a.n * sizeof(float); }
+
+// K cut into `splits` ranges across workgroups (per tiles each), then the ranges added in order.
+template <int M, int SPLITS, typename OutT>
+static hipError_t launch_sec_split_cfg(const GemvArgs& a, hipStream_t stream, int per) {
+  const int ks = a.k / SPLITS, kw = ks / 1024, tiles = (a.n + 15) / 16, threads = per * kw * 64;
+  const size_t lds = sec_lds_bytes(M, ks, per * kw);
+  const int groups = (tiles + per - 1) / per;
+  float* part = static_cast<float*>(a.workspace);
+  hipLaunchKernelGGL((gemv_q4k_sec<M, OutT, 0, true, SPLITS>), dim3(groups * SPLITS), dim3(threads), lds, stream,
+                     static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w), static_cast<OutT*>(a.out),
+                     a.n, a.k, per, nullptr, nullptr, part);
+  hipError_t status = hipGetLastError();
+  if (status != hipSuccess) return status;
+  hipLaunchKernelGGL((gemv_q4k_sec_reduce<SPLITS, OutT>), dim3((a.n + 255) / 256, M), dim3(256), 0, stream, part,
+                     static_cast<OutT*>(a.out), a.n, M);
+  return hipGetLastError();
+}
+
+template <int M, typename OutT>
+static hipError_t launch_sec_split(const GemvArgs& a, hipStream_t stream, int per, int splits) {
+  if constexpr (M < 4) {
+    return hipErrorInvalidValue;  // x of M <= 3 rows fits without a split
+  } else {
+    if (!a.workspace || a.workspace_bytes < sec_split_bytes(a, splits)) return hipErrorInvalidValue;
+    return splits == 2 ? launch_sec_split_cfg<M, 2, OutT>(a, stream, per)
+                       : launch_sec_split_cfg<M, 4, OutT>(a, stream, per);
+  }
+}
+
 // SwiGLU pairs at 2 <= M <= 8 on the sector-aligned kernel: one gate tile and the same up tile
 // per workgroup (2 x K/1024 waves, so K <= 8192), x in LDS.
 template <int M, typename OutT, int PAIR>
@@ -945,6 +1016,7 @@ static hipError_t launch_plan_typed(const GemvArgs& a, const GemvPlan& plan, hip
   switch (plan.kernel) {
     case kGemvSec: return launch_sec<M, OutT>(a, stream, plan.a, plan.b != 0);
     case kGemvMt: return launch_mt<M, OutT>(a, stream, plan.a, plan.b);
+    case kGemvSecSplit: return launch_sec_split<M, OutT>(a, stream, plan.a, plan.b);
     default: return launch_mfma<M, OutT>(a, stream, plan.a);
   }
 }
@@ -971,6 +1043,17 @@ static bool sec_fits(const GemvArgs& a, int per) {
   return (long)a.m * a.k / 8 <= 8L * threads && sec_lds_bytes(a.m, a.k, per * kw) <= kSecMaxLds;
 }
 
+// The K-split form: M >= 4 (the instantiated range), 2 or 4 ranges of whole 1024-column
+// sectors, at most 16 waves, x of one range staged like the unsplit kernel's, and partial sums
+// within 32-bit offsets.
+static bool sec_split_fits(const GemvArgs& a, int per, int splits) {
+  if (a.m < 4 || (splits != 2 && splits != 4) || a.k % (1024 * splits) != 0) return false;
+  const int ks = a.k / splits, kw = ks / 1024;
+  if (per < 1 || per * kw > 16 || sec_split_bytes(a, splits) >= (1ull << 31)) return false;
+  const int threads = per * kw * 64;
+  return (long)a.m * ks / 8 <= 8L * threads && sec_lds_bytes(a.m, ks, per * kw) <= kSecMaxLds;
+}
+
 static bool mt_fits(const GemvArgs& a, int tiles, int s) {
   if (a.k % 256 != 0 || (tiles != 1 && tiles != 2) || (s != 2 && s != 3)) return false;
   const int waves = (a.k / 256 + s - 1) / s;
@@ -984,8 +1067,13 @@ bool gemv_q4k_plan_fits(const GemvArgs& a, const GemvPlan& plan) {
     case kGemvSec: return (plan.b == 0 || plan.b == 1) && sec_fits(a, plan.a);
     case kGemvMt: return mt_fits(a, plan.a, plan.b);
     case kGemvMfma: return (plan.a == 4 || plan.a == 8) && plan.b == 0;
+    case kGemvSecSplit: return sec_split_fits(a, plan.a, plan.b);
     default: return false;
   }
+}
+
+size_t gemv_q4k_plan_workspace(const GemvArgs& a, const GemvPlan& plan) {
+  return plan.kernel == kGemvSecSplit ? sec_split_bytes(a, plan.b) : 0;
 }
 
 // The library's multi-row plan.  Sector-aligned kernel for matrices of at least 512 tiles
@@ -994,8 +1082,13 @@ bool gemv_q4k_plan_fits(const GemvArgs& a, const GemvPlan& plan) {
 // that still gives 256 workgroups (so every CU holds one), x first only where every workgroup
 // starts at once (at most one per CU of the 256); shorter and narrower shapes take
 // gemv_q4k_mt (4096 x 4096: 6.1 us both) with x in LDS, 2 super-blocks per wave up to K = 8192
-// and 3 up to 12288, two tiles per workgroup from 8192 rows; else gemv_q4k_mfma, K split over
-// 8 waves up to 512 tiles (about 12 waves per CU on 256 CUs), else over 4.
+// and 3 up to 12288, two tiles per workgroup from 8192 rows.  Long rows whose x does not fit in
+// LDS (M = 8 down, 4096 x 12288: 196 KB of x) split K across workgroups when that gives one round
+// of 128 to 256 workgroups, the most workgroups first, then the shorter ranges of x (M = 8 down: 4 ranges
+// of 3 sectors, 4 tiles per workgroup, 256 workgroups; 13.2 against 16.5 us for gemv_q4k_mfma
+// with the reduce, in a timing harness); it needs a workspace, which the entry points give from
+// the library's scratch.  Else gemv_q4k_mfma, K split over 8 waves up to 512 tiles (about 12
+// waves per CU on 256 CUs), else over 4.
 bool gemv_q4k_plan(const GemvArgs& a, GemvPlan* plan) {
   if (a.type != kQ4_K || a.x_f32 || a.m < 2 || a.m > 8 || a.k % 256 != 0) return false;
   const int kw = a.k / 1024, tiles = (a.n + 15) / 16, blocks = a.k / 256;
@@ -1004,6 +1097,21 @@ bool gemv_q4k_plan(const GemvArgs& a, GemvPlan* plan) {
     if (sec_fits(a, per)) {
       *plan = GemvPlan{kGemvSec, per, (tiles + per - 1) / per <= 256 ? 1 : 0};
       return true;
+    }
+    if (kw >= 8) {
+      GemvPlan best{-1, 0, 0};
+      int best_grid = 127;
+      for (int splits = 4; splits >= 2; splits -= 2)
+        for (int p = 1; p <= 16; ++p) {
+          const long grid = (long)((tiles + p - 1) / p) * splits;
+          if (grid > 256 || grid <= best_grid || !sec_split_fits(a, p, splits)) continue;
+          best = GemvPlan{kGemvSecSplit, p, splits};
+          best_grid = (int)grid;
+        }
+      if (best.kernel == kGemvSecSplit) {
+        *plan = best;
+        return true;
+      }
     }
   }
   const GemvPlan mt{kGemvMt, a.n >= 8192 ? 2 : 1, blocks <= 32 ? 2 : 3};
@@ -1029,6 +1137,9 @@ static hipError_t launch_typed(const GemvArgs& a, hipStream_t stream, bool* hand
     *handled = false;
     return hipSuccess;
   }
+  // a call without a workspace runs the plan that reads x per wave
+  if (plan.kernel == kGemvSecSplit && (!a.workspace || a.workspace_bytes < gemv_q4k_plan_workspace(a, plan)))
+    plan = GemvPlan{kGemvMfma, (a.n + 15) / 16 <= 512 ? 8 : 4, 0};
   return launch_plan_m<OutT>(a, plan, stream);
 }
 

@@ -17,6 +17,10 @@ struct GemvArgs {
   // fp32 activations (the packed call form): the M = 1 GEMV multiplies them in fp32, the
   // GEMM rounds them to fp16 as it stages its activation tiles
   bool x_f32 = false;
+  // device memory for a multi-row GEMV plan that splits K across workgroups (its fp32 partial
+  // sums); without it such a shape runs the plan that reads x per wave
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
 };
 
 struct DequantArgs {
@@ -54,7 +58,9 @@ hipError_t launch_gemv_q4k_pair(const GemvArgs* args, hipStream_t stream, bool* 
 //                              the weight loads are issued, 0 to issue them behind x
 //   kGemvMt   (gemv_q4k_mt):   a = tiles per workgroup (1-2), b = super-blocks per wave (2-3)
 //   kGemvMfma (gemv_q4k_mfma): a = waves per workgroup splitting K (4 or 8), b = 0
-enum { kGemvSec = 0, kGemvMt = 1, kGemvMfma = 2 };
+//   kGemvSecSplit (gemv_q4k_sec over K ranges, then gemv_q4k_sec_reduce): a = 16-row tiles per
+//                              workgroup (1-16), b = K ranges (2 or 4); M >= 4, a workspace
+enum { kGemvSec = 0, kGemvMt = 1, kGemvMfma = 2, kGemvSecSplit = 3 };
 struct GemvPlan {
   int kernel, a, b;
 };
@@ -63,7 +69,10 @@ struct GemvPlan {
 bool gemv_q4k_plan(const GemvArgs& args, GemvPlan* plan);
 // Whether plan fits args's shape (the launch limits of its kernel).
 bool gemv_q4k_plan_fits(const GemvArgs& args, const GemvPlan& plan);
-// Launch a plan that fits (hipErrorInvalidValue otherwise).
+// Bytes of workspace a plan needs (args.workspace, args.workspace_bytes): 0 for all but kGemvSecSplit.
+size_t gemv_q4k_plan_workspace(const GemvArgs& args, const GemvPlan& plan);
+// Launch a plan that fits (hipErrorInvalidValue otherwise, also for a plan whose workspace
+// args does not provide).
 hipError_t launch_gemv_q4k_plan(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream);
 // Decode GEMV on Q8_1-quantized activations with integer dot products (GGML's path), Q4_0,
 // Q8_0, Q4_K and Q6_K, M <= 8, fp16 or fp32 x (args.x_f32); x is quantized inside each

@@ -131,6 +131,59 @@ int32_t check_device(const TensorCallV1* call, TensorErrorV1* error) {
   return TENSOR_OK;
 }
 
+// One call's use of the library's scratch (after check_device).  The scratch is one array per
+// device: an eager call on another stream than the previous eager call first waits for that
+// call's event, and the lease holds scratch_mutex from acquire to release so that host threads
+// cannot interleave between the wait and the record.  Under stream capture nothing is waited for
+// or recorded (the graph's replays choose their streams later).
+class ScratchLease {
+ public:
+  int32_t acquire(const TensorCallV1* call, hipStream_t stream, TensorErrorV1* error) {
+    lock_.lock();
+    hipError_t status = scratch_setup(call->stream.device_ordinal, &state_);
+    if (status != hipSuccess) return hip_fail(error, status, "scratch set-up");
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    status = hipStreamIsCapturing(stream, &capture);
+    if (status != hipSuccess) return hip_fail(error, status, "hipStreamIsCapturing");
+    eager_ = capture == hipStreamCaptureStatusNone;
+    if (eager_ && state_->used && state_->last != stream) {
+      status = hipStreamWaitEvent(stream, state_->done, 0);
+      if (status != hipSuccess) return hip_fail(error, status, "hipStreamWaitEvent(scratch)");
+    }
+    return TENSOR_OK;
+  }
+  // After the call's launches: an eager call records its event.
+  int32_t release(hipStream_t stream, TensorErrorV1* error) {
+    if (eager_) {
+      const hipError_t status = hipEventRecord(state_->done, stream);
+      if (status != hipSuccess) return hip_fail(error, status, "hipEventRecord(scratch)");
+      state_->last = stream;
+      state_->used = true;
+    }
+    return TENSOR_OK;
+  }
+  void* address() const { return state_->address; }
+
+ private:
+  std::unique_lock<std::mutex> lock_{scratch_mutex, std::defer_lock};
+  ScratchState* state_ = nullptr;
+  bool eager_ = false;
+};
+
+// A multi-row Q4_K GEMV whose plan splits K across workgroups takes its partial sums in the
+// scratch: the lease is taken when the plan needs one (a Q4_K call with 2 <= M <= 8).
+int32_t gemv_workspace(const TensorCallV1* call, tensor_gguf::GemvArgs* args, const tensor_gguf::GemvPlan& plan,
+                       hipStream_t stream, ScratchLease* lease, bool* leased, TensorErrorV1* error) {
+  *leased = false;
+  const size_t need = tensor_gguf::gemv_q4k_plan_workspace(*args, plan);
+  if (need == 0 || need > kScratchBytes) return TENSOR_OK;  // beyond the scratch: the plan without it
+  if (int32_t s = lease->acquire(call, stream, error)) return s;
+  *leased = true;
+  args->workspace = lease->address();
+  args->workspace_bytes = kScratchBytes;
+  return TENSOR_OK;
+}
+
 // A rank-2 contiguous device buffer of one of the allowed dtypes.
 int32_t check_matrix(const TensorArgumentV1& arg, const char* name, int ordinal, uint32_t dtype_a,
                      uint32_t dtype_b, TensorErrorV1* error) {
@@ -197,9 +250,14 @@ int32_t linear_call(const TensorCallV1* call, TensorErrorV1* error, Op op) {
   args.out_half = a[2].dtype == TENSOR_FLOAT16;
   hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
   const bool gemv = op == Op::kGemv || (op == Op::kLinear && m <= tensor_gguf::kGemvMaxM);
+  ScratchLease lease;
+  bool leased = false;
+  tensor_gguf::GemvPlan plan;
+  if (gemv && tensor_gguf::gemv_q4k_plan(args, &plan))
+    if (int32_t s = gemv_workspace(call, &args, plan, stream, &lease, &leased, error)) return s;
   hipError_t status = gemv ? tensor_gguf::launch_gemv(args, stream) : tensor_gguf::launch_gemm(args, stream);
   if (status != hipSuccess) return hip_fail(error, status, gemv ? "GGUF GEMV launch" : "GGUF GEMM launch");
-  return TENSOR_OK;
+  return leased ? lease.release(stream, error) : TENSOR_OK;
 }
 
 // Grouped decode GEMV: x shared by `count` (w, out) pairs, arguments
@@ -413,13 +471,20 @@ int32_t gemv_variant_call(const TensorCallV1* call, TensorErrorV1* error) {
   if (!tensor_gguf::gemv_q4k_plan(args, &probe))
     return fail(error, TENSOR_ERROR_ARGUMENT, "multi-row GEMV plans take Q4_K with 2 <= M <= 8");
   const tensor_gguf::GemvPlan plan{(int)kernel, (int)pa, (int)pb};
-  if (kernel > 2 || pa > 16 || pb > 16 || !tensor_gguf::gemv_q4k_plan_fits(args, plan))
+  if (kernel > 3 || pa > 16 || pb > 16 || !tensor_gguf::gemv_q4k_plan_fits(args, plan))
     return fail(error, TENSOR_ERROR_ARGUMENT, "GEMV plan (%u, %u, %u) does not fit this shape", (unsigned)kernel,
                 (unsigned)pa, (unsigned)pb);
+  if (tensor_gguf::gemv_q4k_plan_workspace(args, plan) > kScratchBytes)
+    return fail(error, TENSOR_ERROR_ARGUMENT, "GEMV plan (%u, %u, %u): its partial sums exceed the scratch",
+                (unsigned)kernel, (unsigned)pa, (unsigned)pb);
   if (int32_t s = check_device(call, error)) return s;
-  hipError_t status = tensor_gguf::launch_gemv_q4k_plan(args, plan, reinterpret_cast<hipStream_t>(call->stream.handle));
+  hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
+  ScratchLease lease;
+  bool leased = false;
+  if (int32_t s = gemv_workspace(call, &args, plan, stream, &lease, &leased, error)) return s;
+  hipError_t status = tensor_gguf::launch_gemv_q4k_plan(args, plan, stream);
   if (status != hipSuccess) return hip_fail(error, status, "GGUF GEMV launch");
-  return TENSOR_OK;
+  return leased ? lease.release(stream, error) : TENSOR_OK;
 }
 
 // The packed call form: [x, w, out, type, m, n, k] with flat buffers (see tensor_hip.h).
@@ -540,26 +605,10 @@ int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has
   }
   if (int32_t s = check_device(call, error)) return s;
   hipStream_t stream = reinterpret_cast<hipStream_t>(call->stream.handle);
-  // The scratch is one array per device: an eager call on another stream than the previous eager
-  // call first waits for that call's event, and the mutex keeps host threads from interleaving
-  // between the wait and the record.  Under stream capture nothing is waited for or recorded
-  // (the graph's replays choose their streams later).
-  std::unique_lock<std::mutex> scratch_lock(scratch_mutex, std::defer_lock);
-  ScratchState* scratch_use = nullptr;
-  bool eager = false;
+  ScratchLease lease;
   if (!has_workspace) {
-    scratch_lock.lock();
-    hipError_t status = scratch_setup(call->stream.device_ordinal, &scratch_use);
-    if (status != hipSuccess) return hip_fail(error, status, "scratch set-up");
-    workspace = scratch_use->address;
-    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    status = hipStreamIsCapturing(stream, &capture);
-    if (status != hipSuccess) return hip_fail(error, status, "hipStreamIsCapturing");
-    eager = capture == hipStreamCaptureStatusNone;
-    if (eager && scratch_use->used && scratch_use->last != stream) {
-      status = hipStreamWaitEvent(stream, scratch_use->done, 0);
-      if (status != hipSuccess) return hip_fail(error, status, "hipStreamWaitEvent(scratch)");
-    }
+    if (int32_t s = lease.acquire(call, stream, error)) return s;
+    workspace = lease.address();
   }
   hipError_t status = hipSuccess;
   tensor_gguf::GemvArgs one[tensor_gguf::kGemmGroupMax];
@@ -583,13 +632,7 @@ int32_t gemm_group_call(const TensorCallV1* call, TensorErrorV1* error, bool has
     for (int i = 0; i < count && status == hipSuccess; ++i) status = tensor_gguf::launch_gemm(one[i], stream);
   }
   if (status != hipSuccess) return hip_fail(error, status, "GGUF grouped GEMM launch");
-  if (eager) {
-    status = hipEventRecord(scratch_use->done, stream);
-    if (status != hipSuccess) return hip_fail(error, status, "hipEventRecord(scratch)");
-    scratch_use->last = stream;
-    scratch_use->used = true;
-  }
-  return TENSOR_OK;
+  return has_workspace ? TENSOR_OK : lease.release(stream, error);
 }
 
 }  // namespace

@@ -30,10 +30,11 @@ from tensor_amd.runtime.session import Session
 # Multi-row Q4_K GEMV kernels by plan index, and the launch fields (a, b) each accepts:
 # sector-aligned tiles (tiles per workgroup, x staged before the weight loads), multi-tile with x
 # in LDS (tiles per workgroup, super-blocks per wave), x read per wave (waves splitting K, 0).
-GEMV_KERNELS = ("sec", "mt", "mfma")
+GEMV_KERNELS = ("sec", "mt", "mfma", "sec_split")
 GEMV_FIELDS = {0: [(a, b) for a in (1, 2, 3) for b in (0, 1)],
                1: [(a, b) for a in (1, 2) for b in (2, 3)],
-               2: [(4, 0), (8, 0)]}
+               2: [(4, 0), (8, 0)],
+               3: [(a, b) for a in (1, 2, 3, 4, 5, 6, 8) for b in (2, 4)]}
 
 
 def gemm_tiles() -> list:

@@ -556,7 +556,7 @@ def test_gemv_plan_query_names_the_library_plans_at_the_baseline_shapes():
     query, no launch), and the paths the query leaves to other kernels."""
     from tensor_amd.providers.hip import GEMV_FIELDS, GEMV_KERNELS
 
-    assert GEMV_KERNELS == ("sec", "mt", "mfma")
+    assert GEMV_KERNELS == ("sec", "mt", "mfma", "sec_split")
     lib = _native.library()
 
     def plan(code, m, k, n):
@@ -569,7 +569,9 @@ def test_gemv_plan_query_names_the_library_plans_at_the_baseline_shapes():
     assert plan(12, 4, 4096, 12288) == (0, 3, 1)   # gate / up at M=4: sector tiles, 3 per workgroup, x first
     assert plan(12, 4, 12288, 4096) == (0, 1, 1)   # down at M=4: one tile, 12 K ranges
     assert plan(12, 8, 4096, 12288) == (0, 3, 1)
-    assert plan(12, 8, 12288, 4096) == (2, 8, 0)   # down at M=8: x (196 KB) does not fit LDS
+    assert plan(12, 8, 12288, 4096) == (3, 4, 4)   # down at M=8: x (196 KB) does not fit LDS, so K splits
+    #                                                into 4 ranges, 4 tiles per workgroup: 256 workgroups
+    assert plan(12, 8, 12288, 64) == (2, 8, 0)     # too few tiles for a split round: x read per wave
     assert plan(12, 4, 4096, 4096) == (1, 1, 2)    # narrower shapes: the multi-tile kernel
     for query in ((12, 1, 4096, 12288), (14, 4, 4096, 4096), (8, 4, 4096, 4096)):
         assert plan(*query)[0] == -1               # M = 1 and the other encodings: other kernels

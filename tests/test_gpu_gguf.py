@@ -107,7 +107,7 @@ def test_gemv_parity_small(hip_device, encoding, m, k):
     ("q4_k", 12288, 4096, 4, "float16"),
     ("q4_k", 4096, 12288, 4, "float16"),   # C2 down at M = 4: one 16-row tile x 12 K ranges per workgroup
     ("q4_k", 12288, 4096, 8, "float16"),   # C2 gate at M = 8
-    ("q4_k", 4096, 12288, 8, "float16"),
+    ("q4_k", 4096, 12288, 8, "float16"),   # C2 down at M = 8: K split into 4 ranges across workgroups
     ("q6_k", 151936, 4096, 1, "float32"),  # C3 LM head, fp32 logits
     ("q6_k", 4096, 12288, 1, "float16"),   # C5 down (Q6_K)
     ("q6_k", 1001, 12288, 1, "float32"),   # three steps per row, ragged last workgroup
@@ -177,14 +177,16 @@ def test_gemv_q6k_tall_rows_each_within_tolerance(hip_device, c_oracle, n):
     (4, 4101, 12288),   # sector-aligned for a long row, twelve K ranges, ragged rows
     (4, 4096, 12288),   # C2 down at M = 4: 256 workgroups, so x is staged before the weights
     (2, 100, 16384),    # sector-aligned, sixteen K ranges of one 16-row tile
-    (5, 4100, 12288),   # x too large for the sector kernel: three super-blocks per wave, x in LDS
+    (5, 4100, 12288),   # x too large for the sector kernel: K split into 4 ranges, 5 tiles per workgroup
     (8, 4100, 4096),    # narrow matrix: the LDS multi-tile kernel
     (3, 9000, 2560),    # K not a multiple of 1024: two tiles per wave, five waves
     (2, 40, 256),       # one super-block, one wave
     (4, 8200, 512),     # two tiles per wave and a single wave: the wave stores both tiles
-    (8, 1024, 12288),   # x too large for LDS: the one-super-block-per-step kernel
-    (8, 4100, 12288),   # C2 down at M = 8 (one super-block per step), ragged rows
-    (6, 300, 16384),    # the longest rows, x too large for LDS
+    (8, 1024, 12288),   # x too large for LDS: K split into 4 ranges, 2 tiles per workgroup
+    (8, 4100, 12288),   # C2 down at M = 8 with ragged rows: 4 ranges, 5 tiles per workgroup (208 workgroups)
+    (4, 1000, 16384),   # the split at the smallest M it runs: 4 ranges, one tile per workgroup
+    (6, 2000, 12288),   # 4 ranges, 2 tiles per workgroup, ragged last tile
+    (6, 300, 16384),    # the longest rows, x too large for LDS, too few tiles for a split: x per wave
     (8, 64, 16384),     # x of 256 KB
     (8, 300, 8448),     # K not a multiple of 1024 and x too large for LDS
 ])
@@ -310,12 +312,13 @@ def test_gemv_swiglu_parity(hip_device, encoding, m, n, k):
     assert np.array_equal(zero, np.zeros_like(zero))
 
 
-@pytest.mark.parametrize("encoding", ["q4_k", "q6_k"])
-def test_gemv_input_families_and_graph_replay(hip_device, encoding):
+@pytest.mark.parametrize("encoding,m,k", [("q4_k", 1, 4096), ("q6_k", 1, 4096),
+                                          ("q4_k", 8, 12288)])  # K split across workgroups + reduce
+def test_gemv_input_families_and_graph_replay(hip_device, encoding, m, k):
     """One captured graph, replayed after x changes: random, x*-1.5, zeros."""
     code = Q.ggml_type(encoding)
-    n, k, m = 1024, 4096, 1
-    note("gemv-graph", encoding)
+    n = 1024
+    note("gemv-graph", encoding, m, k)
     raw = cases.weight(n, k, encoding, 50)
     x = cases.activation(m, k, 51)
     exe = hip_device.load("gguf_gemv", encoding=encoding, out_dtype="float32")

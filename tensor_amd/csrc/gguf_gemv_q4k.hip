@@ -1080,7 +1080,9 @@ size_t gemv_q4k_plan_workspace(const GemvArgs& a, const GemvPlan& plan) {
 // (gate / up, 12288 x 4096: 11.0 us at M = 4 against 12.8 us for gemv_q4k_mt) and rows of at
 // least 8192 columns (down, 4096 x 12288: 12.5 against 14.5 us), three tiles per workgroup when
 // that still gives 256 workgroups (so every CU holds one), x first only where every workgroup
-// starts at once (at most one per CU of the 256); shorter and narrower shapes take
+// starts at once (at most one per CU of the 256) and x is at most 32 KB (M = 4 gate: 10.4 against
+// 10.7-11.0 us; with 64 KB at the M = 8 gate or 96 KB at the M = 4 down, the weights issued behind x
+// run 1-3% faster in the plan sweep and a timing harness); shorter and narrower shapes take
 // gemv_q4k_mt (4096 x 4096: 6.1 us both) with x in LDS, 2 super-blocks per wave up to K = 8192
 // and 3 up to 12288, two tiles per workgroup from 8192 rows.  Long rows whose x does not fit in
 // LDS (M = 8 down, 4096 x 12288: 196 KB of x) split K across workgroups when that gives one round
@@ -1095,7 +1097,8 @@ bool gemv_q4k_plan(const GemvArgs& a, GemvPlan* plan) {
   if (a.k % 1024 == 0 && (tiles >= 512 || kw >= 8)) {
     const int per = tiles >= 768 && 3 * kw <= 16 ? 3 : tiles >= 512 && 2 * kw <= 16 ? 2 : 1;
     if (sec_fits(a, per)) {
-      *plan = GemvPlan{kGemvSec, per, (tiles + per - 1) / per <= 256 ? 1 : 0};
+      const bool xfirst = (tiles + per - 1) / per <= 256 && (long)a.m * a.k * 2 <= 32 * 1024;
+      *plan = GemvPlan{kGemvSec, per, xfirst ? 1 : 0};
       return true;
     }
     if (kw >= 8) {

@@ -567,8 +567,9 @@ def test_gemv_plan_query_names_the_library_plans_at_the_baseline_shapes():
         return kernel.value, a.value, b.value
 
     assert plan(12, 4, 4096, 12288) == (0, 3, 1)   # gate / up at M=4: sector tiles, 3 per workgroup, x first
-    assert plan(12, 4, 12288, 4096) == (0, 1, 1)   # down at M=4: one tile, 12 K ranges
-    assert plan(12, 8, 4096, 12288) == (0, 3, 1)
+    assert plan(12, 4, 12288, 4096) == (0, 1, 0)   # down at M=4: one tile, 12 K ranges, 96 KB of x
+    #                                                staged behind the weight loads
+    assert plan(12, 8, 4096, 12288) == (0, 3, 0)   # gate at M=8: 64 KB of x, behind the weight loads
     assert plan(12, 8, 12288, 4096) == (3, 4, 4)   # down at M=8: x (196 KB) does not fit LDS, so K splits
     #                                                into 4 ranges, 4 tiles per workgroup: 256 workgroups
     assert plan(12, 8, 12288, 64) == (2, 8, 0)     # too few tiles for a split round: x read per wave

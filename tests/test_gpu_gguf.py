@@ -175,7 +175,8 @@ def test_gemv_q6k_tall_rows_each_within_tolerance(hip_device, c_oracle, n):
     (6, 12296, 4096),   # sector-aligned, three tiles per workgroup, last workgroup one tile
     (3, 8200, 8192),    # sector-aligned, two tiles x eight K ranges (1024 threads)
     (4, 4101, 12288),   # sector-aligned for a long row, twelve K ranges, ragged rows
-    (4, 4096, 12288),   # C2 down at M = 4: 256 workgroups, so x is staged before the weights
+    (4, 4096, 12288),   # C2 down at M = 4: 256 workgroups, its 96 KB of x staged behind the weight loads
+    (4, 12288, 4096),   # C2 gate at M = 4: 256 workgroups, 32 KB of x staged before the weight loads
     (2, 100, 16384),    # sector-aligned, sixteen K ranges of one 16-row tile
     (5, 4100, 12288),   # x too large for the sector kernel: K split into 4 ranges, 5 tiles per workgroup
     (8, 4100, 4096),    # narrow matrix: the LDS multi-tile kernel

@@ -1071,6 +1071,41 @@ def test_gemv_q8_1_edge_shapes_and_zero_blocks(hip_device, encoding, m, n, k):
         buffer.release()
 
 
+def test_gemv_k_split_calls_on_two_streams_take_the_scratch_in_turn():
+    """The multi-row GEMV plan that splits K across workgroups keeps its partial sums in the
+    library's scratch: eager calls on two sessions' streams, enqueued back to back with no host
+    wait between them, are ordered one after the other by the library, so each gives the bits
+    it gives alone."""
+    import tensor_amd as tx
+
+    m, n, k = 8, 1000, 12288
+    note("gemv-split-two-streams", m, n, k)
+    inputs = [(cases.activation(m, k, 1600 + i), cases.weight(n, k, "q4_k", 1610 + i)) for i in range(2)]
+    with tx.Device(0, provider="hip") as first, tx.Device(0, provider="hip") as second:
+        assert first.stream != second.stream
+        assert first.gemv_plan("q4_k", m, k, n)["name"] == "sec_split"
+        sessions = (first, second)
+        alone = [run_linear(device, "gguf_gemv", "q4_k", x, raw, "float32")
+                 for device, (x, raw) in zip(sessions, inputs)]
+        calls, outs, keep = [], [], []
+        for device, (x, raw) in zip(sessions, inputs):
+            exe = device.load("gguf_gemv", encoding="q4_k", out_dtype="float32")
+            xb, wb, out = device.from_numpy(x), device.from_numpy(raw), device.empty((m, n), "float32")
+            device.fill_bytes(out, 0xFF)
+            calls.append(exe.bind(xb, wb, out))
+            outs.append(out)
+            keep += [xb, wb]
+            device.synchronize()
+        for _ in range(3):
+            calls[0].launch()
+            calls[1].launch()
+        for device in sessions:
+            device.synchronize()
+        for session in range(2):
+            got = outs[session].to_numpy()
+            assert np.array_equal(got.view(np.uint32), alone[session].view(np.uint32)), session
+
+
 @pytest.mark.parametrize("m,n,k", [(4, 2000, 4096), (3, 777, 8192), (8, 1000, 12288), (2, 40, 1280)])
 def test_gemv_every_multirow_plan_through_the_variant_entry(hip_device, c_oracle, m, n, k):
     """Every multi-row Q4_K plan the variant entry accepts at ragged shapes (fp32 out): each within

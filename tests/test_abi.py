@@ -584,6 +584,38 @@ def test_gemv_plan_query_names_the_library_plans_at_the_baseline_shapes():
     assert lib.tensor_gguf_gemv_plan_v1(12, 4, 4000, 4096, *map(c.byref, out), c.byref(error)) == ERR_ARG
 
 
+def test_gemv_k_split_plans_stay_in_one_round_and_fit_the_scratch():
+    """Where the multi-row plan splits K across workgroups (kernel 3), its workgroups make one
+    round on 256 CUs (128-256 of them), each K range is whole 1024-column sectors, and the fp32
+    partial sums fit the library's 32 MiB scratch; shapes whose x fits in LDS never split."""
+    lib = _native.library()
+
+    def plan(m, k, n):
+        kernel, a, b = c.c_int32(), c.c_int32(), c.c_int32()
+        error = abi.ErrorDescriptor()
+        assert lib.tensor_gguf_gemv_plan_v1(12, m, k, n, c.byref(kernel), c.byref(a), c.byref(b),
+                                            c.byref(error)) == OK, error.message
+        return kernel.value, a.value, b.value
+
+    seen = 0
+    for m in range(2, 9):
+        for k in (4096, 8192, 12288, 16384):
+            for n in (64, 300, 1000, 2048, 4096, 4100, 8192, 12288):
+                kernel, per, splits = plan(m, k, n)
+                if kernel != 3:
+                    continue
+                seen += 1
+                tiles = (n + 15) // 16
+                grid = -(-tiles // per) * splits
+                assert m >= 4 and splits in (2, 4), (m, k, n, per, splits)
+                assert 128 <= grid <= 256, (m, k, n, per, splits, grid)
+                assert k % (1024 * splits) == 0 and per * (k // 1024 // splits) <= 16
+                assert splits * m * n * 4 <= 32 << 20
+                assert m * k * 2 > 64 * 1024, (m, k)  # x of the whole row would not fit with its tables
+    assert seen >= 10
+    assert plan(8, 12288, 4096) == (3, 4, 4)
+
+
 def test_gemv_variant_refuses_a_plan_that_does_not_fit():
     """tensor_gguf_gemv_variant_v1 checks the named kernel and fields against the shape before
     any HIP call (fake device addresses; CPU only): a plan that fits gets as far as the device

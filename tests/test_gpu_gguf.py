@@ -187,6 +187,7 @@ def test_gemv_q6k_tall_rows_each_within_tolerance(hip_device, c_oracle, n):
     (8, 4100, 12288),   # C2 down at M = 8 with ragged rows: 4 ranges, 5 tiles per workgroup (208 workgroups)
     (4, 1000, 16384),   # the split at the smallest M it runs: 4 ranges, one tile per workgroup
     (6, 2000, 12288),   # 4 ranges, 2 tiles per workgroup, ragged last tile
+    (7, 4096, 12288),   # 4 ranges at an odd row count: output rows past M in every tile
     (6, 300, 16384),    # the longest rows, x too large for LDS, too few tiles for a split: x per wave
     (8, 64, 16384),     # x of 256 KB
     (8, 300, 8448),     # K not a multiple of 1024 and x too large for LDS

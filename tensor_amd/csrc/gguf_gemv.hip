@@ -835,6 +835,11 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t stream) {
                                                 : launch_gemv_q6k_fast(a, stream, &handled);
     if (handled) return status;
   }
+  if (a.type == kQ2_K || a.type == kQ3_K) {
+    bool handled = false;
+    const hipError_t status = launch_gemv_q23k_fast(a, stream, &handled);
+    if (handled) return status;
+  }
   return a.out_half ? launch_out<_Float16>(a, stream) : launch_out<float>(a, stream);
 }
 

@@ -95,6 +95,8 @@ hipError_t launch_gemv_q6k_f32x(const GemvArgs& args, hipStream_t stream, bool* 
 hipError_t launch_gemv_q5k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 // Q6_K fast path (LDS-staged x, M = 1, K in {4096, 8192, 12288}).
 hipError_t launch_gemv_q6k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
+// Q2_K / Q3_K fast path (LDS-staged x, per-sub-block decode, M = 1, K in {4096, 8192, 12288, 16384}).
+hipError_t launch_gemv_q23k_fast(const GemvArgs& args, hipStream_t stream, bool* handled);
 hipError_t launch_dequant(const DequantArgs& args, hipStream_t stream);
 hipError_t launch_gemm(const GemvArgs& args, hipStream_t stream);
 

@@ -117,6 +117,10 @@ def test_gemv_parity_small(hip_device, encoding, m, k):
     ("q5_k", 12288, 4096, 1, "float16"),   # Q5_K through the M = 1 kernel (4 rows per workgroup)
     ("q5_k", 4096, 12288, 1, "float32"),   # three 4096-column steps, 8 rows per workgroup
     ("q5_k", 1003, 16384, 1, "float16"),   # four steps, ragged last workgroup
+    ("q3_k", 12288, 4096, 1, "float16"),   # Q3_K / Q2_K through the per-sub-block M = 1 kernel
+    ("q3_k", 4096, 12288, 1, "float32"),
+    ("q2_k", 12288, 4096, 1, "float32"),
+    ("q2_k", 4096, 12288, 1, "float16"),
     ("q4_k", 1536, 4096, 1, "float16"),    # one GPU's rows of an 8-way gate
     ("q4_k", 4096, 1536, 1, "float16"),    # one GPU's K slice of an 8-way down (generic kernel)
     ("q6_k", 4096, 1536, 1, "float16"),
@@ -149,6 +153,30 @@ def test_gemv_q32_m1_every_row_length(hip_device, c_oracle, encoding):
             assert not np.isnan(got).any(), (k, out_dtype)
             err = R.relative_l2(got, expected)
             assert err <= (2e-4 if out_dtype == "float32" else TOLERANCE), (k, out_dtype, err)
+
+
+@pytest.mark.parametrize("encoding", ["q2_k", "q3_k"])
+@pytest.mark.parametrize("source", ["quantized", "random_bits"])
+def test_gemv_q23k_m1_every_row_length_each_row_within_tolerance(hip_device, c_oracle, encoding, source):
+    """M = 1 Q2_K / Q3_K rows of 4096 .. 16384 columns (the per-sub-block kernel: one to four
+    4096-column steps, a ragged last workgroup of 203 rows), from quantized weights and from
+    random block bytes (every scale, min and third-bit pattern in every position).  Each row is
+    checked, so a misplaced plane, scale or run sum fails even where the whole output's
+    relative L2 would hide it."""
+    code = Q.ggml_type(encoding)
+    n = 203
+    for k in (4096, 8192, 12288, 16384):
+        note("gemv-q23k-m1", encoding, source, n, k)
+        raw = cases.weight(n, k, encoding, 47) if source == "quantized" else cases.random_blocks(encoding, n, k, 48)
+        x = cases.activation(1, k, 49)
+        expected = c_oracle.linear(x, raw, code, n, k)
+        scale = float(np.sqrt(np.mean(expected.astype(np.float64) ** 2)))
+        for out_dtype in ("float32", "float16"):
+            got = run_linear(hip_device, "gguf_gemv", encoding, x, raw, out_dtype)
+            assert not np.isnan(got).any(), (k, out_dtype)
+            assert R.relative_l2(got, expected) <= (2e-4 if out_dtype == "float32" else TOLERANCE), (k, out_dtype)
+            err = np.abs(got[0].astype(np.float32) - expected[0])
+            assert err.max() <= 2e-3 * scale + 1e-3 * np.abs(expected).max(), (k, out_dtype, int(err.argmax()))
 
 
 @pytest.mark.parametrize("n", [65536 + 1007, 70000])

@@ -365,11 +365,11 @@ __global__ __launch_bounds__(256) void gemv_q32(const _Float16* __restrict__ x,
 // 14.9 -> 13.2 us; Q4_0 3.68 -> 3.24, 8.59 -> 7.40, 8.39 -> 8.03 us (WAVES 8 for one or two
 // blocks per lane, else 4).
 //
-// ALIGNED (Q8_0, w 4-byte aligned): the 34-byte blocks of odd lanes start at 2 mod 4, so half of
-// every load instruction's lanes read unaligned, and loads that are not 4-byte aligned cost
+// ALIGNED (w 4-byte aligned): the 34- and 18-byte blocks of odd lanes start at 2 mod 4, so half
+// of every load instruction's lanes read unaligned, and loads that are not 4-byte aligned cost
 // Q8_0 a sixth of its load time (loads alone at 12288 x 4096: 11.95 against 9.81 us with the
 // addresses rounded down).  Every load is then 4-aligned: an even lane reads its block from byte
-// 0 (36 bytes, 2 into the odd block that always follows it) and realigns the codes by 2 bytes;
+// 0 (2 bytes more, into the odd block that always follows it) and realigns the codes by 2 bytes;
 // an odd lane reads its codes from byte 2 as they are, and its d from the dword 2 bytes before
 // the block.
 template <int TYPE, int WAVES, int STEPS, typename OutT, bool ALIGNED = false>
@@ -377,6 +377,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q32_m1(const _Float16* __rest
                                                           const uint8_t* __restrict__ w,
                                                           OutT* __restrict__ out, int n_rows) {
   constexpr int kBytes = TYPE == kQ8_0 ? 34 : 18;
+  constexpr int NW = TYPE == kQ8_0 ? 8 : 4;  // code dwords per block
   constexpr float kBias = TYPE == kQ8_0 ? 1152.0f : 1032.0f;  // as in gemv_q32
   constexpr int T = WAVES * 64, K = 2048 * STEPS, BLOCKS = K / 32, CHUNKS = K / 8;
   constexpr int XC = (CHUNKS + T - 1) / T;  // 16-byte x chunks per thread
@@ -398,12 +399,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q32_m1(const _Float16* __rest
   for (int s = 0; s < STEPS; ++s) {
     const uint8_t* block = wr + (lane + 64 * s) * kBytes;
     if constexpr (ALIGNED) {
-      // even: bytes 0-31 and the dword at 32 (codes 30, 31 and the next block's d);
-      // odd: bytes 2-33 (the codes) and the dword at -2 (d in its high half)
+      // even: bytes 0 .. 4 NW - 1 and the dword after them (the last 2 code bytes and the next
+      // block's d); odd: the codes from byte 2 and the dword at -2 (d in its high half)
       const uint8_t* win = block + (odd ? 2 : 0);
       q0[s] = load16(win);
-      q1[s] = load16(win + 16);
-      head[s] = load4(odd ? block - 2 : block + 32);
+      if constexpr (TYPE == kQ8_0) q1[s] = load16(win + 16);
+      head[s] = load4(odd ? block - 2 : block + 4 * NW);
     } else {
       head[s] = load4(block);  // fp16 d in the low half
       q0[s] = load16(block + 2);
@@ -434,12 +435,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q32_m1(const _Float16* __rest
       // code word u = bytes 2 + 4u .. of the block: window dwords u, u + 1 shifted by 2 (even
       // lanes) or dword u (odd lanes: shift 0)
       const uint32_t sh = odd ? 0u : 2u;
-      uint32_t wd[9] = {q0[s].x, q0[s].y, q0[s].z, q0[s].w, q1[s].x, q1[s].y, q1[s].z, q1[s].w, head[s]};
-      uint32_t cw[8];
+      uint32_t wd[NW + 1];
+      wd[0] = q0[s].x; wd[1] = q0[s].y; wd[2] = q0[s].z; wd[3] = q0[s].w;
+      if constexpr (TYPE == kQ8_0) {
+        wd[4] = q1[s].x; wd[5] = q1[s].y; wd[6] = q1[s].z; wd[7] = q1[s].w;
+      }
+      wd[NW] = head[s];
+      uint32_t cw[NW];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) cw[u] = __builtin_amdgcn_alignbyte(wd[u + 1], wd[u], sh);
+      for (int u = 0; u < NW; ++u) cw[u] = __builtin_amdgcn_alignbyte(wd[u + 1], wd[u], sh);
       q0[s] = make_uint4(cw[0], cw[1], cw[2], cw[3]);
-      q1[s] = make_uint4(cw[4], cw[5], cw[6], cw[7]);
+      if constexpr (TYPE == kQ8_0) q1[s] = make_uint4(cw[4], cw[5], cw[6], cw[7]);
       dbits = odd ? head[s] >> 16 : wd[0];
     }
     if constexpr (TYPE == kQ8_0) {
@@ -473,13 +479,157 @@ static void launch_q32_m1_steps(const GemvArgs& a, hipStream_t stream) {
   const _Float16* x = static_cast<const _Float16*>(a.x);
   const uint8_t* w = static_cast<const uint8_t*>(a.w);
   OutT* out = static_cast<OutT*>(a.out);
-  if constexpr (TYPE == kQ8_0) {
-    if ((reinterpret_cast<uintptr_t>(w) & 3) == 0) {
-      hipLaunchKernelGGL((gemv_q32_m1<TYPE, WAVES, STEPS, OutT, true>), grid, block, 0, stream, x, w, out, a.n);
-      return;
-    }
+  if ((reinterpret_cast<uintptr_t>(w) & 3) == 0) {
+    hipLaunchKernelGGL((gemv_q32_m1<TYPE, WAVES, STEPS, OutT, true>), grid, block, 0, stream, x, w, out, a.n);
+    return;
   }
   hipLaunchKernelGGL((gemv_q32_m1<TYPE, WAVES, STEPS, OutT>), grid, block, 0, stream, x, w, out, a.n);
+}
+
+// Q4_1, Q5_0 and Q5_1 at M = 1, K a multiple of 2048 up to 16384: gemv_q32_m1's plan (one row
+// per wave, one 32-element block per lane and STEPS = K / 2048 blocks per lane held in
+// registers, x staged in LDS behind an LDS-only barrier).  Element j < 16 of a block is the low
+// nibble of code byte j and element j + 16 its high nibble; Q5's fifth bit of element j is bit
+// j of qh, spread four at a time into bit 4 of each code byte by one multiply
+// (b * 0x00204081 moves bit k of b to bit 8k).  Codes widen to fp16 "1024 + q" (v_perm_b32) for
+// v_dot2_f32_f16; per block, with the sum sx of its 32 x values:
+//   Q4_1, Q5_1: d * (a - 1024 sx) + m * sx,   Q5_0: d * (a - 1040 sx)   (a: sum of (1024 + q) x).
+// Q5_0's 22-byte blocks start at 2 mod 4 in odd lanes, so its loads are made 4-byte aligned as
+// Q8_0's are: an even lane reads 24 bytes from the block's start (2 into the odd block after it)
+// and realigns qh and the codes by 2 bytes; an odd lane reads them from byte 2 as they are, and
+// its d from the dword 2 bytes before the block.
+// Block formats (public GGML layouts): Q4_1 fp16 d, fp16 m, 16 code bytes (20 B); Q5_0 fp16 d,
+// 4 bytes qh, 16 code bytes (22 B); Q5_1 fp16 d, fp16 m, qh, 16 code bytes (24 B).
+__device__ __forceinline__ uint32_t spread4(uint32_t b) { return (b * 0x00204081u) & 0x01010101u; }
+
+template <int TYPE, int WAVES, int STEPS, typename OutT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q5_m1(const _Float16* __restrict__ x, const uint8_t* __restrict__ w,
+                                                         OutT* __restrict__ out, int n_rows) {
+  constexpr int kBytes = TYPE == kQ4_1 ? 20 : TYPE == kQ5_0 ? 22 : 24;
+  constexpr bool HAS_H = TYPE != kQ4_1;
+  constexpr int T = WAVES * 64, K = 2048 * STEPS, BLOCKS = K / 32, CHUNKS = K / 8;
+  constexpr int XC = (CHUNKS + T - 1) / T;  // 16-byte x chunks per thread
+  __shared__ __attribute__((aligned(16))) uint8_t xl[CHUNKS * 20];  // 64 + 16 bytes per block
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  const uint8_t* const wr = w + (size_t)min(row, n_rows - 1) * (size_t)(BLOCKS * kBytes);
+  uint4 xr[XC];
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    if (CHUNKS % T == 0 || c < CHUNKS) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * c);
+  }
+  // Q5_0: six window dwords (16 + 4 bytes, and the sixth: the dword after them for an even
+  // lane, the one holding d for an odd lane); Q4_1 / Q5_1: the d, m dword, Q5_1's qh, the codes
+  uint4 qv[STEPS];
+  uint32_t w4[STEPS], w5[STEPS];
+  const bool odd = lane & 1;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const uint8_t* block = wr + (lane + 64 * s) * kBytes;
+    if constexpr (TYPE == kQ5_0) {
+      const uint8_t* win = block + (odd ? 2 : 0);
+      qv[s] = load16(win);
+      w4[s] = load4(win + 16);
+      w5[s] = load4(odd ? block - 2 : win + 20);
+    } else if constexpr (TYPE == kQ4_1) {
+      w5[s] = load4(block);  // d, m
+      qv[s] = load16(block + 4);
+    } else {
+      w5[s] = load4(block);      // d, m
+      w4[s] = load4(block + 4);  // qh
+      qv[s] = load16(block + 8);
+    }
+  }
+  asm volatile("" ::: "memory");  // every load above is issued before the x stores below
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = threadIdx.x + i * T;
+    if (CHUNKS % T == 0 || c < CHUNKS) *reinterpret_cast<uint4*>(xl + 16 * c + 16 * (c >> 2)) = xr[i];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  if (row >= n_rows) return;
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const uint4* xp = reinterpret_cast<const uint4*>(xl + 80 * (lane + 64 * s));
+    uint4 xs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xs[i] = xp[i];
+    const float sx = sum16(xs[0], xs[1]) + sum16(xs[2], xs[3]);
+    uint32_t q[4], qh = 0;
+    float d, m = 0.0f;
+    if constexpr (TYPE == kQ5_0) {
+      // even lane: window from byte 0, shift 2; odd lane: from byte 2, shift 0
+      const uint32_t sh = odd ? 0u : 2u;
+      const uint32_t wd[6] = {qv[s].x, qv[s].y, qv[s].z, qv[s].w, w4[s], w5[s]};
+      qh = __builtin_amdgcn_alignbyte(wd[1], wd[0], sh);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) q[u] = __builtin_amdgcn_alignbyte(wd[u + 2], wd[u + 1], sh);
+      d = half_bits_to_float(odd ? w5[s] >> 16 : wd[0]);
+    } else {
+      q[0] = qv[s].x; q[1] = qv[s].y; q[2] = qv[s].z; q[3] = qv[s].w;
+      if constexpr (TYPE == kQ5_1) qh = w4[s];
+      d = half_bits_to_float(w5[s]);
+      m = half_bits_to_float(w5[s] >> 16);
+    }
+    float a = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint32_t lo = q[u] & 0x0F0F0F0Fu, hi = (q[u] >> 4) & 0x0F0F0F0Fu;
+      if constexpr (HAS_H) {
+        lo |= spread4((qh >> (4 * u)) & 15u) << 4;
+        hi |= spread4((qh >> (16 + 4 * u)) & 15u) << 4;
+      }
+      // element 4u.. low nibbles; 16 + 4u.. high nibbles
+      a = dot2(magic01(lo), word(xs[u >> 1], 2 * (u & 1)), a);
+      a = dot2(magic23(lo), word(xs[u >> 1], 2 * (u & 1) + 1), a);
+      a = dot2(magic01(hi), word(xs[2 + (u >> 1)], 2 * (u & 1)), a);
+      a = dot2(magic23(hi), word(xs[2 + (u >> 1)], 2 * (u & 1) + 1), a);
+    }
+    if constexpr (TYPE == kQ5_0) acc = fmaf(d, a - 1040.0f * sx, acc);
+    else acc = fmaf(d, a - 1024.0f * sx, fmaf(m, sx, acc));
+  }
+  const float v = wave_sum(acc);
+  if (lane == 0) store_out<OutT>(out, (size_t)row, v);
+}
+
+template <int TYPE, int STEPS, typename OutT>
+static void launch_q5_m1_steps(const GemvArgs& a, hipStream_t stream) {
+  constexpr int WAVES = STEPS <= 2 ? 8 : 4;
+  hipLaunchKernelGGL((gemv_q5_m1<TYPE, WAVES, STEPS, OutT>), dim3((a.n + WAVES - 1) / WAVES), dim3(WAVES * 64), 0,
+                     stream, static_cast<const _Float16*>(a.x), static_cast<const uint8_t*>(a.w),
+                     static_cast<OutT*>(a.out), a.n);
+}
+
+// gemv_q5_m1 for Q4_1 / Q5_0 / Q5_1 at M = 1 and K = 2048 .. 16384 in steps of 2048 (Q5_0: w
+// 4-byte aligned, as any torch or hipMalloc buffer is); false for the other shapes.
+template <typename OutT>
+static bool launch_q5_m1(const GemvArgs& a, hipStream_t stream) {
+  if (a.m != 1 || a.k % 2048 || a.k > 16384 || a.n <= 0) return false;
+  if (a.type == kQ5_0 && (reinterpret_cast<uintptr_t>(a.w) & 3)) return false;
+  const int steps = a.k / 2048;
+#define TENSOR_GGUF_Q5_M1(T)                                          \
+  case T:                                                             \
+    switch (steps) {                                                  \
+      case 1: launch_q5_m1_steps<T, 1, OutT>(a, stream); return true; \
+      case 2: launch_q5_m1_steps<T, 2, OutT>(a, stream); return true; \
+      case 3: launch_q5_m1_steps<T, 3, OutT>(a, stream); return true; \
+      case 4: launch_q5_m1_steps<T, 4, OutT>(a, stream); return true; \
+      case 5: launch_q5_m1_steps<T, 5, OutT>(a, stream); return true; \
+      case 6: launch_q5_m1_steps<T, 6, OutT>(a, stream); return true; \
+      case 7: launch_q5_m1_steps<T, 7, OutT>(a, stream); return true; \
+      default: launch_q5_m1_steps<T, 8, OutT>(a, stream); return true; \
+    }
+  switch (a.type) {
+    TENSOR_GGUF_Q5_M1(kQ4_1)
+    TENSOR_GGUF_Q5_M1(kQ5_0)
+    TENSOR_GGUF_Q5_M1(kQ5_1)
+    default: return false;
+  }
+#undef TENSOR_GGUF_Q5_M1
 }
 
 // gemv_q32_m1 for K = 2048 .. 16384 in steps of 2048; false for the other shapes.
@@ -795,6 +945,9 @@ static hipError_t launch_m(const GemvArgs& a, hipStream_t stream) {
       else hipLaunchKernelGGL((gemv_q32<kQ4_0, M, R, OutT>), grid, block, 0, stream, x, w, out, a.n, a.k);
       break;
     default:
+      if constexpr (M == 1) {
+        if (launch_q5_m1<OutT>(a, stream)) break;
+      }
       if (!launch_blocks<M, OutT, false>(a, nullptr, stream)) return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -155,6 +155,29 @@ def test_gemv_q32_m1_every_row_length(hip_device, c_oracle, encoding):
             assert err <= (2e-4 if out_dtype == "float32" else TOLERANCE), (k, out_dtype, err)
 
 
+@pytest.mark.parametrize("encoding", ["q4_1", "q5_0", "q5_1"])
+@pytest.mark.parametrize("source", ["quantized", "random_bits"])
+def test_gemv_q5_m1_every_row_length_each_row_within_tolerance(hip_device, c_oracle, encoding, source):
+    """M = 1 Q4_1 / Q5_0 / Q5_1 rows of 2048 .. 16384 columns (one 32-element block per lane and
+    one to eight blocks per lane, 8- and 4-wave workgroups, a ragged last workgroup of 203 rows;
+    Q5_0's 22-byte blocks read through 4-byte-aligned windows), from quantized weights and from
+    random block bytes (every fifth-bit pattern).  Each row is checked."""
+    code = Q.ggml_type(encoding)
+    n = 203
+    for k in range(2048, 16384 + 1, 2048):
+        note("gemv-q5-m1", encoding, source, n, k)
+        raw = cases.weight(n, k, encoding, 51) if source == "quantized" else cases.random_blocks(encoding, n, k, 52)
+        x = cases.activation(1, k, 53)
+        expected = c_oracle.linear(x, raw, code, n, k)
+        scale = float(np.sqrt(np.mean(expected.astype(np.float64) ** 2)))
+        for out_dtype in ("float32", "float16"):
+            got = run_linear(hip_device, "gguf_gemv", encoding, x, raw, out_dtype)
+            assert not np.isnan(got).any(), (k, out_dtype)
+            assert R.relative_l2(got, expected) <= (2e-4 if out_dtype == "float32" else TOLERANCE), (k, out_dtype)
+            err = np.abs(got[0].astype(np.float32) - expected[0])
+            assert err.max() <= 2e-3 * scale + 1e-3 * np.abs(expected).max(), (k, out_dtype, int(err.argmax()))
+
+
 @pytest.mark.parametrize("encoding", ["q2_k", "q3_k"])
 @pytest.mark.parametrize("source", ["quantized", "random_bits"])
 def test_gemv_q23k_m1_every_row_length_each_row_within_tolerance(hip_device, c_oracle, encoding, source):

@@ -605,7 +605,7 @@ static void launch_q5_m1_steps(const GemvArgs& a, hipStream_t stream) {
 }
 
 // gemv_q5_m1 for Q4_1 / Q5_0 / Q5_1 at M = 1 and K = 2048 .. 16384 in steps of 2048 (Q5_0: w
-// 4-byte aligned, as any torch or hipMalloc buffer is); false for the other shapes.
+// 4-byte aligned, as the entry points' 16-byte buffer alignment ensures); false for the other shapes.
 template <typename OutT>
 static bool launch_q5_m1(const GemvArgs& a, hipStream_t stream) {
   if (a.m != 1 || a.k % 2048 || a.k > 16384 || a.n <= 0) return false;

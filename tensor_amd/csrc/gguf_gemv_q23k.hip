@@ -241,7 +241,7 @@ static hipError_t launch_q23k_typed(const GemvArgs& a, hipStream_t stream, bool*
 hipError_t launch_gemv_q23k_fast(const GemvArgs& a, hipStream_t stream, bool* handled) {
   *handled = false;
   if (a.m != 1 || a.n <= 0) return hipSuccess;
-  // Q3_K's windows assume 4-byte aligned weights (any torch or hipMalloc buffer is)
+  // Q3_K's windows assume 4-byte aligned weights (the entry points accept 16-byte aligned buffers only)
   if (a.type == kQ3_K && (reinterpret_cast<uintptr_t>(a.w) & 3) == 0)
     return a.out_half ? launch_q23k_typed<kQ3_K, _Float16>(a, stream, handled)
                       : launch_q23k_typed<kQ3_K, float>(a, stream, handled);

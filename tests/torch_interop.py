@@ -53,6 +53,27 @@ def check_linear(oracle, encoding, m, n, k, out_dtype, seed=60):
     return kernel, xt, wt, out
 
 
+def check_misaligned_weights():
+    """Weights at a 2-byte storage offset are refused before any launch.  The M = 1 kernels of
+    Q8_0, Q4_0, Q6_K, Q3_K and Q5_0 read their 2-mod-4 blocks through 4-byte-aligned windows,
+    which the entry points' 16-byte buffer alignment guarantees."""
+    for encoding in ("q8_0", "q6_k", "q3_k"):
+        step(f"misaligned weights {encoding}: refused")
+        raw, x = cases.weight(64, 4096, encoding, 80), cases.activation(1, 4096, 81)
+        kernel = tt.load("gguf_linear", encoding=encoding, out_dtype="float32")
+        xt = torch.from_numpy(x).cuda()
+        buf = torch.empty(raw.nbytes + 2, dtype=torch.uint8, device=xt.device)
+        shifted = buf[2:].view(raw.shape)
+        shifted.copy_(torch.from_numpy(raw).cuda())
+        assert shifted.data_ptr() % 4 == 2
+        try:
+            kernel(xt, shifted)
+        except ValueError as error:
+            assert "alignment" in str(error), error
+        else:
+            raise AssertionError(f"{encoding}: a 2-byte-aligned weight pointer was accepted")
+
+
 def expect(oracle, got, x, raw, code, n, k):
     expected = oracle.linear(x, raw, code, n, k, prefill=x.shape[0] > 8)
     error = R.relative_l2(got.float().cpu().numpy(), expected)
@@ -265,6 +286,7 @@ def main():
     check_raw_into_prepare(kernel, xt, wt, out)
     check_linear(oracle, "q4_k", 64, 1024, 4096, "float16")
     check_linear(oracle, "q6_k", 3, 1000, 2560, "float32")
+    check_misaligned_weights()
     check_compile(oracle)
     check_bundle()
     check_showcase_call(oracle)

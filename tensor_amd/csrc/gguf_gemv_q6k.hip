@@ -35,10 +35,17 @@ __device__ __forceinline__ uint32_t q6k_quad_mov(uint32_t v) {
 // 16 b + 8 hh + 4 p + c, so the runs c = 0..3 that one lane reads (fixed b, hh, p) are adjacent.
 __device__ __forceinline__ int run_slot(int r) { return (r & ~15) | (r & 8) | ((r & 1) << 2) | ((r >> 1) & 3); }
 
-template <int R, int STEPS, int WAVES, typename OutT, bool ALIGNED = false>
+//
+// KSPLIT (R = 1): the STEPS steps of a row go to STEPS waves of the workgroup, WAVES / STEPS rows
+// per workgroup, each wave one step (so three times the waves of a one-row-per-wave grid, and
+// the aligned one-step loads); the waves' totals meet in LDS and are added in step order.
+template <int R, int STEPS, int WAVES, typename OutT, bool ALIGNED = false, bool KSPLIT = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __restrict__ x,
                                                            const uint8_t* __restrict__ w,
                                                            OutT* __restrict__ out, int n_rows) {
+  static_assert(!KSPLIT || (R == 1 && WAVES % STEPS == 0), "one step per wave");
+  constexpr int LS = KSPLIT ? 1 : STEPS;            // steps per wave
+  constexpr int ROWS = KSPLIT ? WAVES / STEPS : 0;  // KSPLIT: rows per workgroup
   constexpr int K = STEPS * 4096;
   constexpr int ROW_BYTES = STEPS * 16 * 210;
   constexpr int T = WAVES * 64, XC = (K / 8 + T - 1) / T;  // 16-byte x chunks per thread
@@ -47,7 +54,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __res
   // them (see run_slot), staged with x so that no wave sums x itself
   __shared__ __attribute__((aligned(16))) float sxl[K / 16];
   const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * WAVES + (threadIdx.x >> 6)) * R;
+  const int wave = threadIdx.x >> 6;
+  const int row0 = KSPLIT ? blockIdx.x * ROWS + wave % (KSPLIT ? ROWS : 1) : (blockIdx.x * WAVES + wave) * R;
+  const int s0 = KSPLIT ? wave / (KSPLIT ? ROWS : 1) : 0;  // the wave's first step
   const int slot = lane >> 2, part = lane & 3, hh = part >> 1, l0 = 16 * (part & 1);
   // x first, then every weight load of the wave, pinned above a compiler barrier: on each CU
   // the small x load is not queued behind weight traffic, and the workgroup barrier below
@@ -58,17 +67,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __res
     const int c = threadIdx.x + i * T;
     if (c < K / 8) xr[i] = load16(reinterpret_cast<const uint8_t*>(x) + 16 * c);
   }
-  uint4 qa[R][STEPS], qb[R][STEPS], qh[R][STEPS];
-  uint2 sc8[R][STEPS];
-  uint32_t sc_next[R][STEPS];  // ALIGNED: the dword after the 8 scale bytes' window
-  uint32_t dw[R][STEPS];
+  uint4 qa[R][LS], qb[R][LS], qh[R][LS];
+  uint2 sc8[R][LS];
+  uint32_t sc_next[R][LS];  // ALIGNED: the dword after the 8 scale bytes' window
+  uint32_t dw[R][LS];
   const uint32_t sh = ALIGNED ? 2 * (slot & 1) : 0;  // block address mod 4
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const uint8_t* wr = w + (size_t)min(row0 + r, n_rows - 1) * ROW_BYTES + slot * 210;
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      const uint8_t* block = wr + s * 16 * 210;
+    for (int s = 0; s < LS; ++s) {
+      const uint8_t* block = wr + (s0 + s) * 16 * 210;
       if constexpr (ALIGNED) {
         // windows at block - sh: those of an odd slot start in the even block before it, and the
         // last ones of an even slot end 2 bytes into the odd block after it
@@ -104,20 +113,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __res
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-  if (row0 >= n_rows) return;
+  if (!KSPLIT && row0 >= n_rows) return;  // KSPLIT: every wave meets the second barrier
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
 #pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
+  for (int s = 0; s < LS; ++s) {
     // the four 16-element runs 128 hh + 32 c + l0 (c = 0..3), one scale group each; their
     // sums of x are four consecutive slots
     uint4 xs[4][2];
-    const float4 s4 = *reinterpret_cast<const float4*>(&sxl[(s * 16 + slot) * 16 + 8 * hh + 4 * (part & 1)]);
+    const int sb = (s0 + s) * 16 + slot;  // super-block index in the row
+    const float4 s4 = *reinterpret_cast<const float4*>(&sxl[sb * 16 + 8 * hh + 4 * (part & 1)]);
     const float sx[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int ch = ((s * 16 + slot) * 256 + 128 * hh + 32 * c + l0) >> 3;
+      const int ch = (sb * 256 + 128 * hh + 32 * c + l0) >> 3;
       xs[c][0] = *reinterpret_cast<const uint4*>(xlds + 16 * ch + 16 * (ch >> 3));
       xs[c][1] = *reinterpret_cast<const uint4*>(xlds + 16 * (ch + 1) + 16 * ((ch + 1) >> 3));
     }
@@ -173,10 +183,25 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q6k_lds(const _Float16* __res
       acc[r] = v;
     }
   }
+  if constexpr (KSPLIT) {
+    __shared__ float red[WAVES];  // wave totals, wave = step * ROWS + row in the workgroup
+    const float v = wave_sum(acc[0]);
+    if (lane == 0) red[wave] = v;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if (wave < ROWS && lane == 0 && row0 < n_rows) {
+      float total = red[wave];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const float v = wave_sum(acc[r]);
-    if (lane == 0 && row0 + r < n_rows) store_out<OutT>(out, (size_t)(row0 + r), v);
+      for (int s = 1; s < STEPS; ++s) total += red[s * ROWS + wave];
+      store_out<OutT>(out, (size_t)row0, total);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(acc[r]);
+      if (lane == 0 && row0 + r < n_rows) store_out<OutT>(out, (size_t)(row0 + r), v);
+    }
   }
 }
 
@@ -289,8 +314,11 @@ hipError_t launch_gemv_q6k_f32x(const GemvArgs& a, hipStream_t stream, bool* han
   return a.out_half ? launch_q6k_f32_typed<_Float16>(a, stream, handled) : launch_q6k_f32_typed<float>(a, stream, handled);
 }
 
-// The aligned loads at K = 4096 (one step); at three steps they measured slower (the form with a
-// second load per piece: 12.3 against 10.3 us at 4096 x 12288).
+// The aligned loads at K = 4096 (one step), and at K = 12288 in the K-split form (three waves
+// per row, four rows per 12-wave workgroup, one aligned step per wave): in a timing harness
+// 10.05 against 10.19 us at 4096 x 12288 and 4.58 against 5.75 us at 1001 x 12288, where one
+// row per wave leaves most of the GPU idle.  Aligned loads with all three steps in one wave
+// measured level or slower (10.24-12.3 against 10.19-10.3 us at 4096 x 12288).
 template <int R, int STEPS, int WAVES, typename OutT>
 static hipError_t launch_q6k(const GemvArgs& a, hipStream_t stream) {
   constexpr int per_block = WAVES * R;
@@ -301,6 +329,14 @@ static hipError_t launch_q6k(const GemvArgs& a, hipStream_t stream) {
   if constexpr (STEPS == 1) {
     if ((reinterpret_cast<uintptr_t>(w) & 3) == 0) {
       hipLaunchKernelGGL((gemv_q6k_lds<R, STEPS, WAVES, OutT, true>), grid, block, 0, stream, x, w, out, a.n);
+      return hipGetLastError();
+    }
+  }
+  if constexpr (STEPS == 3 && R == 1) {
+    if ((reinterpret_cast<uintptr_t>(w) & 3) == 0) {
+      constexpr int KS_WAVES = 12, KS_ROWS = KS_WAVES / STEPS;
+      hipLaunchKernelGGL((gemv_q6k_lds<1, STEPS, KS_WAVES, OutT, true, true>), dim3((a.n + KS_ROWS - 1) / KS_ROWS),
+                         dim3(KS_WAVES * 64), 0, stream, x, w, out, a.n);
       return hipGetLastError();
     }
   }
